@@ -1,0 +1,215 @@
+/*
+ * lsrm_hip.h -- C ABI of the MI355X (gfx950) variable-block native sparse
+ * attention library (liblsrm_hip.so).
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * (passed as void*), launches its kernels on that stream and returns a
+ * status code without synchronising the host.  No entry point allocates
+ * device memory: callers pass a workspace whose size the matching
+ * *_workspace_size() function reports.  All index tensors are int32 and all
+ * tensors are dense row-major (contiguous) in the layouts stated below.
+ *
+ * Reference interfaces replaced (paths relative to the LSRM repository):
+ *   lsrm_block_mean_pool      sparse/module/spatial_sparse_attention.py:27-37
+ *                             (SpatialSparseAttentionIn.sparse3d_compression,
+ *                              torch.segment_reduce(reduce="mean"))
+ *   lsrm_select_blocks        no reference function (the block-selection rule
+ *                             of the benchmark); nearest analogue
+ *                             sparse/ops/block_score.py:16-98
+ *   lsrm_sel_attn_validate    the asserts of
+ *                             sparse/ops/triton_native_sparse_attention_impl_kvcentric.py:1295-1301
+ *                             plus the metadata contract the kernels assume
+ *   lsrm_sel_attn_fwd         ..._impl_kvcentric.py:931-1010 (native_sparse_attn_forward)
+ *   lsrm_sel_attn_bwd         ..._impl_kvcentric.py:1018-1263 (native_sparse_attn_backward)
+ *   lsrm_reverse_query_map    ..._impl_kvcentric.py:575-684 (_build_reverse_query_mapping)
+ *   lsrm_block_ids            builds the self-block selection that turns the
+ *                             selected-attention kernels into
+ *                             sparse/ops/block_window_attention.py:14-31
+ *                             (sparse_window_attention)
+ */
+#ifndef LSRM_HIP_H
+#define LSRM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes. */
+enum lsrm_dtype {
+  LSRM_F32 = 0,
+  LSRM_F16 = 1,
+  LSRM_BF16 = 2
+};
+
+/* Status codes returned by every entry point. */
+enum lsrm_status {
+  LSRM_OK = 0,
+  LSRM_ERR_INVALID_ARG = 1, /* null pointer, negative size, bad combination */
+  LSRM_ERR_UNSUPPORTED = 2, /* dtype / head_dim / group size not built      */
+  LSRM_ERR_WORKSPACE = 3,   /* workspace smaller than *_workspace_size()    */
+  LSRM_ERR_LAUNCH = 4       /* a HIP launch or device query failed          */
+};
+
+/* Bits of the flag word written by lsrm_sel_attn_validate. */
+enum lsrm_meta_error {
+  LSRM_META_OFFSETS_NOT_MONOTONE = 1,  /* cu_block_include_tokens decreases  */
+  LSRM_META_BLOCK_OUT_OF_RANGE = 2,    /* a block's tokens outside [0, n_k)  */
+  LSRM_META_SEQBLOCKS_BAD = 4,         /* cu_seqblocks not monotone / > n_blocks */
+  LSRM_META_SEQLENS_BAD = 8,           /* cu_seqlens_q/k not monotone / too big */
+  LSRM_META_TOPK_NOT_PREFIX = 16,      /* a valid index after an invalid one  */
+  LSRM_META_TOPK_EMPTY_ROW = 32,       /* a query row selects no block        */
+  LSRM_META_BLOCK_OUTSIDE_SEQ = 64     /* a batch's blocks leave its k range  */
+};
+
+const char* lsrm_status_string(int status);
+int lsrm_version(void);
+
+/* ------------------------------------------------------------------------
+ * Block mean pooling (key/value block compression).
+ *   x               [n_tokens, channels] of x_dtype
+ *   cu_block_tokens [n_blocks + 1] int32, block b = rows [cu[b], cu[b+1])
+ *   out             [n_blocks, channels] of out_dtype
+ * Arithmetic contract (bit-exact, shared with the CPU oracle): rows are cut
+ * into pieces at every multiple of 64 of the global row index and at block
+ * boundaries; each piece is summed in fp32 in row order starting from +0.0;
+ * a block's piece sums are added in order starting from +0.0; the mean is the
+ * IEEE fp32 quotient sum / length, rounded to out_dtype to nearest-even.  An
+ * empty block yields NaN (0/0), as torch.segment_reduce(mean) does.
+ * Replaces: sparse/module/spatial_sparse_attention.py:27-37.
+ * ---------------------------------------------------------------------- */
+size_t lsrm_block_mean_pool_workspace_size(int64_t n_tokens, int64_t channels,
+                                           int64_t n_blocks);
+int lsrm_block_mean_pool(const void* x, int x_dtype, int64_t n_tokens,
+                         int64_t channels, const int32_t* cu_block_tokens,
+                         int64_t n_blocks, void* out, int out_dtype,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Per-query-block top-k block selection (self attention: queries and keys
+ * share tokens and the block partition).
+ *   q [n_tokens, hq, head_dim], k [n_tokens, hkv, head_dim] of dtype
+ *   cu_seqblocks [batch + 1], cu_block_tokens [n_blocks + 1]
+ *   forced_blocks [n_forced] batch-local block ids always selected (may be
+ *   NULL when n_forced == 0); force_self != 0 also forces the query's block.
+ * Rule: pooled means (fp32, lsrm_block_mean_pool contract) of Q and K per
+ * block; score(b, c) = sum over the hq/hkv query heads g of kv head h, then
+ * over d, of (double)pq[b,g,d] * (double)pk[c,h,d], accumulated in fp64 in
+ * that order; candidates are the blocks of the query block's batch element;
+ * forced blocks first (self, then forced_blocks in order, duplicates and
+ * out-of-range ids dropped, truncated to topk), remaining slots by (score
+ * descending, block id ascending).  Output rows list the selected
+ * batch-local ids ascending, padded with -1.
+ *   topk_idx     [hkv, n_tokens, topk] int32 (every token of a block gets the
+ *                block's row; the layout spatial_selection_attention reads)
+ *   topk_compact [hkv, n_blocks, topk] int32 (one row per query block)
+ * No reference function; nearest analogue sparse/ops/block_score.py:16-98.
+ * ---------------------------------------------------------------------- */
+size_t lsrm_select_blocks_workspace_size(int64_t n_tokens, int64_t n_blocks,
+                                         int64_t hq, int64_t hkv,
+                                         int64_t head_dim);
+int lsrm_select_blocks(const void* q, const void* k, int dtype,
+                       int64_t n_tokens, int64_t hq, int64_t hkv,
+                       int64_t head_dim, const int32_t* cu_seqblocks,
+                       int64_t batch, const int32_t* cu_block_tokens,
+                       int64_t n_blocks, int64_t topk,
+                       const int32_t* forced_blocks, int64_t n_forced,
+                       int force_self, int32_t* topk_idx,
+                       int32_t* topk_compact, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Metadata validation for the selected-attention entry points.  Writes the
+ * OR of lsrm_meta_error bits into *flags (device int32, overwritten).
+ * Replaces the host asserts of ..._impl_kvcentric.py:1295-1301 and checks
+ * the contract the reference leaves unchecked.
+ * ---------------------------------------------------------------------- */
+int lsrm_sel_attn_validate(const int32_t* topk_idx, int64_t hkv, int64_t n_q,
+                           int64_t topk, const int32_t* cu_seqblocks,
+                           const int32_t* cu_block_tokens, int64_t n_blocks,
+                           const int32_t* cu_seqlens_q,
+                           const int32_t* cu_seqlens_k, int64_t batch,
+                           int64_t n_k, int32_t* flags, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Selected-block attention, forward.
+ *   q [n_q, hq, head_dim], k/v [n_k, hkv, head_dim] of dtype (F16 or BF16)
+ *   topk_idx [hkv, n_q, topk] int32 batch-local block ids; an entry is valid
+ *   when 0 <= id < blocks of the query's batch element; every valid entry is
+ *   used, in list order (a repeated block counts twice).
+ *   out [n_q, hq, head_dim] dtype; lse [hq, n_q] fp32 in log2 units
+ *   (lse = log2 sum exp2(scale*log2(e)*q.k)).  A row with no valid entry
+ *   gives out = 0 and lse = -inf.
+ * head_dim in {32, 64, 128}; hq % hkv == 0 and hq / hkv <= 64.
+ * Replaces: ..._impl_kvcentric.py:931-1010 (forward_kernel_varblock 55-247).
+ * ---------------------------------------------------------------------- */
+size_t lsrm_sel_attn_workspace_size(int64_t n_q, int64_t n_k, int64_t hq,
+                                    int64_t hkv, int64_t topk,
+                                    int64_t n_blocks, int backward);
+int lsrm_sel_attn_fwd(const void* q, const void* k, const void* v, int dtype,
+                      int64_t n_q, int64_t n_k, int64_t hq, int64_t hkv,
+                      int64_t head_dim, const int32_t* topk_idx, int64_t topk,
+                      const int32_t* cu_seqblocks,
+                      const int32_t* cu_block_tokens, int64_t n_blocks,
+                      const int32_t* cu_seqlens_q, int64_t batch,
+                      float softmax_scale, void* out, float* lse,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Selected-block attention, backward.  Inputs as for the forward plus
+ * dout [n_q, hq, head_dim] and the forward's out and lse.  Writes
+ * dq [n_q, hq, head_dim], dk/dv [n_k, hkv, head_dim] (dtype) and
+ * delta [hq, n_q] fp32 (rowsum(out * dout)).  dK/dV are accumulated per
+ * 64-key tile by a single writer in a fixed order (deterministic, no float
+ * atomics).  Keys no query selects get zero gradient.
+ * Replaces: ..._impl_kvcentric.py:1018-1263 (backward_kernel_dq 262-478,
+ * _build_reverse_query_mapping 575-684, backward_kernel_dkdv_fastest 687-923).
+ * ---------------------------------------------------------------------- */
+int lsrm_sel_attn_bwd(const void* dout, const void* q, const void* k,
+                      const void* v, const void* out, const float* lse,
+                      int dtype, int64_t n_q, int64_t n_k, int64_t hq,
+                      int64_t hkv, int64_t head_dim, const int32_t* topk_idx,
+                      int64_t topk, const int32_t* cu_seqblocks,
+                      const int32_t* cu_block_tokens, int64_t n_blocks,
+                      const int32_t* cu_seqlens_q, int64_t batch,
+                      float softmax_scale, void* dq, void* dk, void* dv,
+                      float* delta, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* ------------------------------------------------------------------------
+ * Reverse (CSR) query map of a top-k selection: for each kv head h and
+ * global block c, the ascending list of query ids that selected c (a query
+ * selecting c twice appears twice).
+ *   cu_reverse_count      [hkv, n_blocks + 1] int32 exclusive prefix
+ *   reverse_query_indices [hkv, capacity] int32; capacity >= the largest
+ *                         per-head entry count (n_q * topk always suffices)
+ *   totals                [hkv] int32 entry count per head
+ * Replaces: ..._impl_kvcentric.py:575-684 (_build_reverse_query_mapping).
+ * ---------------------------------------------------------------------- */
+size_t lsrm_reverse_query_map_workspace_size(int64_t n_q, int64_t hkv,
+                                             int64_t topk, int64_t n_blocks);
+int lsrm_reverse_query_map(const int32_t* topk_idx, int64_t hkv, int64_t n_q,
+                           int64_t topk, const int32_t* cu_seqlens_q,
+                           const int32_t* cu_seqblocks, int64_t batch,
+                           int64_t n_blocks, int32_t* cu_reverse_count,
+                           int32_t* reverse_query_indices, int64_t capacity,
+                           int32_t* totals, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Batch-local block id of every token: ids[hkv, n_tokens, 1] with
+ * ids[h, t, 0] = b - cu_seqblocks[batch of b] for cu[b] <= t < cu[b+1].
+ * Feeding it to lsrm_sel_attn_fwd/bwd gives block-diagonal ("window")
+ * attention, the semantics of sparse/ops/block_window_attention.py:14-31.
+ * ---------------------------------------------------------------------- */
+int lsrm_block_ids(const int32_t* cu_seqblocks, int64_t batch,
+                   const int32_t* cu_block_tokens, int64_t n_blocks,
+                   int64_t n_tokens, int64_t hkv, int32_t* ids, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LSRM_HIP_H */

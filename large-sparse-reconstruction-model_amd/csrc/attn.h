@@ -1,0 +1,171 @@
+// Pieces shared by the selected-attention forward and backward kernels.
+//
+// A query tile is a run of queries of one kv head whose top-k rows are
+// identical (tiles come from the device-side plan).  Its rows are
+// (query, query head) pairs: row r <-> query q0 + r / g, head h * g + r % g,
+// 128 rows per tile, 32 rows per wave.  The tile attends to the key stream
+// formed by concatenating the token ranges of its valid selected blocks in
+// list order; the stream is processed in 64-key LDS tiles, so only the very
+// last key tile of a query tile is partial.
+#pragma once
+
+#include "common.h"
+#include "plan.h"
+
+namespace lsrm {
+
+constexpr int KT = 64;       // keys per LDS tile
+constexpr int ROWS = 128;    // rows per query tile (4 waves x 32)
+constexpr int MAXSEL = 256;  // top-k entries per row supported
+
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;    // forward output (backward only)
+  const uint16_t* dout; // backward only
+  const float* lse_in;  // backward only
+  uint16_t* out;        // forward: O; backward dq kernel: dQ
+  float* lse;           // forward: LSE; backward: delta
+  uint16_t* dk;
+  uint16_t* dv;
+  const int32_t* topk;
+  const int32_t* cu_sb;
+  const int32_t* cu_blk;
+  const int32_t* cu_q;
+  int64_t nb, batch, nq, nk;
+  int topk_n, hq, hkv, g;
+  float scale;       // softmax scale
+  float scale_log2;  // softmax scale * log2(e)
+  TilePlan plan;
+  RevMap rev;        // backward: tile-granular reverse map
+  KeyItems items;    // backward: 64-key chunks of every block
+};
+
+// Valid selected blocks of one selection row, compacted, with the prefix of
+// their lengths (the key stream).
+struct SelLds {
+  int tok[MAXSEL];
+  int cum[MAXSEL + 1];
+  int len_tmp[MAXSEL];
+  int tok_tmp[MAXSEL];
+  int n;
+};
+
+// All 256 threads: reads row `q` of kv head h and fills s.  Entries that are
+// invalid or name an empty block are dropped; list order is kept.
+__device__ inline void load_selection(const AttnArgs& a, int h, int64_t q,
+                                      SelLds& s) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  int b, bs, nbb;
+  bool st;
+  query_batch(a.cu_q, a.batch, a.cu_sb, q, &b, &bs, &nbb, &st);
+  const int32_t* row = a.topk + ((int64_t)h * a.nq + q) * a.topk_n;
+  for (int j = tid; j < a.topk_n; j += blockDim.x) {
+    const int v = row[j];
+    int len = 0, t0 = 0;
+    if (v >= 0 && v < nbb && (int64_t)bs + v < a.nb) {
+      int64_t s0 = a.cu_blk[bs + v], s1 = a.cu_blk[bs + v + 1];
+      s0 = s0 < 0 ? 0 : (s0 > a.nk ? a.nk : s0);
+      s1 = s1 < s0 ? s0 : (s1 > a.nk ? a.nk : s1);
+      t0 = (int)s0;
+      len = (int)(s1 - s0);
+    }
+    s.len_tmp[j] = len;
+    s.tok_tmp[j] = t0;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    int cn = 0, cc = 0;
+    for (int base = 0; base < a.topk_n; base += 64) {
+      const int j = base + lane;
+      int len = 0, t0 = 0;
+      if (j < a.topk_n) {
+        len = s.len_tmp[j];
+        t0 = s.tok_tmp[j];
+      }
+      const bool keep = len > 0;
+      const unsigned long long m = __ballot(keep);
+      const int pos = cn + __popcll(m & ((1ull << lane) - 1ull));
+      int x = len;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+      }
+      if (keep) {
+        s.tok[pos] = t0;
+        s.cum[pos + 1] = cc + x;
+      }
+      cn += __popcll(m);
+      cc += __shfl(x, 63);
+    }
+    if (lane == 0) {
+      s.cum[0] = 0;
+      s.n = cn;
+    }
+  }
+  __syncthreads();
+}
+
+// Token of stream position p (< total keys); `cur` is a monotone cursor.
+__device__ inline int stream_token(const SelLds& s, int p, int& cur) {
+  while (cur + 1 < s.n && s.cum[cur + 1] <= p) ++cur;
+  return s.tok[cur] + (p - s.cum[cur]);
+}
+
+// Copies n_words 32-bit words (n_words in {2, 4, 8}) from global memory.
+template <int NW>
+__device__ inline void gload(uint32_t* dst, const uint16_t* src) {
+  if constexpr (NW == 2) {
+    const u32x2 w = *reinterpret_cast<const u32x2*>(src);
+    dst[0] = w[0];
+    dst[1] = w[1];
+  } else {
+#pragma unroll
+    for (int i = 0; i < NW / 4; ++i) {
+      const u32x4 w = reinterpret_cast<const u32x4*>(src)[i];
+      dst[4 * i] = w[0];
+      dst[4 * i + 1] = w[1];
+      dst[4 * i + 2] = w[2];
+      dst[4 * i + 3] = w[3];
+    }
+  }
+}
+
+template <int NW>
+__device__ inline void sstore(uint16_t* dst, const uint32_t* src) {
+  if constexpr (NW == 2) {
+    *reinterpret_cast<u32x2*>(dst) = u32x2{src[0], src[1]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < NW / 4; ++i)
+      reinterpret_cast<u32x4*>(dst)[i] =
+          u32x4{src[4 * i], src[4 * i + 1], src[4 * i + 2], src[4 * i + 3]};
+  }
+}
+
+// 16-bit element i of a packed word array.
+__device__ inline uint32_t half_of(const uint32_t* w, int i) {
+  return (w[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
+}
+
+// Fetches the next work item with one atomic; returns the item index (or a
+// value >= total when the queue is drained), broadcast through LDS.
+__device__ inline int fetch_work(int32_t* counter, int* s_slot) {
+  if (threadIdx.x == 0) *s_slot = atomicAdd(counter, 1);
+  __syncthreads();
+  return *s_slot;
+}
+
+// Kv head owning global tile index w (head_off ascending, hkv small).
+__device__ inline int head_of(const int32_t* head_off, int hkv, int w) {
+  int h = 0;
+  while (h + 1 < hkv && head_off[h + 1] <= w) ++h;
+  return h;
+}
+
+// Persistent-grid size for a kernel: CUs x resident workgroups per CU.
+int persistent_grid(const void* kernel, int block, size_t dyn_lds);
+
+}  // namespace lsrm

@@ -1,0 +1,241 @@
+// C entry points of the selected-attention forward/backward, status strings
+// and device queries shared by the launchers.
+#include <mutex>
+
+#include "attn.h"
+
+namespace lsrm {
+
+int launch_fwd(int dtype, int d, const AttnArgs& a, hipStream_t st);
+int launch_bwd(int dtype, int d, const AttnArgs& a, hipStream_t st);
+
+int device_cu_count() {
+  static std::mutex mu;
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cache[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+        hipSuccess)
+      return 0;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+int persistent_grid(const void* kernel, int block, size_t dyn_lds) {
+  static std::mutex mu;
+  struct Entry {
+    const void* fn;
+    int dev;
+    int per_cu;
+  };
+  static Entry cache[128];
+  static int n_cache = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  const int cus = device_cu_count();
+  if (cus <= 0) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n_cache; ++i)
+    if (cache[i].fn == kernel && cache[i].dev == dev)
+      return cus * cache[i].per_cu;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block,
+                                                   dyn_lds) != hipSuccess ||
+      per_cu <= 0)
+    per_cu = 1;
+  if (n_cache < 128) cache[n_cache++] = Entry{kernel, dev, per_cu};
+  return cus * per_cu;
+}
+
+struct AttnWs {
+  TilePlan plan;
+  RevMap rev;
+  KeyItems items;
+};
+
+// Carves (or sizes, when ws.base is null) the attention workspace and builds
+// the plan on the stream.
+int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
+              int64_t hkv, int64_t topk_n, const int32_t* cu_sb,
+              const int32_t* cu_blk, int64_t nb, const int32_t* cu_q,
+              int64_t batch, int g, bool backward, AttnWs& w, hipStream_t st) {
+  const int tq = ROWS / g;
+  int rc = build_tile_plan(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, tq, ws,
+                           w.plan, st);
+  if (rc) return rc;
+  if (backward) {
+    w.rev = RevMap{};
+    w.rev.cap = nq * topk_n;
+    rc = build_reverse_map(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, nb, true,
+                           &w.plan, ws, w.rev, st);
+    if (rc) return rc;
+    rc = build_key_items(cu_blk, nb, nk, ws, w.items, st);
+    if (rc) return rc;
+  }
+  return LSRM_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_attn_args(int dtype, int64_t n_q, int64_t n_k, int64_t hq,
+                    int64_t hkv, int64_t head_dim, int64_t topk,
+                    int64_t n_blocks, int64_t batch) {
+  if (n_q < 0 || n_k < 0 || hq <= 0 || hkv <= 0 || topk <= 0 || n_blocks < 0 ||
+      batch <= 0)
+    return LSRM_ERR_INVALID_ARG;
+  if (hq % hkv != 0) return LSRM_ERR_INVALID_ARG;
+  if (dtype != LSRM_BF16 && dtype != LSRM_F16) return LSRM_ERR_UNSUPPORTED;
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return LSRM_ERR_UNSUPPORTED;
+  if (hq / hkv > 64 || topk > MAXSEL) return LSRM_ERR_UNSUPPORTED;
+  if (n_q > INT32_MAX / (topk > 0 ? topk : 1) || n_k > INT32_MAX)
+    return LSRM_ERR_UNSUPPORTED;
+  return LSRM_OK;
+}
+
+}  // namespace lsrm
+
+using namespace lsrm;
+
+extern "C" const char* lsrm_status_string(int status) {
+  switch (status) {
+    case LSRM_OK: return "ok";
+    case LSRM_ERR_INVALID_ARG: return "invalid argument";
+    case LSRM_ERR_UNSUPPORTED: return "unsupported dtype, head_dim, group size or size";
+    case LSRM_ERR_WORKSPACE: return "workspace too small";
+    case LSRM_ERR_LAUNCH: return "HIP launch or device query failed";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int lsrm_version(void) { return 100; }
+
+extern "C" size_t lsrm_sel_attn_workspace_size(int64_t n_q, int64_t n_k,
+                                               int64_t hq, int64_t hkv,
+                                               int64_t topk, int64_t n_blocks,
+                                               int backward) {
+  if (n_q < 0 || n_k < 0 || hq <= 0 || hkv <= 0 || topk <= 0 || n_blocks < 0 ||
+      hq % hkv != 0)
+    return 0;
+  Carver ws{nullptr, 0, 0};
+  AttnWs w{};
+  attn_plan(ws, nullptr, n_q, n_k, hkv, topk, nullptr, nullptr, n_blocks,
+            nullptr, 1, (int)(hq / hkv), backward != 0, w, nullptr);
+  return ws.used + 256;
+}
+
+extern "C" int lsrm_sel_attn_fwd(
+    const void* q, const void* k, const void* v, int dtype, int64_t n_q,
+    int64_t n_k, int64_t hq, int64_t hkv, int64_t head_dim,
+    const int32_t* topk_idx, int64_t topk, const int32_t* cu_seqblocks,
+    const int32_t* cu_block_tokens, int64_t n_blocks,
+    const int32_t* cu_seqlens_q, int64_t batch, float softmax_scale, void* out,
+    float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk, n_blocks,
+                           batch);
+  if (rc) return rc;
+  if (n_q == 0) return LSRM_OK;
+  if (!q || !k || !v || !out || !lse || !topk_idx || !cu_seqblocks ||
+      !cu_block_tokens || !cu_seqlens_q || !aligned16(q) || !aligned16(k) ||
+      !aligned16(v) || !aligned16(out) || !(softmax_scale > 0.0f))
+    return LSRM_ERR_INVALID_ARG;
+  const size_t need =
+      lsrm_sel_attn_workspace_size(n_q, n_k, hq, hkv, topk, n_blocks, 0);
+  if (workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  Carver ws{reinterpret_cast<char*>(align_up((size_t)workspace, 256)), 0,
+            workspace_bytes - 256};
+  const int g = (int)(hq / hkv);
+  AttnWs w{};
+  rc = attn_plan(ws, topk_idx, n_q, n_k, hkv, topk, cu_seqblocks,
+                 cu_block_tokens, n_blocks, cu_seqlens_q, batch, g, false, w,
+                 st);
+  if (rc) return rc;
+  AttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.out = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  a.topk = topk_idx;
+  a.cu_sb = cu_seqblocks;
+  a.cu_blk = cu_block_tokens;
+  a.cu_q = cu_seqlens_q;
+  a.nb = n_blocks;
+  a.batch = batch;
+  a.nq = n_q;
+  a.nk = n_k;
+  a.topk_n = (int)topk;
+  a.hq = (int)hq;
+  a.hkv = (int)hkv;
+  a.g = g;
+  a.scale = softmax_scale;
+  a.scale_log2 = softmax_scale * 1.44269504f;  // as the reference (kvcentric:125)
+  a.plan = w.plan;
+  return launch_fwd(dtype, (int)head_dim, a, st);
+}
+
+extern "C" int lsrm_sel_attn_bwd(
+    const void* dout, const void* q, const void* k, const void* v,
+    const void* out, const float* lse, int dtype, int64_t n_q, int64_t n_k,
+    int64_t hq, int64_t hkv, int64_t head_dim, const int32_t* topk_idx,
+    int64_t topk, const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
+    int64_t n_blocks, const int32_t* cu_seqlens_q, int64_t batch,
+    float softmax_scale, void* dq, void* dk, void* dv, float* delta,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk, n_blocks,
+                           batch);
+  if (rc) return rc;
+  if (n_q == 0) return LSRM_OK;
+  if (!dout || !q || !k || !v || !out || !lse || !dq || !dk || !dv || !delta ||
+      !topk_idx || !cu_seqblocks || !cu_block_tokens || !cu_seqlens_q ||
+      !aligned16(dout) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
+      !aligned16(out) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
+      !(softmax_scale > 0.0f))
+    return LSRM_ERR_INVALID_ARG;
+  const size_t need =
+      lsrm_sel_attn_workspace_size(n_q, n_k, hq, hkv, topk, n_blocks, 1);
+  if (workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  Carver ws{reinterpret_cast<char*>(align_up((size_t)workspace, 256)), 0,
+            workspace_bytes - 256};
+  const int g = (int)(hq / hkv);
+  AttnWs w{};
+  rc = attn_plan(ws, topk_idx, n_q, n_k, hkv, topk, cu_seqblocks,
+                 cu_block_tokens, n_blocks, cu_seqlens_q, batch, g, true, w,
+                 st);
+  if (rc) return rc;
+  AttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.o = static_cast<const uint16_t*>(out);
+  a.dout = static_cast<const uint16_t*>(dout);
+  a.lse_in = lse;
+  a.out = static_cast<uint16_t*>(dq);
+  a.lse = delta;
+  a.dk = static_cast<uint16_t*>(dk);
+  a.dv = static_cast<uint16_t*>(dv);
+  a.topk = topk_idx;
+  a.cu_sb = cu_seqblocks;
+  a.cu_blk = cu_block_tokens;
+  a.cu_q = cu_seqlens_q;
+  a.nb = n_blocks;
+  a.batch = batch;
+  a.nq = n_q;
+  a.nk = n_k;
+  a.topk_n = (int)topk;
+  a.hq = (int)hq;
+  a.hkv = (int)hkv;
+  a.g = g;
+  a.scale = softmax_scale;
+  a.scale_log2 = softmax_scale * 1.44269504f;  // as the reference (kvcentric:125)
+  a.plan = w.plan;
+  a.rev = w.rev;
+  a.items = w.items;
+  return launch_bwd(dtype, (int)head_dim, a, st);
+}

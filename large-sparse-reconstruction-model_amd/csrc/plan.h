@@ -1,0 +1,80 @@
+// Device-side planning shared by the selected-attention kernels: query tiles
+// (runs of identical top-k rows cut into pieces of at most TQ queries) and
+// reverse (CSR) maps from blocks to the rows that selected them.
+#pragma once
+
+#include "common.h"
+
+namespace lsrm {
+
+// Queries of one kv head that share a selection row: [q0, q0 + qn).
+struct TilePlan {
+  int2* tiles;          // [hkv, n_q]; tile t of head h at tiles[h * n_q + t]
+  int32_t* tile_count;  // [hkv]
+  int32_t* head_off;    // [hkv + 1] exclusive prefix of tile_count
+  int32_t* counter;     // persistent-kernel work counter, zeroed by the plan
+};
+
+// CSR map block -> rows (tiles or queries) that selected it, per kv head.
+struct RevMap {
+  int32_t* cu_rev;  // [hkv, n_blocks + 1]
+  int32_t* rev;     // [hkv, cap]
+  int32_t* totals;  // [hkv]
+  int64_t cap;
+};
+
+// Workspace carving: pass a Carver with base == nullptr to size.
+int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
+                    int64_t topk_n, const int32_t* cu_q, int64_t batch,
+                    const int32_t* cu_sb, int tq, Carver& ws, TilePlan& plan,
+                    hipStream_t st);
+
+// rows_are_tiles: rows are the tiles of `plan` (row r of head h reads the
+// selection of query tiles[h*nq + r].x); otherwise rows are queries.
+int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
+                      int64_t topk_n, const int32_t* cu_q, int64_t batch,
+                      const int32_t* cu_sb, int64_t nb, bool rows_are_tiles,
+                      const TilePlan* plan, Carver& ws, RevMap& map,
+                      hipStream_t st);
+
+// Key chunks of at most 64 tokens inside each block (head independent):
+// item i = (block, first token, length) packed in an int4 {c, t0, len, 0}.
+struct KeyItems {
+  int4* items;        // [n_blocks + n_k / 64 + 1]
+  int32_t* n_items;   // device scalar
+};
+int build_key_items(const int32_t* cu_blk, int64_t nb, int64_t nk, Carver& ws,
+                    KeyItems& ki, hipStream_t st);
+
+int launch_zero_i32(int32_t* p, int64_t n, hipStream_t st);
+
+// Batch element owning query i (cu_q ascending), clamped to [0, batch).
+__device__ inline int batch_of(const int32_t* cu_q, int64_t batch, int64_t i) {
+  int64_t b = upper_index(cu_q, 0, batch + 1, i);
+  if (b < 0) b = 0;
+  if (b >= batch) b = batch - 1;
+  return (int)b;
+}
+
+// Query i's batch element and its block range; nbb = 0 when i lies outside
+// every sequence.
+__device__ inline void query_batch(const int32_t* cu_q, int64_t batch,
+                                   const int32_t* cu_sb, int64_t i, int* b_out,
+                                   int* bs_out, int* nbb_out,
+                                   bool* seq_start) {
+  if (batch <= 0 || i < cu_q[0] || i >= cu_q[batch]) {
+    *b_out = -1;
+    *bs_out = 0;
+    *nbb_out = 0;
+    *seq_start = true;
+    return;
+  }
+  const int b = batch_of(cu_q, batch, i);
+  *b_out = b;
+  *bs_out = cu_sb[b];
+  const int nbb = cu_sb[b + 1] - cu_sb[b];
+  *nbb_out = nbb > 0 ? nbb : 0;
+  *seq_start = (i == cu_q[b]);
+}
+
+}  // namespace lsrm

@@ -1,0 +1,693 @@
+// Planning kernels: batched exclusive scans, query-tile plans, reverse (CSR)
+// maps with a deterministic per-segment sort, key-chunk items, metadata
+// validation and per-token block ids.
+//
+// The reverse map replaces the reference's _count_queries_kernel /
+// _scatter_queries_kernel / host-looped segmented sort
+// (sparse/ops/triton_native_sparse_attention_impl_kvcentric.py:494-684) with
+// count -> scan -> atomic scatter -> per-segment sort, all on the device and
+// without host synchronisation.
+#include "plan.h"
+
+namespace lsrm {
+
+constexpr int SCAN_T = 256;
+constexpr int SCAN_PER = 16;
+constexpr int SCAN_CHUNK = SCAN_T * SCAN_PER;
+
+__device__ inline int wave_sum(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Exclusive scan of one value per thread over a 256-thread block; returns the
+// exclusive prefix and writes the block total to *total.
+__device__ inline int block_excl_scan(int v, int* total) {
+  __shared__ int s_w[SCAN_T / 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) s_w[w] = x;
+  __syncthreads();
+  int off = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < SCAN_T / 64; ++i) {
+    if (i < w) off += s_w[i];
+    tot += s_w[i];
+  }
+  __syncthreads();
+  *total = tot;
+  return off + x - v;
+}
+
+template <class F>
+__global__ __launch_bounds__(SCAN_T) void scan_reduce(F f, int64_t n,
+                                                      int32_t* sums,
+                                                      int nchunks) {
+  const int seg = blockIdx.y;
+  const int64_t base = (int64_t)blockIdx.x * SCAN_CHUNK + threadIdx.x * SCAN_PER;
+  const int64_t lim = f.limit(seg, n);
+  int s = 0;
+  for (int i = 0; i < SCAN_PER; ++i) {
+    const int64_t idx = base + i;
+    if (idx < lim) s += f(seg, idx);
+  }
+  int tot;
+  block_excl_scan(s, &tot);
+  if (threadIdx.x == 0) sums[(int64_t)seg * nchunks + blockIdx.x] = tot;
+}
+
+// In-place exclusive scan of each segment's chunk sums; totals[seg] = total.
+__global__ __launch_bounds__(SCAN_T) void scan_chunks(int32_t* sums,
+                                                      int nchunks,
+                                                      int32_t* totals) {
+  const int seg = blockIdx.x;
+  int32_t* p = sums + (int64_t)seg * nchunks;
+  int carry = 0;
+  for (int base = 0; base < nchunks; base += SCAN_T) {
+    const int i = base + threadIdx.x;
+    const int v = i < nchunks ? p[i] : 0;
+    int tot;
+    const int ex = block_excl_scan(v, &tot);
+    if (i < nchunks) p[i] = carry + ex;
+    carry += tot;
+  }
+  if (threadIdx.x == 0) totals[seg] = carry;
+}
+
+template <class F, class W>
+__global__ __launch_bounds__(SCAN_T) void scan_apply(F f, W w, int64_t n,
+                                                     const int32_t* sums,
+                                                     int nchunks) {
+  const int seg = blockIdx.y;
+  const int64_t base = (int64_t)blockIdx.x * SCAN_CHUNK + threadIdx.x * SCAN_PER;
+  const int64_t lim = f.limit(seg, n);
+  int v[SCAN_PER];
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < SCAN_PER; ++i) {
+    const int64_t idx = base + i;
+    v[i] = idx < lim ? f(seg, idx) : 0;
+    s += v[i];
+  }
+  int tot;
+  int ex = block_excl_scan(s, &tot) + sums[(int64_t)seg * nchunks + blockIdx.x];
+#pragma unroll
+  for (int i = 0; i < SCAN_PER; ++i) {
+    const int64_t idx = base + i;
+    if (idx < lim) w(seg, idx, ex, v[i], lim);
+    ex += v[i];
+  }
+}
+
+// Runs scan_reduce / scan_chunks / scan_apply over `nseg` segments of at
+// most n elements; totals[seg] receives each segment's sum.
+template <class F, class W>
+int run_scan(F f, W w, int64_t n, int nseg, int32_t* chunk_sums,
+             int32_t* totals, hipStream_t st) {
+  if (n <= 0 || nseg <= 0) return LSRM_OK;
+  const int nchunks = ceil_div(n, SCAN_CHUNK);
+  dim3 grid(nchunks, nseg);
+  hipLaunchKernelGGL((scan_reduce<F>), grid, dim3(SCAN_T), 0, st, f, n,
+                     chunk_sums, nchunks);
+  hipLaunchKernelGGL(scan_chunks, dim3(nseg), dim3(SCAN_T), 0, st, chunk_sums,
+                     nchunks, totals);
+  hipLaunchKernelGGL((scan_apply<F, W>), grid, dim3(SCAN_T), 0, st, f, w, n,
+                     chunk_sums, nchunks);
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
+}
+
+inline int64_t scan_sums_size(int64_t n, int64_t nseg) {
+  return (int64_t)ceil_div(n > 0 ? n : 1, SCAN_CHUNK) * nseg;
+}
+
+// ------------------------------------------------------------- utilities --
+
+__global__ void zero_i32_kernel(int32_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+int launch_zero_i32(int32_t* p, int64_t n, hipStream_t st) {
+  if (n <= 0) return LSRM_OK;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(zero_i32_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                     p, n);
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
+}
+
+// Number of valid (batch-local id in [0, nbb)) entries in a selection row is
+// not needed; rows compare by their sequence of normalised entries.
+__device__ inline int norm_entry(int v, int nbb) {
+  return (v >= 0 && v < nbb) ? v : -1;
+}
+
+// --------------------------------------------------------------- tiles --
+
+// brk[h, i] = 1 where a new run of identical (normalised) rows starts.
+__global__ __launch_bounds__(256) void breaks_kernel(
+    const int32_t* __restrict__ topk, int64_t nq, int k,
+    const int32_t* __restrict__ cu_q, int64_t batch,
+    const int32_t* __restrict__ cu_sb, uint8_t* __restrict__ brk) {
+  const int h = blockIdx.y;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nq) return;
+  int b, bs, nbb;
+  bool start;
+  query_batch(cu_q, batch, cu_sb, i, &b, &bs, &nbb, &start);
+  bool br = (i == 0) || start;
+  if (!br) {
+    const int32_t* r1 = topk + ((int64_t)h * nq + i) * k;
+    const int32_t* r0 = r1 - k;
+    for (int j = 0; j < k; ++j) {
+      if (norm_entry(r1[j], nbb) != norm_entry(r0[j], nbb)) {
+        br = true;
+        break;
+      }
+    }
+  }
+  brk[(int64_t)h * nq + i] = br ? 1 : 0;
+}
+
+struct BrkF {
+  const uint8_t* brk;
+  int64_t nq;
+  __device__ int64_t limit(int, int64_t n) const { return n; }
+  __device__ int operator()(int h, int64_t i) const {
+    return brk[(int64_t)h * nq + i];
+  }
+};
+struct RunStartW {
+  int32_t* run_start;  // [hkv, nq + 1]
+  int64_t nq;
+  __device__ void operator()(int h, int64_t i, int ex, int v,
+                             int64_t lim) const {
+    int32_t* rs = run_start + (int64_t)h * (nq + 1);
+    if (v) rs[ex] = (int32_t)i;
+    if (i == lim - 1) rs[ex + v] = (int32_t)nq;
+  }
+};
+
+struct RunTilesF {
+  const int32_t* run_start;
+  const int32_t* n_runs;  // [hkv]
+  int64_t nq;
+  int tq;
+  __device__ int64_t limit(int h, int64_t) const { return n_runs[h]; }
+  __device__ int operator()(int h, int64_t r) const {
+    const int32_t* rs = run_start + (int64_t)h * (nq + 1);
+    const int len = rs[r + 1] - rs[r];
+    return (len + tq - 1) / tq;
+  }
+};
+struct EmitTilesW {
+  const int32_t* run_start;
+  int2* tiles;
+  int64_t nq;
+  int tq;
+  __device__ void operator()(int h, int64_t r, int ex, int v, int64_t) const {
+    const int32_t* rs = run_start + (int64_t)h * (nq + 1);
+    const int s = rs[r];
+    const int len = rs[r + 1] - s;
+    int2* out = tiles + (int64_t)h * nq + ex;
+    for (int t = 0; t < v; ++t) {
+      const int q0 = s + t * tq;
+      const int rem = len - t * tq;
+      out[t] = make_int2(q0, rem < tq ? rem : tq);
+    }
+  }
+};
+
+__global__ void head_offsets_kernel(const int32_t* counts, int hkv,
+                                    int32_t* head_off, int32_t* counter) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    int acc = 0;
+    head_off[0] = 0;
+    for (int h = 0; h < hkv; ++h) {
+      acc += counts[h];
+      head_off[h + 1] = acc;
+    }
+    counter[0] = 0;
+    counter[1] = 0;
+  }
+}
+
+int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
+                    int64_t topk_n, const int32_t* cu_q, int64_t batch,
+                    const int32_t* cu_sb, int tq, Carver& ws, TilePlan& plan,
+                    hipStream_t st) {
+  uint8_t* brk = ws.take<uint8_t>((size_t)(hkv * nq));
+  int32_t* run_start = ws.take<int32_t>((size_t)(hkv * (nq + 1)));
+  int32_t* n_runs = ws.take<int32_t>((size_t)hkv);
+  int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nq, hkv));
+  plan.tiles = ws.take<int2>((size_t)(hkv * (nq > 0 ? nq : 1)));
+  plan.tile_count = ws.take<int32_t>((size_t)hkv);
+  plan.head_off = ws.take<int32_t>((size_t)(hkv + 1));
+  plan.counter = ws.take<int32_t>(64);
+  if (!ws.base) return LSRM_OK;
+  if (!ws.ok()) return LSRM_ERR_WORKSPACE;
+
+  if (nq > 0) {
+    dim3 grid(ceil_div(nq, 256), (unsigned)hkv);
+    hipLaunchKernelGGL(breaks_kernel, grid, dim3(256), 0, st, topk, nq,
+                       (int)topk_n, cu_q, batch, cu_sb, brk);
+    LSRM_CHECK_LAUNCH();
+    int rc = run_scan(BrkF{brk, nq}, RunStartW{run_start, nq}, nq, (int)hkv,
+                      sums, n_runs, st);
+    if (rc) return rc;
+    rc = run_scan(RunTilesF{run_start, n_runs, nq, tq},
+                  EmitTilesW{run_start, plan.tiles, nq, tq}, nq, (int)hkv, sums,
+                  plan.tile_count, st);
+    if (rc) return rc;
+  } else {
+    int rc = launch_zero_i32(plan.tile_count, hkv, st);
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(head_offsets_kernel, dim3(1), dim3(64), 0, st,
+                     plan.tile_count, (int)hkv, plan.head_off, plan.counter);
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
+}
+
+// --------------------------------------------------------- reverse map --
+
+// Row source: row r of head h reads the selection of query `query(h, r)`.
+struct RowSrc {
+  const int2* tiles;      // null: rows are queries
+  const int32_t* count;   // rows per head (tiles) or null
+  int64_t nq;
+  __device__ int64_t n_rows(int h) const {
+    return tiles ? (int64_t)count[h] : nq;
+  }
+  __device__ int64_t query(int h, int64_t r) const {
+    return tiles ? (int64_t)tiles[(int64_t)h * nq + r].x : r;
+  }
+};
+
+__global__ __launch_bounds__(256) void rev_count_kernel(
+    const int32_t* __restrict__ topk, int64_t nq, int k,
+    const int32_t* __restrict__ cu_q, int64_t batch,
+    const int32_t* __restrict__ cu_sb, int64_t nb, RowSrc rows,
+    int32_t* __restrict__ counts) {
+  const int h = blockIdx.y;
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows.n_rows(h)) return;
+  const int64_t q = rows.query(h, r);
+  int b, bs, nbb;
+  bool start;
+  query_batch(cu_q, batch, cu_sb, q, &b, &bs, &nbb, &start);
+  const int32_t* row = topk + ((int64_t)h * nq + q) * k;
+  for (int j = 0; j < k; ++j) {
+    const int v = row[j];
+    if (v >= 0 && v < nbb && (int64_t)bs + v < nb)
+      atomicAdd(&counts[(int64_t)h * nb + bs + v], 1);
+  }
+}
+
+__global__ __launch_bounds__(256) void rev_scatter_kernel(
+    const int32_t* __restrict__ topk, int64_t nq, int k,
+    const int32_t* __restrict__ cu_q, int64_t batch,
+    const int32_t* __restrict__ cu_sb, int64_t nb, RowSrc rows,
+    const int32_t* __restrict__ cu_rev, int32_t* __restrict__ fill,
+    int32_t* __restrict__ rev, int64_t cap) {
+  const int h = blockIdx.y;
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows.n_rows(h)) return;
+  const int64_t q = rows.query(h, r);
+  int b, bs, nbb;
+  bool start;
+  query_batch(cu_q, batch, cu_sb, q, &b, &bs, &nbb, &start);
+  const int32_t* row = topk + ((int64_t)h * nq + q) * k;
+  for (int j = 0; j < k; ++j) {
+    const int v = row[j];
+    if (v >= 0 && v < nbb && (int64_t)bs + v < nb) {
+      const int64_t c = bs + v;
+      const int64_t pos =
+          cu_rev[(int64_t)h * (nb + 1) + c] +
+          atomicAdd(&fill[(int64_t)h * nb + c], 1);
+      if (pos < cap) rev[(int64_t)h * cap + pos] = (int32_t)r;
+    }
+  }
+}
+
+struct CountF {
+  const int32_t* counts;
+  int64_t nb;
+  __device__ int64_t limit(int, int64_t n) const { return n; }
+  __device__ int operator()(int h, int64_t c) const {
+    return counts[(int64_t)h * nb + c];
+  }
+};
+struct CuRevW {
+  int32_t* cu_rev;
+  int64_t nb;
+  __device__ void operator()(int h, int64_t c, int ex, int v,
+                             int64_t lim) const {
+    int32_t* p = cu_rev + (int64_t)h * (nb + 1);
+    p[c] = ex;
+    if (c == lim - 1) p[c + 1] = ex + v;
+  }
+};
+
+constexpr int SORT_CAP = 8192;  // segments sorted in LDS up to this length
+
+// Sorts every segment rev[h, cu_rev[h,c] .. cu_rev[h,c+1]) ascending.  Short
+// segments use an LDS bitonic sort; longer ones a windowed counting sort over
+// the row-id range through `aux` (same shape as rev).
+__global__ __launch_bounds__(256) void rev_sort_kernel(
+    const int32_t* __restrict__ cu_rev, int32_t* __restrict__ rev,
+    int32_t* __restrict__ aux, int64_t nb, int64_t cap, RowSrc rows) {
+  __shared__ int s[SORT_CAP];
+  const int h = blockIdx.y;
+  const int64_t c = blockIdx.x;
+  const int64_t s0 = cu_rev[(int64_t)h * (nb + 1) + c];
+  int64_t s1 = cu_rev[(int64_t)h * (nb + 1) + c + 1];
+  if (s1 > cap) s1 = cap;
+  const int64_t len = s1 - s0;
+  if (len <= 1) return;
+  int32_t* seg = rev + (int64_t)h * cap + s0;
+  if (len <= SORT_CAP) {
+    int p = 1;
+    while (p < len) p <<= 1;
+    for (int i = threadIdx.x; i < p; i += blockDim.x)
+      s[i] = i < len ? seg[i] : INT32_MAX;
+    __syncthreads();
+    for (int kk = 2; kk <= p; kk <<= 1) {
+      for (int j = kk >> 1; j > 0; j >>= 1) {
+        for (int i = threadIdx.x; i < p; i += blockDim.x) {
+          const int ixj = i ^ j;
+          if (ixj > i) {
+            const bool up = (i & kk) == 0;
+            const int a = s[i], bb = s[ixj];
+            if ((a > bb) == up) {
+              s[i] = bb;
+              s[ixj] = a;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int i = threadIdx.x; i < len; i += blockDim.x) seg[i] = s[i];
+    return;
+  }
+  // Windowed counting sort: values are row ids in [0, n_rows).
+  int32_t* out = aux + (int64_t)h * cap + s0;
+  const int64_t range = rows.n_rows(h);
+  __shared__ int s_base;
+  if (threadIdx.x == 0) s_base = 0;
+  __syncthreads();
+  for (int64_t w0 = 0; w0 < range; w0 += SORT_CAP) {
+    for (int i = threadIdx.x; i < SORT_CAP; i += blockDim.x) s[i] = 0;
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) {
+      const int64_t v = seg[i] - w0;
+      if (v >= 0 && v < SORT_CAP) atomicAdd(&s[v], 1);
+    }
+    __syncthreads();
+    // Exclusive scan of the window counts: 256 threads x 32 entries.
+    constexpr int PER = SORT_CAP / 256;
+    int loc[PER];
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      loc[i] = s[threadIdx.x * PER + i];
+      sum += loc[i];
+    }
+    int tot;
+    int ex = block_excl_scan(sum, &tot) + s_base;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int n = loc[i];
+      for (int m = 0; m < n; ++m)
+        out[ex + m] = (int32_t)(w0 + threadIdx.x * PER + i);
+      ex += n;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) s_base += tot;
+    __syncthreads();
+  }
+  for (int64_t i = threadIdx.x; i < len; i += blockDim.x) seg[i] = out[i];
+}
+
+int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
+                      int64_t topk_n, const int32_t* cu_q, int64_t batch,
+                      const int32_t* cu_sb, int64_t nb, bool rows_are_tiles,
+                      const TilePlan* plan, Carver& ws, RevMap& map,
+                      hipStream_t st) {
+  int32_t* counts = ws.take<int32_t>((size_t)(hkv * (nb > 0 ? nb : 1)));
+  int32_t* fill = ws.take<int32_t>((size_t)(hkv * (nb > 0 ? nb : 1)));
+  int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, hkv));
+  int32_t* aux = ws.take<int32_t>((size_t)(hkv * (map.cap > 0 ? map.cap : 1)));
+  if (!map.cu_rev) map.cu_rev = ws.take<int32_t>((size_t)(hkv * (nb + 1)));
+  if (!map.rev) map.rev = ws.take<int32_t>((size_t)(hkv * (map.cap > 0 ? map.cap : 1)));
+  if (!map.totals) map.totals = ws.take<int32_t>((size_t)hkv);
+  if (!ws.base) return LSRM_OK;
+  if (!ws.ok()) return LSRM_ERR_WORKSPACE;
+
+  RowSrc rows{rows_are_tiles ? plan->tiles : nullptr,
+              rows_are_tiles ? plan->tile_count : nullptr, nq};
+  int rc = launch_zero_i32(counts, hkv * nb, st);
+  if (rc) return rc;
+  rc = launch_zero_i32(fill, hkv * nb, st);
+  if (rc) return rc;
+  if (nb == 0) {
+    rc = launch_zero_i32(map.cu_rev, hkv, st);
+    if (rc) return rc;
+    return launch_zero_i32(map.totals, hkv, st);
+  }
+  if (nq > 0) {
+    dim3 grid(ceil_div(nq, 256), (unsigned)hkv);
+    hipLaunchKernelGGL(rev_count_kernel, grid, dim3(256), 0, st, topk, nq,
+                       (int)topk_n, cu_q, batch, cu_sb, nb, rows, counts);
+    LSRM_CHECK_LAUNCH();
+  }
+  rc = run_scan(CountF{counts, nb}, CuRevW{map.cu_rev, nb}, nb, (int)hkv, sums,
+                map.totals, st);
+  if (rc) return rc;
+  if (nq > 0) {
+    dim3 grid(ceil_div(nq, 256), (unsigned)hkv);
+    hipLaunchKernelGGL(rev_scatter_kernel, grid, dim3(256), 0, st, topk, nq,
+                       (int)topk_n, cu_q, batch, cu_sb, nb, rows, map.cu_rev,
+                       fill, map.rev, map.cap);
+    LSRM_CHECK_LAUNCH();
+    dim3 sgrid((unsigned)nb, (unsigned)hkv);
+    hipLaunchKernelGGL(rev_sort_kernel, sgrid, dim3(256), 0, st, map.cu_rev,
+                       map.rev, aux, nb, map.cap, rows);
+    LSRM_CHECK_LAUNCH();
+  }
+  return LSRM_OK;
+}
+
+// ----------------------------------------------------------- key items --
+
+struct KeyChunksF {
+  const int32_t* cu;
+  int64_t nk;
+  __device__ int64_t limit(int, int64_t n) const { return n; }
+  __device__ int operator()(int, int64_t c) const {
+    int64_t s = cu[c], e = cu[c + 1];
+    s = s < 0 ? 0 : (s > nk ? nk : s);
+    e = e < 0 ? 0 : (e > nk ? nk : e);
+    return e > s ? (int)((e - s + 63) / 64) : 0;
+  }
+};
+struct KeyChunksW {
+  const int32_t* cu;
+  int64_t nk;
+  int4* items;
+  int64_t cap;
+  __device__ void operator()(int, int64_t c, int ex, int v, int64_t) const {
+    int64_t s = cu[c], e = cu[c + 1];
+    s = s < 0 ? 0 : (s > nk ? nk : s);
+    e = e < 0 ? 0 : (e > nk ? nk : e);
+    for (int t = 0; t < v && ex + t < cap; ++t) {
+      const int64_t t0 = s + 64 * t;
+      const int64_t len = e - t0 < 64 ? e - t0 : 64;
+      items[ex + t] = make_int4((int)c, (int)t0, (int)len, 0);
+    }
+  }
+};
+
+int build_key_items(const int32_t* cu_blk, int64_t nb, int64_t nk, Carver& ws,
+                    KeyItems& ki, hipStream_t st) {
+  const int64_t cap = nb + nk / 64 + 2;
+  ki.items = ws.take<int4>((size_t)cap);
+  ki.n_items = ws.take<int32_t>(64);
+  int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, 1));
+  if (!ws.base) return LSRM_OK;
+  if (!ws.ok()) return LSRM_ERR_WORKSPACE;
+  int rc = launch_zero_i32(ki.n_items, 1, st);
+  if (rc) return rc;
+  return run_scan(KeyChunksF{cu_blk, nk}, KeyChunksW{cu_blk, nk, ki.items, cap}, nb,
+                  1, sums, ki.n_items, st);
+}
+
+// ------------------------------------------------------------ validate --
+
+__global__ __launch_bounds__(256) void validate_meta_kernel(
+    const int32_t* __restrict__ cu_sb, const int32_t* __restrict__ cu_blk,
+    int64_t nb, const int32_t* __restrict__ cu_q,
+    const int32_t* __restrict__ cu_k, int64_t batch, int64_t nq, int64_t nk,
+    int32_t* flags) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int f = 0;
+  if (i < nb) {
+    const int64_t s = cu_blk[i], e = cu_blk[i + 1];
+    if (e < s) f |= LSRM_META_OFFSETS_NOT_MONOTONE;
+    if (s < 0 || e > nk) f |= LSRM_META_BLOCK_OUT_OF_RANGE;
+  }
+  if (i < batch) {
+    if (cu_sb[i + 1] < cu_sb[i] || cu_sb[i] < 0 || cu_sb[i + 1] > nb)
+      f |= LSRM_META_SEQBLOCKS_BAD;
+    if (cu_q[i + 1] < cu_q[i] || cu_k[i + 1] < cu_k[i] || cu_q[i] < 0 ||
+        cu_k[i] < 0 || cu_k[i + 1] > nk)
+      f |= LSRM_META_SEQLENS_BAD;
+    if (i == 0 && (cu_q[0] != 0 || cu_q[batch] != nq))
+      f |= LSRM_META_SEQLENS_BAD;
+    const int64_t b0 = cu_sb[i], b1 = cu_sb[i + 1];
+    if (b0 >= 0 && b1 <= nb && b1 > b0) {
+      if (cu_blk[b0] < cu_k[i] || cu_blk[b1] > cu_k[i + 1])
+        f |= LSRM_META_BLOCK_OUTSIDE_SEQ;
+    }
+  }
+  if (f) atomicOr(flags, f);
+}
+
+__global__ __launch_bounds__(256) void validate_topk_kernel(
+    const int32_t* __restrict__ topk, int64_t nq, int k,
+    const int32_t* __restrict__ cu_q, int64_t batch,
+    const int32_t* __restrict__ cu_sb, int32_t* flags) {
+  const int h = blockIdx.y;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nq) return;
+  int b, bs, nbb;
+  bool start;
+  query_batch(cu_q, batch, cu_sb, i, &b, &bs, &nbb, &start);
+  const int32_t* row = topk + ((int64_t)h * nq + i) * k;
+  bool seen_invalid = false, any = false;
+  int f = 0;
+  for (int j = 0; j < k; ++j) {
+    const bool valid = norm_entry(row[j], nbb) >= 0;
+    if (valid) {
+      any = true;
+      if (seen_invalid) f |= LSRM_META_TOPK_NOT_PREFIX;
+    } else {
+      seen_invalid = true;
+    }
+  }
+  if (!any) f |= LSRM_META_TOPK_EMPTY_ROW;
+  if (f) atomicOr(flags, f);
+}
+
+// ----------------------------------------------------------- block ids --
+
+__global__ __launch_bounds__(256) void block_ids_kernel(
+    const int32_t* __restrict__ cu_sb, int64_t batch,
+    const int32_t* __restrict__ cu_blk, int64_t nb, int64_t n, int64_t hkv,
+    int32_t* __restrict__ ids) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  int id = -1;
+  const int64_t b = upper_index(cu_blk, 0, nb + 1, t);
+  if (b >= 0 && b < nb && t < cu_blk[b + 1]) {
+    const int64_t e = upper_index(cu_sb, 0, batch + 1, b);
+    if (e >= 0 && e < batch) id = (int)(b - cu_sb[e]);
+  }
+  for (int64_t h = 0; h < hkv; ++h) ids[h * n + t] = id;
+}
+
+}  // namespace lsrm
+
+using namespace lsrm;
+
+extern "C" int lsrm_sel_attn_validate(
+    const int32_t* topk_idx, int64_t hkv, int64_t n_q, int64_t topk,
+    const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
+    int64_t n_blocks, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+    int64_t batch, int64_t n_k, int32_t* flags, void* stream) {
+  if (hkv <= 0 || n_q < 0 || topk <= 0 || n_blocks < 0 || batch <= 0 ||
+      n_k < 0 || !flags || !cu_seqblocks || !cu_block_tokens || !cu_seqlens_q ||
+      !cu_seqlens_k || (n_q > 0 && !topk_idx))
+    return LSRM_ERR_INVALID_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  int rc = launch_zero_i32(flags, 1, st);
+  if (rc) return rc;
+  const int64_t m = n_blocks > batch ? n_blocks : batch;
+  hipLaunchKernelGGL(validate_meta_kernel, dim3(ceil_div(m > 0 ? m : 1, 256)),
+                     dim3(256), 0, st, cu_seqblocks, cu_block_tokens, n_blocks,
+                     cu_seqlens_q, cu_seqlens_k, batch, n_q, n_k, flags);
+  LSRM_CHECK_LAUNCH();
+  if (n_q > 0) {
+    dim3 grid(ceil_div(n_q, 256), (unsigned)hkv);
+    hipLaunchKernelGGL(validate_topk_kernel, grid, dim3(256), 0, st, topk_idx,
+                       n_q, (int)topk, cu_seqlens_q, batch, cu_seqblocks,
+                       flags);
+    LSRM_CHECK_LAUNCH();
+  }
+  return LSRM_OK;
+}
+
+extern "C" size_t lsrm_reverse_query_map_workspace_size(int64_t n_q,
+                                                        int64_t hkv,
+                                                        int64_t topk,
+                                                        int64_t n_blocks) {
+  if (n_q < 0 || hkv <= 0 || topk <= 0 || n_blocks < 0) return 0;
+  Carver ws{nullptr, 0, 0};
+  RevMap map{};
+  map.cap = n_q * topk;
+  // cu_rev / rev / totals are caller outputs: mark them present.
+  map.cu_rev = reinterpret_cast<int32_t*>(1);
+  map.rev = reinterpret_cast<int32_t*>(1);
+  map.totals = reinterpret_cast<int32_t*>(1);
+  build_reverse_map(nullptr, hkv, n_q, topk, nullptr, 1, nullptr, n_blocks,
+                    false, nullptr, ws, map, nullptr);
+  return ws.used + 256;
+}
+
+extern "C" int lsrm_reverse_query_map(
+    const int32_t* topk_idx, int64_t hkv, int64_t n_q, int64_t topk,
+    const int32_t* cu_seqlens_q, const int32_t* cu_seqblocks, int64_t batch,
+    int64_t n_blocks, int32_t* cu_reverse_count,
+    int32_t* reverse_query_indices, int64_t capacity, int32_t* totals,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  if (hkv <= 0 || n_q < 0 || topk <= 0 || n_blocks < 0 || batch <= 0 ||
+      capacity < 0 || !cu_reverse_count || !totals || !cu_seqlens_q ||
+      !cu_seqblocks || (n_q > 0 && !topk_idx) ||
+      (capacity > 0 && !reverse_query_indices))
+    return LSRM_ERR_INVALID_ARG;
+  const size_t need =
+      lsrm_reverse_query_map_workspace_size(n_q, hkv, topk, n_blocks);
+  if (workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
+  Carver ws{reinterpret_cast<char*>(align_up((size_t)workspace, 256)), 0,
+            workspace_bytes - 256};
+  RevMap map{cu_reverse_count, reverse_query_indices, totals, capacity};
+  // The sort's aux buffer is sized by map.cap: keep it equal to capacity.
+  return build_reverse_map(topk_idx, hkv, n_q, topk, cu_seqlens_q, batch,
+                           cu_seqblocks, n_blocks, false, nullptr, ws, map,
+                           (hipStream_t)stream);
+}
+
+extern "C" int lsrm_block_ids(const int32_t* cu_seqblocks, int64_t batch,
+                              const int32_t* cu_block_tokens, int64_t n_blocks,
+                              int64_t n_tokens, int64_t hkv, int32_t* ids,
+                              void* stream) {
+  if (batch <= 0 || n_blocks < 0 || n_tokens < 0 || hkv <= 0 || !cu_seqblocks ||
+      !cu_block_tokens || (n_tokens > 0 && !ids))
+    return LSRM_ERR_INVALID_ARG;
+  if (n_tokens == 0) return LSRM_OK;
+  hipLaunchKernelGGL(block_ids_kernel, dim3(ceil_div(n_tokens, 256)), dim3(256),
+                     0, (hipStream_t)stream, cu_seqblocks, batch,
+                     cu_block_tokens, n_blocks, n_tokens, hkv, ids);
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
+}

@@ -1,0 +1,246 @@
+// Block mean pooling over variable-length token blocks (key/value block
+// compression of LSRM, sparse/module/spatial_sparse_attention.py:27-37, which
+// calls torch.segment_reduce(reduce="mean") on a [N, H*D] tensor).
+//
+// Two streaming kernels:
+//   pool_pieces  : one thread per (64-row chunk, 8-channel group) sums its rows
+//                  in fp32, emitting a partial sum each time a block boundary
+//                  is crossed.  Partial (block b, chunk j) lives at row b + j
+//                  of the partial buffer (unique because blocks are
+//                  contiguous and ordered).
+//   pool_combine : one thread per (block, 8-channel group) adds the block's
+//                  partials in chunk order, divides by the length and rounds.
+// Every add is sequential, so the result is a fixed function of the input
+// (the contract the CPU oracle restates bit for bit).
+#include "common.h"
+
+namespace lsrm {
+
+constexpr int POOL_CHUNK = 64;  // rows per piece boundary (part of the contract)
+constexpr int POOL_VEC = 8;     // channels per thread on the vector path
+
+template <int DT>
+struct Vec8 {
+  // Loads channels [c, c+8) of row r as fp32.
+  __device__ static inline void load(const void* x, int64_t off, float* v) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(
+        reinterpret_cast<const uint16_t*>(x) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = to_f32<DT>((uint16_t)(w[i] & 0xffffu));
+      v[2 * i + 1] = to_f32<DT>((uint16_t)(w[i] >> 16));
+    }
+  }
+};
+template <>
+struct Vec8<LSRM_F32> {
+  __device__ static inline void load(const void* x, int64_t off, float* v) {
+    const float4* p =
+        reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + off);
+    float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+};
+
+template <int DT>
+__device__ inline float load1(const void* x, int64_t off) {
+  if constexpr (DT == LSRM_F32)
+    return reinterpret_cast<const float*>(x)[off];
+  else
+    return to_f32<DT>(reinterpret_cast<const uint16_t*>(x)[off]);
+}
+
+// VEC channels per thread (8 on the 16-byte path, 1 on the scalar path).
+template <int DT, int VEC>
+__global__ __launch_bounds__(256) void pool_pieces(
+    const void* __restrict__ x, int64_t n, int64_t ch,
+    const int32_t* __restrict__ cu, int64_t nb, float* __restrict__ partial) {
+  const int64_t n_vec = ch / VEC;
+  const int64_t n_chunks = (n + POOL_CHUNK - 1) / POOL_CHUNK;
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= n_chunks * n_vec) return;
+  const int64_t j = item / n_vec;
+  const int64_t c0 = (item - j * n_vec) * VEC;
+  const int64_t r0 = j * POOL_CHUNK;
+  const int64_t r1 = r0 + POOL_CHUNK < n ? r0 + POOL_CHUNK : n;
+
+  // b = last block whose start is <= r0 (-1: before the first block,
+  // nb: past the last).  bs/be bound the rows block b owns.
+  int64_t b = upper_index(cu, 0, nb + 1, r0);
+  if (b > nb) b = nb;
+  int64_t be = b < 0 ? (int64_t)cu[0] : (b < nb ? (int64_t)cu[b + 1] : INT64_MAX);
+  int64_t bs = (b >= 0 && b < nb) ? (int64_t)cu[b] : INT64_MAX;
+
+  float acc[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) acc[i] = 0.0f;
+  bool have = false;
+
+  auto flush = [&]() {
+    float* dst = partial + (b + j) * ch + c0;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) dst[i] = acc[i];
+  };
+
+  constexpr int U = VEC == 8 ? 8 : 16;  // rows in flight per thread
+  for (int64_t r = r0; r < r1; r += U) {
+    float v[U][VEC];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (r + u < r1) {
+        if constexpr (VEC == 8)
+          Vec8<DT>::load(x, (r + u) * ch + c0, v[u]);
+        else
+          v[u][0] = load1<DT>(x, (r + u) * ch + c0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t row = r + u;
+      if (row < r1) {
+        while (b < nb && row >= be) {
+          if (have) flush();
+          have = false;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[i] = 0.0f;
+          ++b;
+          bs = b < nb ? (int64_t)cu[b] : INT64_MAX;
+          be = b < nb ? (int64_t)cu[b + 1] : INT64_MAX;
+        }
+        if (b >= 0 && b < nb && row >= bs) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[i] = acc[i] + v[u][i];
+          have = true;
+        }
+      }
+    }
+  }
+  if (have && b >= 0 && b < nb) flush();
+}
+
+template <int ODT>
+__device__ inline void store_out(void* out, int64_t off, float v) {
+  if constexpr (ODT == LSRM_F32)
+    reinterpret_cast<float*>(out)[off] = v;
+  else
+    reinterpret_cast<uint16_t*>(out)[off] = from_f32<ODT>(v);
+}
+
+template <int ODT, int VEC>
+__global__ __launch_bounds__(256) void pool_combine(
+    const float* __restrict__ partial, int64_t n, int64_t ch,
+    const int32_t* __restrict__ cu, int64_t nb, void* __restrict__ out) {
+  const int64_t n_vec = ch / VEC;
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= nb * n_vec) return;
+  const int64_t b = item / n_vec;
+  const int64_t c0 = (item - b * n_vec) * VEC;
+  int64_t s = cu[b], e = cu[b + 1];
+  s = s < 0 ? 0 : (s > n ? n : s);
+  e = e < 0 ? 0 : (e > n ? n : e);
+  float acc[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) acc[i] = 0.0f;
+  if (e > s) {
+    const int64_t j0 = s / POOL_CHUNK, j1 = (e - 1) / POOL_CHUNK;
+    for (int64_t j = j0; j <= j1; ++j) {
+      const float* src = partial + (b + j) * ch + c0;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[i] = acc[i] + src[i];
+    }
+  }
+  // IEEE quotient; a block with no rows gives 0/0 = NaN.
+  const float len = e > s ? (float)(e - s) : 0.0f;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) store_out<ODT>(out, b * ch + c0 + i, acc[i] / len);
+}
+
+int64_t pool_partial_rows(int64_t n, int64_t nb) {
+  return nb + (n + POOL_CHUNK - 1) / POOL_CHUNK;
+}
+
+// Launches the two pooling kernels; partial needs pool_partial_rows * ch floats.
+int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
+                           const int32_t* cu, int64_t nb, void* out,
+                           int out_dtype, float* partial, hipStream_t st) {
+  if (nb == 0) return LSRM_OK;
+  const bool vec = (ch % POOL_VEC) == 0 && ((uintptr_t)x % 16) == 0 &&
+                   ((uintptr_t)partial % 16) == 0;
+  const int64_t n_vec = vec ? ch / POOL_VEC : ch;
+  const int64_t n_chunks = (n + POOL_CHUNK - 1) / POOL_CHUNK;
+  if (n > 0) {
+    const int64_t items = n_chunks * n_vec;
+    dim3 grid((unsigned)((items + 255) / 256));
+#define LSRM_POOL_P(DT)                                                      \
+  do {                                                                       \
+    if (vec)                                                                 \
+      hipLaunchKernelGGL((pool_pieces<DT, 8>), grid, dim3(256), 0, st, x, n, \
+                         ch, cu, nb, partial);                               \
+    else                                                                     \
+      hipLaunchKernelGGL((pool_pieces<DT, 1>), grid, dim3(256), 0, st, x, n, \
+                         ch, cu, nb, partial);                               \
+  } while (0)
+    switch (x_dtype) {
+      case LSRM_F32: LSRM_POOL_P(LSRM_F32); break;
+      case LSRM_F16: LSRM_POOL_P(LSRM_F16); break;
+      case LSRM_BF16: LSRM_POOL_P(LSRM_BF16); break;
+      default: return LSRM_ERR_UNSUPPORTED;
+    }
+#undef LSRM_POOL_P
+    LSRM_CHECK_LAUNCH();
+  }
+  {
+    const int64_t items = nb * n_vec;
+    dim3 grid((unsigned)((items + 255) / 256));
+#define LSRM_POOL_C(ODT)                                                     \
+  do {                                                                       \
+    if (vec)                                                                 \
+      hipLaunchKernelGGL((pool_combine<ODT, 8>), grid, dim3(256), 0, st,     \
+                         partial, n, ch, cu, nb, out);                       \
+    else                                                                     \
+      hipLaunchKernelGGL((pool_combine<ODT, 1>), grid, dim3(256), 0, st,     \
+                         partial, n, ch, cu, nb, out);                       \
+  } while (0)
+    switch (out_dtype) {
+      case LSRM_F32: LSRM_POOL_C(LSRM_F32); break;
+      case LSRM_F16: LSRM_POOL_C(LSRM_F16); break;
+      case LSRM_BF16: LSRM_POOL_C(LSRM_BF16); break;
+      default: return LSRM_ERR_UNSUPPORTED;
+    }
+#undef LSRM_POOL_C
+    LSRM_CHECK_LAUNCH();
+  }
+  return LSRM_OK;
+}
+
+}  // namespace lsrm
+
+extern "C" size_t lsrm_block_mean_pool_workspace_size(int64_t n_tokens,
+                                                      int64_t channels,
+                                                      int64_t n_blocks) {
+  if (n_tokens < 0 || channels < 0 || n_blocks < 0) return 0;
+  return (size_t)lsrm::pool_partial_rows(n_tokens, n_blocks) *
+             (size_t)channels * sizeof(float) +
+         256;
+}
+
+extern "C" int lsrm_block_mean_pool(const void* x, int x_dtype,
+                                    int64_t n_tokens, int64_t channels,
+                                    const int32_t* cu_block_tokens,
+                                    int64_t n_blocks, void* out, int out_dtype,
+                                    void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  if (n_tokens < 0 || channels <= 0 || n_blocks < 0) return LSRM_ERR_INVALID_ARG;
+  if (n_blocks > 0 && (!cu_block_tokens || !out)) return LSRM_ERR_INVALID_ARG;
+  if (n_tokens > 0 && !x) return LSRM_ERR_INVALID_ARG;
+  if (x_dtype < LSRM_F32 || x_dtype > LSRM_BF16) return LSRM_ERR_UNSUPPORTED;
+  if (out_dtype < LSRM_F32 || out_dtype > LSRM_BF16) return LSRM_ERR_UNSUPPORTED;
+  const size_t need =
+      lsrm_block_mean_pool_workspace_size(n_tokens, channels, n_blocks);
+  if (workspace_bytes < need || (need > 256 && !workspace)) return LSRM_ERR_WORKSPACE;
+  float* partial = reinterpret_cast<float*>(lsrm::align_up((size_t)workspace, 256));
+  return lsrm::launch_block_mean_pool(x, x_dtype, n_tokens, channels,
+                                      cu_block_tokens, n_blocks, out, out_dtype,
+                                      partial, (hipStream_t)stream);
+}

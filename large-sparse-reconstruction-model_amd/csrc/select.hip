@@ -1,0 +1,284 @@
+// Per-query-block top-k block selection.
+//
+// The rule (no reference function implements it; the reference's learned
+// selection is sparse/ops/block_score.py:16-98): mean-pool Q and K per block
+// (fp32, the lsrm_block_mean_pool contract), score every (query block b,
+// key block c) pair of a batch element as
+//     s(b, c) = sum_{g in group(h)} sum_d (double)pq[b,g,d] * (double)pk[c,h,d]
+// accumulated in fp64 in that order (fp32 x fp32 products are exact in fp64,
+// so the sum is a fixed function of the pooled means), then take the forced
+// blocks followed by the best remaining blocks under (score descending,
+// block id ascending).  Selected ids are written ascending, -1 padded.
+#include "common.h"
+
+namespace lsrm {
+
+int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
+                           const int32_t* cu, int64_t nb, void* out,
+                           int out_dtype, float* partial, hipStream_t st);
+int64_t pool_partial_rows(int64_t n, int64_t nb);
+
+constexpr int SCORE_TILE = 64;
+constexpr int SEL_MAXD = 128;
+constexpr int SEL_CAND_LDS = 8192;      // candidate scores cached in LDS
+constexpr int SEL_MAX_CAND = 65536;     // bitmap capacity (blocks per batch)
+constexpr int SEL_MAXK = 256;
+
+// scores[h, b, c] for b, c in [0, nb): 64x64 tile per workgroup, 4x4 per
+// thread, fp64 accumulation over (g, d) in order.
+__global__ __launch_bounds__(256) void score_kernel(
+    const float* __restrict__ pq, const float* __restrict__ pk, int64_t nb,
+    int hq, int hkv, int d, double* __restrict__ scores) {
+  __shared__ float sq[SCORE_TILE][SEL_MAXD + 1];
+  __shared__ float sk[SCORE_TILE][SEL_MAXD + 1];
+  const int h = blockIdx.z;
+  const int64_t b0 = (int64_t)blockIdx.y * SCORE_TILE;
+  const int64_t c0 = (int64_t)blockIdx.x * SCORE_TILE;
+  const int g_n = hq / hkv;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  double acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+
+  for (int i = threadIdx.x; i < SCORE_TILE * d; i += 256) {
+    const int r = i / d, dd = i - r * d;
+    sk[r][dd] = (c0 + r < nb) ? pk[(c0 + r) * (int64_t)hkv * d + (int64_t)h * d + dd] : 0.0f;
+  }
+  for (int g = 0; g < g_n; ++g) {
+    const int hh = h * g_n + g;
+    for (int i = threadIdx.x; i < SCORE_TILE * d; i += 256) {
+      const int r = i / d, dd = i - r * d;
+      sq[r][dd] = (b0 + r < nb) ? pq[(b0 + r) * (int64_t)hq * d + (int64_t)hh * d + dd] : 0.0f;
+    }
+    __syncthreads();
+    for (int dd = 0; dd < d; ++dd) {
+      double a[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = (double)sq[ty * 4 + i][dd];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = (double)sk[tx * 4 + j][dd];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fma(a[i], bv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t b = b0 + ty * 4 + i;
+    if (b >= nb) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t c = c0 + tx * 4 + j;
+      if (c < nb) scores[((int64_t)h * nb + b) * nb + c] = acc[i][j];
+    }
+  }
+}
+
+__device__ inline bool sel_better(double s1, int i1, double s2, int i2) {
+  return s1 > s2 || (s1 == s2 && i1 < i2);
+}
+
+// One workgroup per (query block b, kv head h).
+__global__ __launch_bounds__(256) void topk_kernel(
+    const double* __restrict__ scores, int64_t nb,
+    const int32_t* __restrict__ cu_sb, int64_t batch,
+    const int32_t* __restrict__ cu_blk, int64_t n_tokens, int topk,
+    const int32_t* __restrict__ forced, int n_forced, int force_self,
+    int32_t* __restrict__ topk_idx, int32_t* __restrict__ compact) {
+  __shared__ double s_sc[SEL_CAND_LDS];
+  __shared__ uint32_t s_taken[SEL_MAX_CAND / 32];
+  __shared__ int s_sel[SEL_MAXK];
+  __shared__ int s_out[SEL_MAXK];
+  __shared__ double s_ws[4];
+  __shared__ int s_wi[4];
+  __shared__ int s_nsel;
+
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t e = upper_index(cu_sb, 0, batch + 1, b);
+  int32_t* crow = compact + ((int64_t)h * nb + b) * topk;
+  if (e < 0 || e >= batch || b >= cu_sb[e + 1]) {
+    for (int j = tid; j < topk; j += 256) crow[j] = -1;
+    return;
+  }
+  const int64_t cs = cu_sb[e];
+  const int nbb = (int)(cu_sb[e + 1] - cs);
+  const bool cached = nbb <= SEL_CAND_LDS;
+  const double* row = scores + ((int64_t)h * nb + b) * nb + cs;
+
+  for (int i = tid; i < (nbb + 31) / 32; i += 256) s_taken[i] = 0u;
+  if (cached) {
+    for (int i = tid; i < nbb; i += 256) {
+      const double v = row[i];
+      s_sc[i] = (v != v) ? -__builtin_inf() : v;
+    }
+  }
+  __syncthreads();
+  const int kmax = topk < nbb ? topk : nbb;
+  if (tid == 0) {
+    int n = 0;
+    auto add = [&](int id) {
+      if (n >= kmax || id < 0 || id >= nbb) return;
+      if (s_taken[id >> 5] & (1u << (id & 31))) return;
+      s_taken[id >> 5] |= 1u << (id & 31);
+      s_sel[n++] = id;
+    };
+    if (force_self) add((int)(b - cs));
+    for (int f = 0; f < n_forced; ++f) add(forced[f]);
+    s_nsel = n;
+  }
+  __syncthreads();
+
+  for (int n = s_nsel; n < kmax; ++n) {
+    double bs = -__builtin_inf();
+    int bi = INT32_MAX;
+    for (int i = tid; i < nbb; i += 256) {
+      if (s_taken[i >> 5] & (1u << (i & 31))) continue;
+      double v;
+      if (cached) {
+        v = s_sc[i];
+      } else {
+        v = row[i];
+        if (v != v) v = -__builtin_inf();
+      }
+      if (sel_better(v, i, bs, bi)) {
+        bs = v;
+        bi = i;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const double os = __shfl_xor(bs, o);
+      const int oi = __shfl_xor(bi, o);
+      if (sel_better(os, oi, bs, bi)) {
+        bs = os;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      s_ws[w] = bs;
+      s_wi[w] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      double fs = s_ws[0];
+      int fi = s_wi[0];
+      for (int i = 1; i < 4; ++i)
+        if (sel_better(s_ws[i], s_wi[i], fs, fi)) {
+          fs = s_ws[i];
+          fi = s_wi[i];
+        }
+      s_sel[n] = fi;
+      s_taken[fi >> 5] |= 1u << (fi & 31);
+    }
+    __syncthreads();
+  }
+  // Ascending order by rank (ids are distinct), -1 padding.
+  for (int j = tid; j < topk; j += 256) s_out[j] = -1;
+  __syncthreads();
+  for (int j = tid; j < kmax; j += 256) {
+    const int v = s_sel[j];
+    int r = 0;
+    for (int m = 0; m < kmax; ++m) r += s_sel[m] < v;
+    s_out[r] = v;
+  }
+  __syncthreads();
+  for (int j = tid; j < topk; j += 256) crow[j] = s_out[j];
+  int64_t t0 = cu_blk[b], t1 = cu_blk[b + 1];
+  t0 = t0 < 0 ? 0 : (t0 > n_tokens ? n_tokens : t0);
+  t1 = t1 < t0 ? t0 : (t1 > n_tokens ? n_tokens : t1);
+  int32_t* dst = topk_idx + ((int64_t)h * n_tokens + t0) * topk;
+  const int64_t total = (t1 - t0) * topk;
+  for (int64_t i = tid; i < total; i += 256) dst[i] = s_out[i % topk];
+}
+
+struct SelectWs {
+  float* pq;
+  float* pk;
+  float* partial;
+  double* scores;
+};
+
+void carve_select(Carver& ws, int64_t n, int64_t nb, int64_t hq, int64_t hkv,
+                  int64_t d, SelectWs& s) {
+  const int64_t nbc = nb > 0 ? nb : 1;
+  s.pq = ws.take<float>((size_t)(nbc * hq * d));
+  s.pk = ws.take<float>((size_t)(nbc * hkv * d));
+  s.partial = ws.take<float>((size_t)(pool_partial_rows(n, nbc) *
+                                      (hq > hkv ? hq : hkv) * d));
+  s.scores = ws.take<double>((size_t)(hkv * nbc * nbc));
+}
+
+}  // namespace lsrm
+
+using namespace lsrm;
+
+extern "C" size_t lsrm_select_blocks_workspace_size(int64_t n_tokens,
+                                                    int64_t n_blocks,
+                                                    int64_t hq, int64_t hkv,
+                                                    int64_t head_dim) {
+  if (n_tokens < 0 || n_blocks < 0 || hq <= 0 || hkv <= 0 || head_dim <= 0)
+    return 0;
+  Carver ws{nullptr, 0, 0};
+  SelectWs s;
+  carve_select(ws, n_tokens, n_blocks, hq, hkv, head_dim, s);
+  return ws.used + 256;
+}
+
+extern "C" int lsrm_select_blocks(const void* q, const void* k, int dtype,
+                                  int64_t n_tokens, int64_t hq, int64_t hkv,
+                                  int64_t head_dim, const int32_t* cu_seqblocks,
+                                  int64_t batch,
+                                  const int32_t* cu_block_tokens,
+                                  int64_t n_blocks, int64_t topk,
+                                  const int32_t* forced_blocks,
+                                  int64_t n_forced, int force_self,
+                                  int32_t* topk_idx, int32_t* topk_compact,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  if (n_tokens < 0 || hq <= 0 || hkv <= 0 || head_dim <= 0 || batch <= 0 ||
+      n_blocks < 0 || topk <= 0 || n_forced < 0 || !cu_seqblocks ||
+      !cu_block_tokens || (n_forced > 0 && !forced_blocks) ||
+      (n_tokens > 0 && (!q || !k || !topk_idx)) ||
+      (n_blocks > 0 && !topk_compact))
+    return LSRM_ERR_INVALID_ARG;
+  if (hq % hkv != 0) return LSRM_ERR_INVALID_ARG;
+  if (dtype < LSRM_F32 || dtype > LSRM_BF16) return LSRM_ERR_UNSUPPORTED;
+  if (head_dim > SEL_MAXD || topk > SEL_MAXK || n_blocks > SEL_MAX_CAND)
+    return LSRM_ERR_UNSUPPORTED;
+  const size_t need = lsrm_select_blocks_workspace_size(n_tokens, n_blocks, hq,
+                                                        hkv, head_dim);
+  if (workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
+  if (n_blocks == 0) return LSRM_OK;
+  hipStream_t st = (hipStream_t)stream;
+  Carver ws{reinterpret_cast<char*>(align_up((size_t)workspace, 256)), 0,
+            workspace_bytes - 256};
+  SelectWs s;
+  carve_select(ws, n_tokens, n_blocks, hq, hkv, head_dim, s);
+  if (!ws.ok()) return LSRM_ERR_WORKSPACE;
+
+  int rc = launch_block_mean_pool(q, dtype, n_tokens, hq * head_dim,
+                                  cu_block_tokens, n_blocks, s.pq, LSRM_F32,
+                                  s.partial, st);
+  if (rc) return rc;
+  rc = launch_block_mean_pool(k, dtype, n_tokens, hkv * head_dim,
+                              cu_block_tokens, n_blocks, s.pk, LSRM_F32,
+                              s.partial, st);
+  if (rc) return rc;
+  const unsigned nt = (unsigned)ceil_div(n_blocks, SCORE_TILE);
+  hipLaunchKernelGGL(score_kernel, dim3(nt, nt, (unsigned)hkv), dim3(256), 0,
+                     st, s.pq, s.pk, n_blocks, (int)hq, (int)hkv,
+                     (int)head_dim, s.scores);
+  LSRM_CHECK_LAUNCH();
+  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)n_blocks, (unsigned)hkv),
+                     dim3(256), 0, st, s.scores, n_blocks, cu_seqblocks, batch,
+                     cu_block_tokens, n_tokens, (int)topk, forced_blocks,
+                     (int)n_forced, force_self, topk_idx, topk_compact);
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
+}

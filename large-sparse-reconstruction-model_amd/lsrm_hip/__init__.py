@@ -1,0 +1,331 @@
+"""Python binding of liblsrm_hip.so (the C ABI in include/lsrm_hip.h).
+
+PyTorch supplies device memory and the current HIP stream; every compute call
+goes to a gfx950 kernel in liblsrm_hip.so through ctypes.  There is no CPU or
+PyTorch fallback: a missing library or a CPU tensor raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from pathlib import Path
+from typing import Optional, Sequence
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "liblsrm_hip.so"
+
+F32, F16, BF16 = 0, 1, 2
+_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+# lsrm_meta_error bits (include/lsrm_hip.h)
+META_ERRORS = {
+    1: "cu_block_include_tokens is not monotone",
+    2: "a block's token range lies outside [0, n_k)",
+    4: "cu_seqblocks is not monotone or exceeds the block count",
+    8: "cu_seqlens_q / cu_seqlens_k are not valid offsets",
+    16: "a top-k row has a valid block id after an invalid entry",
+    32: "a top-k row selects no valid block",
+    64: "a batch element's blocks leave its key range",
+}
+META_TOPK_EMPTY_ROW = 32
+
+_lib = None
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+_SIGNATURES = {
+    "lsrm_status_string": (ctypes.c_char_p, [_I]),
+    "lsrm_version": (_I, []),
+    "lsrm_block_mean_pool_workspace_size": (_SZ, [_I64, _I64, _I64]),
+    "lsrm_block_mean_pool": (_I, [_P, _I, _I64, _I64, _P, _I64, _P, _I, _P, _SZ, _P]),
+    "lsrm_select_blocks_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "lsrm_select_blocks": (
+        _I,
+        [_P, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I,
+         _P, _P, _P, _SZ, _P],
+    ),
+    "lsrm_sel_attn_validate": (
+        _I, [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _P, _P]),
+    "lsrm_sel_attn_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I]),
+    "lsrm_sel_attn_fwd": (
+        _I,
+        [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P,
+         _I64, _F, _P, _P, _P, _SZ, _P],
+    ),
+    "lsrm_sel_attn_bwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P,
+         _I64, _P, _I64, _F, _P, _P, _P, _P, _P, _SZ, _P],
+    ),
+    "lsrm_reverse_query_map_workspace_size": (_SZ, [_I64, _I64, _I64, _I64]),
+    "lsrm_reverse_query_map": (
+        _I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _SZ, _P]),
+    "lsrm_block_ids": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P]),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Loads liblsrm_hip.so (built in-tree by lsrm_hip.build)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m lsrm_hip.build` "
+                "(there is no CPU fallback)")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def exported_symbols() -> list:
+    return list(_SIGNATURES)
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().lsrm_status_string(rc).decode()
+        raise RuntimeError(f"{what} failed: {msg} (status {rc})")
+
+
+def _dev_check(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                "lsrm_hip kernels need ROCm device tensors; got a tensor on "
+                f"{t.device} (there is no CPU fallback)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError("all tensors must live on the same device")
+    return dev
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    return t.contiguous()
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+
+# --------------------------------------------------------------- pooling --
+
+def block_mean_pool(x: torch.Tensor, cu_block_tokens: torch.Tensor,
+                    out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Mean of each block's rows of a 2-D [N, C] tensor -> [n_blocks, C].
+
+    Bit-exact contract: fp32 sums over pieces cut at multiples of 64 rows and
+    at block boundaries, sequential within and across pieces, IEEE divide,
+    round-to-nearest-even to out_dtype (default: x's dtype).
+    """
+    if x.dim() != 2:
+        raise ValueError("x must be 2-D [n_tokens, channels]")
+    if x.dtype not in _DTYPE_CODE:
+        raise TypeError(f"unsupported dtype {x.dtype}")
+    out_dtype = out_dtype or x.dtype
+    if out_dtype not in _DTYPE_CODE:
+        raise TypeError(f"unsupported output dtype {out_dtype}")
+    dev = _dev_check(x, cu_block_tokens)
+    x = x.contiguous()
+    cu = _i32(cu_block_tokens)
+    n, c = x.shape
+    nb = cu.numel() - 1
+    out = torch.empty(nb, c, dtype=out_dtype, device=dev)
+    if nb == 0:
+        return out
+    with torch.cuda.device(dev):
+        ws_n = lib().lsrm_block_mean_pool_workspace_size(n, c, nb)
+        ws = _workspace(ws_n, dev)
+        _check(lib().lsrm_block_mean_pool(
+            _ptr(x), _DTYPE_CODE[x.dtype], n, c, _ptr(cu), nb, _ptr(out),
+            _DTYPE_CODE[out_dtype], _ptr(ws), ws.numel(), _stream(dev)),
+            "lsrm_block_mean_pool")
+    return out
+
+
+# ------------------------------------------------------------- selection --
+
+def select_blocks(q: torch.Tensor, k: torch.Tensor, cu_seqblocks: torch.Tensor,
+                  cu_block_tokens: torch.Tensor, topk: int,
+                  forced_blocks: Optional[Sequence[int]] = None,
+                  force_self: bool = True):
+    """Per-query-block top-k selection (self attention).
+
+    q [N, Hq, D], k [N, Hkv, D].  Returns (topk_idx [Hkv, N, topk],
+    topk_compact [Hkv, n_blocks, topk]) int32, ids batch-local, ascending,
+    -1 padded.
+    """
+    if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError("q [N, Hq, D] and k [N, Hkv, D] must share N and D")
+    if q.dtype != k.dtype or q.dtype not in _DTYPE_CODE:
+        raise TypeError("q and k must share a float dtype")
+    if q.shape[1] % k.shape[1] != 0:
+        raise ValueError("Hq must be a multiple of Hkv")
+    if topk <= 0:
+        raise ValueError("topk must be positive")
+    dev = _dev_check(q, k, cu_seqblocks, cu_block_tokens)
+    q = q.contiguous()
+    k = k.contiguous()
+    cu_sb = _i32(cu_seqblocks)
+    cu = _i32(cu_block_tokens)
+    n, hq, d = q.shape
+    hkv = k.shape[1]
+    nb = cu.numel() - 1
+    batch = cu_sb.numel() - 1
+    forced = None
+    if forced_blocks is not None and len(forced_blocks) > 0:
+        forced = torch.as_tensor(list(forced_blocks), dtype=torch.int32, device=dev)
+    topk_idx = torch.full((hkv, n, topk), -1, dtype=torch.int32, device=dev)
+    compact = torch.full((hkv, max(nb, 0), topk), -1, dtype=torch.int32, device=dev)
+    if nb == 0 or n == 0:
+        return topk_idx, compact
+    with torch.cuda.device(dev):
+        ws_n = lib().lsrm_select_blocks_workspace_size(n, nb, hq, hkv, d)
+        ws = _workspace(ws_n, dev)
+        _check(lib().lsrm_select_blocks(
+            _ptr(q), _ptr(k), _DTYPE_CODE[q.dtype], n, hq, hkv, d, _ptr(cu_sb), batch,
+            _ptr(cu), nb, topk, _ptr(forced), 0 if forced is None else forced.numel(),
+            1 if force_self else 0, _ptr(topk_idx), _ptr(compact), _ptr(ws), ws.numel(),
+            _stream(dev)), "lsrm_select_blocks")
+    return topk_idx, compact
+
+
+# ------------------------------------------------------------- attention --
+
+def validate(topk_idx: torch.Tensor, cu_seqblocks: torch.Tensor,
+             cu_block_tokens: torch.Tensor, cu_seqlens_q: torch.Tensor,
+             cu_seqlens_k: torch.Tensor, n_k: int) -> int:
+    """Device-side metadata check; returns the lsrm_meta_error bits (syncs)."""
+    dev = _dev_check(topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q, cu_seqlens_k)
+    topk_idx = _i32(topk_idx)
+    hkv, nq, k = topk_idx.shape
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib().lsrm_sel_attn_validate(
+            _ptr(topk_idx), hkv, nq, k, _ptr(_i32(cu_seqblocks)),
+            _ptr(_i32(cu_block_tokens)), cu_block_tokens.numel() - 1,
+            _ptr(_i32(cu_seqlens_q)), _ptr(_i32(cu_seqlens_k)), cu_seqlens_q.numel() - 1,
+            n_k, _ptr(flags), _stream(dev)), "lsrm_sel_attn_validate")
+    return int(flags.item())
+
+
+def describe_meta_error(bits: int) -> str:
+    return "; ".join(msg for b, msg in META_ERRORS.items() if bits & b)
+
+
+def sel_attn_fwd(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
+                 softmax_scale: float):
+    """Selected-block attention forward -> (out [Nq, Hq, D], lse [Hq, Nq] log2)."""
+    dev = _dev_check(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q)
+    nq, hq, d = q.shape
+    nk, hkv, _ = k.shape
+    topk = topk_idx.shape[-1]
+    nb = cu_block_tokens.numel() - 1
+    batch = cu_seqlens_q.numel() - 1
+    out = torch.empty_like(q)
+    lse = torch.empty(hq, nq, dtype=torch.float32, device=dev)
+    if nq == 0:
+        return out, lse
+    with torch.cuda.device(dev):
+        ws_n = lib().lsrm_sel_attn_workspace_size(nq, nk, hq, hkv, topk, nb, 0)
+        ws = _workspace(ws_n, dev)
+        _check(lib().lsrm_sel_attn_fwd(
+            _ptr(q), _ptr(k), _ptr(v), _DTYPE_CODE[q.dtype], nq, nk, hq, hkv, d,
+            _ptr(topk_idx), topk, _ptr(cu_seqblocks), _ptr(cu_block_tokens), nb,
+            _ptr(cu_seqlens_q), batch, float(softmax_scale), _ptr(out), _ptr(lse),
+            _ptr(ws), ws.numel(), _stream(dev)), "lsrm_sel_attn_fwd")
+    return out, lse
+
+
+def sel_attn_bwd(do, q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens,
+                 cu_seqlens_q, softmax_scale: float):
+    """Selected-block attention backward -> (dq, dk, dv, delta)."""
+    dev = _dev_check(do, q, k, v, o, lse, topk_idx)
+    nq, hq, d = q.shape
+    nk, hkv, _ = k.shape
+    topk = topk_idx.shape[-1]
+    nb = cu_block_tokens.numel() - 1
+    batch = cu_seqlens_q.numel() - 1
+    dq = torch.empty_like(q)
+    dk = torch.zeros_like(k)   # keys outside every block get zero gradient
+    dv = torch.zeros_like(v)
+    delta = torch.empty(hq, nq, dtype=torch.float32, device=dev)
+    if nq == 0:
+        return dq, dk, dv, delta
+    with torch.cuda.device(dev):
+        ws_n = lib().lsrm_sel_attn_workspace_size(nq, nk, hq, hkv, topk, nb, 1)
+        ws = _workspace(ws_n, dev)
+        _check(lib().lsrm_sel_attn_bwd(
+            _ptr(do), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse),
+            _DTYPE_CODE[q.dtype], nq, nk, hq, hkv, d, _ptr(topk_idx), topk,
+            _ptr(cu_seqblocks), _ptr(cu_block_tokens), nb, _ptr(cu_seqlens_q), batch,
+            float(softmax_scale), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta),
+            _ptr(ws), ws.numel(), _stream(dev)), "lsrm_sel_attn_bwd")
+    return dq, dk, dv, delta
+
+
+def reverse_query_map(topk_idx: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                      cu_seqblocks: torch.Tensor, total_blocks: int):
+    """CSR inverse of a top-k selection (the reference's
+    _build_reverse_query_mapping): returns (cu_reverse_count [Hkv, nb+1],
+    reverse_query_indices [Hkv, max_entries]) int32, segments ascending.
+    Synchronises once to size the output, as the reference does."""
+    dev = _dev_check(topk_idx, cu_seqlens_q, cu_seqblocks)
+    topk_idx = _i32(topk_idx)
+    hkv, nq, k = topk_idx.shape
+    cap = max(nq * k, 1)
+    cu_rev = torch.empty(hkv, total_blocks + 1, dtype=torch.int32, device=dev)
+    rev = torch.empty(hkv, cap, dtype=torch.int32, device=dev)
+    totals = torch.empty(hkv, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        ws_n = lib().lsrm_reverse_query_map_workspace_size(nq, hkv, k, total_blocks)
+        ws = _workspace(ws_n, dev)
+        _check(lib().lsrm_reverse_query_map(
+            _ptr(topk_idx), hkv, nq, k, _ptr(_i32(cu_seqlens_q)), _ptr(_i32(cu_seqblocks)),
+            cu_seqblocks.numel() - 1, total_blocks, _ptr(cu_rev), _ptr(rev), cap,
+            _ptr(totals), _ptr(ws), ws.numel(), _stream(dev)), "lsrm_reverse_query_map")
+    max_entries = int(totals.max().item()) if hkv > 0 else 0
+    max_entries = max(max_entries, 1)
+    return cu_rev, rev[:, :max_entries].contiguous()
+
+
+def block_ids(cu_seqblocks: torch.Tensor, cu_block_tokens: torch.Tensor, n_tokens: int,
+              hkv: int) -> torch.Tensor:
+    """Batch-local block id of every token, [hkv, n_tokens, 1] int32."""
+    dev = _dev_check(cu_seqblocks, cu_block_tokens)
+    ids = torch.empty(hkv, n_tokens, 1, dtype=torch.int32, device=dev)
+    if n_tokens == 0:
+        return ids
+    with torch.cuda.device(dev):
+        _check(lib().lsrm_block_ids(
+            _ptr(_i32(cu_seqblocks)), cu_seqblocks.numel() - 1, _ptr(_i32(cu_block_tokens)),
+            cu_block_tokens.numel() - 1, n_tokens, hkv, _ptr(ids), _stream(dev)),
+            "lsrm_block_ids")
+    return ids
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

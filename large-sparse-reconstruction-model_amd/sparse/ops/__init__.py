@@ -1,0 +1,26 @@
+"""gfx950 HIP replacement of LSRM's sparse/ops (same public names and
+signatures as sparse/ops/__init__.py:7-9, plus the compression and
+selection operators)."""
+
+from .block_window_attention import sparse_window_attention
+from .compression import block_mean_pool, sparse3d_compression
+from .native_sparse_attention import (
+    NSA,
+    native_sparse_attend,
+    set_validation,
+    set_variant,
+    spatial_selection_attention,
+)
+from .selection import select_blocks
+
+__all__ = [
+    "NSA",
+    "block_mean_pool",
+    "native_sparse_attend",
+    "select_blocks",
+    "set_validation",
+    "set_variant",
+    "sparse3d_compression",
+    "sparse_window_attention",
+    "spatial_selection_attention",
+]

@@ -1,0 +1,171 @@
+"""GPU parity: selected-block attention forward/backward against the fp32
+CPU oracle (north_star tolerance: max-abs 2e-2, mean-abs 2e-3), the reverse
+query map bit-exact, and the sparse.ops API surface."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import lsrm_hip as H
+from helpers import assert_attn_close, random_topk
+from lsrm_hip import workloads as W
+from oracle.attention import sel_attn_ref
+from oracle.revmap import reverse_query_map_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _run_case(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, scale, do=None):
+    """HIP forward (and backward when do is given) vs the oracle."""
+    dq_ = [t.to(DEV) for t in (q, k, v, topk_idx, cu_sb, cu_blk, cu_q)]
+    o, lse = H.sel_attn_fwd(*dq_, scale)
+    qf, kf, vf = (t.float().requires_grad_(do is not None) for t in (q, k, v))
+    o_ref, lse_ref = sel_attn_ref(qf, kf, vf, topk_idx, cu_sb, cu_blk, cu_q, scale)
+    assert_attn_close(o, o_ref, "out")
+    lse_c = lse.cpu()
+    fin = torch.isfinite(lse_ref)
+    assert torch.equal(torch.isfinite(lse_c), fin)
+    assert (lse_c[fin] - lse_ref[fin]).abs().max() <= 2e-2 if fin.any() else True
+    if do is None:
+        return o, lse
+    dq, dk, dv, delta = H.sel_attn_bwd(do.to(DEV), *dq_[:3], o, lse, *dq_[3:], scale)
+    o_ref.backward(do.float())
+    assert_attn_close(dq, qf.grad, "dq")
+    assert_attn_close(dk, kf.grad, "dk")
+    assert_attn_close(dv, vf.grad, "dv")
+    delta_ref = (o.float().cpu() * do.float()).sum(-1).transpose(0, 1)
+    torch.testing.assert_close(delta.cpu(), delta_ref, rtol=1e-4, atol=1e-4)
+    return o, lse, dq, dk, dv
+
+
+def _blocks_topk(w, topk, gen):
+    return random_topk(w.hkv, w.n, w.n_blocks, topk, gen, per_block_cu=w.cu_block_tokens)
+
+
+def test_fwd_block_selection_cfg2_small():
+    w = W.config(2, n=4096, heads=4)
+    q, k, v = W.tensors(w, "cpu")
+    gen = torch.Generator().manual_seed(11)
+    topk = _blocks_topk(w, w.topk, gen)
+    _run_case(q, k, v, topk, w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens, w.scale)
+
+
+def test_fwd_from_select_blocks_cfg3_small():
+    w = W.config(3, n=16384, heads=2)
+    q, k, v = W.tensors(w, "cpu")
+    topk_idx, _ = H.select_blocks(q.to(DEV), k.to(DEV), w.cu_seqblocks.to(DEV),
+                                  w.cu_block_tokens.to(DEV), w.topk, w.forced_blocks, True)
+    _run_case(q, k, v, topk_idx.cpu(), w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens, w.scale)
+
+
+@pytest.mark.parametrize("d,dtype", [(32, torch.bfloat16), (64, torch.float16), (128, torch.bfloat16)])
+def test_fwd_gqa_per_token_rows(d, dtype):
+    # Product shape family: Hq = 8 query heads over Hkv = 2 kv heads; every
+    # token has its own selection row (the 3D-aware maps of the reference).
+    n, hq, hkv = 1536, 8, 2
+    rng = np.random.default_rng(5)
+    sizes = W.uniform_partition(n, 8, 96, rng)
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32))
+    gen = torch.Generator().manual_seed(d)
+    q = torch.randn(n, hq, d, generator=gen).to(dtype)
+    k = torch.randn(n, hkv, d, generator=gen).to(dtype)
+    v = torch.randn(n, hkv, d, generator=gen).to(dtype)
+    topk = random_topk(hkv, n, len(sizes), 6, gen, pad_frac=0.5)
+    cu_sb = torch.tensor([0, len(sizes)], dtype=torch.int32)
+    cu_q = torch.tensor([0, n], dtype=torch.int32)
+    _run_case(q, k, v, topk, cu_sb, cu, cu_q, 1.0 / math.sqrt(d))
+
+
+def test_fwd_duplicates_empty_rows_and_batches():
+    # Two batch elements; repeated ids, -1 padding, out-of-range ids and an
+    # empty row (output 0, lse -inf).
+    n0, n1, hq, d = 700, 500, 4, 64
+    rng = np.random.default_rng(9)
+    s0 = W.uniform_partition(n0, 16, 128, rng)
+    s1 = W.uniform_partition(n1, 16, 128, rng)
+    sizes = np.concatenate([s0, s1])
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32))
+    cu_sb = torch.tensor([0, len(s0), len(sizes)], dtype=torch.int32)
+    cu_q = torch.tensor([0, n0, n0 + n1], dtype=torch.int32)
+    gen = torch.Generator().manual_seed(1)
+    q = torch.randn(n0 + n1, hq, d, generator=gen).to(torch.bfloat16)
+    k = torch.randn(n0 + n1, hq, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(n0 + n1, hq, d, generator=gen).to(torch.bfloat16)
+    topk = torch.full((hq, n0 + n1, 5), -1, dtype=torch.int32)
+    topk[:, :, 0] = 1
+    topk[:, :, 1] = 1          # duplicate counts twice
+    topk[:, :, 2] = 3
+    topk[:, 10:20, :] = -1     # empty rows
+    topk[:, n0 + 5, 0] = len(s1) + 7  # out of range for batch 1 -> ignored
+    _run_case(q, k, v, topk, cu_sb, cu, cu_q, 0.125)
+
+
+def test_bwd_cfg4_small():
+    w = W.config(4, n=4096, heads=4)
+    q, k, v, do = W.tensors(w, "cpu", with_grad_out=True)
+    gen = torch.Generator().manual_seed(4)
+    topk = _blocks_topk(w, w.topk, gen)
+    _run_case(q, k, v, topk, w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens, w.scale, do=do)
+
+
+def test_bwd_gqa_per_token_rows():
+    n, hq, hkv, d = 1024, 8, 2, 32
+    rng = np.random.default_rng(2)
+    sizes = W.uniform_partition(n, 8, 80, rng)
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32))
+    gen = torch.Generator().manual_seed(3)
+    q = torch.randn(n, hq, d, generator=gen).to(torch.bfloat16)
+    k = torch.randn(n, hkv, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(n, hkv, d, generator=gen).to(torch.bfloat16)
+    do = torch.randn(n, hq, d, generator=gen).to(torch.bfloat16)
+    topk = random_topk(hkv, n, len(sizes), 5, gen, pad_frac=0.4)
+    _run_case(q, k, v, topk, torch.tensor([0, len(sizes)], dtype=torch.int32), cu,
+              torch.tensor([0, n], dtype=torch.int32), 1.0 / math.sqrt(d), do=do)
+
+
+def test_deterministic_bitwise():
+    w = W.config(4, n=4096, heads=2)
+    q, k, v, do = (t.to(DEV) for t in W.tensors(w, "cpu", with_grad_out=True))
+    gen = torch.Generator().manual_seed(8)
+    topk = _blocks_topk(w, w.topk, gen).to(DEV)
+    meta = [t.to(DEV) for t in (w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens)]
+    runs = []
+    for _ in range(2):
+        o, lse = H.sel_attn_fwd(q, k, v, topk, *meta, w.scale)
+        dq, dk, dv, _ = H.sel_attn_bwd(do, q, k, v, o, lse, topk, *meta, w.scale)
+        runs.append([t.clone() for t in (o, lse, dq, dk, dv)])
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+
+
+def test_reverse_query_map_bitexact():
+    w = W.config(2, n=3000, heads=3)
+    gen = torch.Generator().manual_seed(6)
+    topk = random_topk(w.hkv, w.n, w.n_blocks, 7, gen, pad_frac=0.3)
+    topk[:, 5, 1] = topk[:, 5, 0]  # a duplicate
+    cu_rev, rev = H.reverse_query_map(topk.to(DEV), w.cu_seqlens.to(DEV), w.cu_seqblocks.to(DEV),
+                                      w.n_blocks)
+    ref_cu, ref_lists = reverse_query_map_ref(topk.numpy(), w.cu_seqlens.numpy(),
+                                              w.cu_seqblocks.numpy(), w.n_blocks)
+    np.testing.assert_array_equal(cu_rev.cpu().numpy(), ref_cu)
+    for h in range(w.hkv):
+        m = int(ref_cu[h, -1])
+        np.testing.assert_array_equal(rev[h, :m].cpu().numpy(), ref_lists[h])
+
+
+def test_reverse_query_map_long_segments():
+    # One block selected by every query: a segment longer than the in-LDS
+    # sort capacity exercises the windowed counting sort.
+    n, nb = 12000, 4
+    cu_q = torch.tensor([0, n], dtype=torch.int32)
+    cu_sb = torch.tensor([0, nb], dtype=torch.int32)
+    gen = torch.Generator().manual_seed(0)
+    topk = torch.zeros(1, n, 2, dtype=torch.int32)
+    topk[0, :, 1] = torch.randint(1, nb, (n,), generator=gen).to(torch.int32)
+    cu_rev, rev = H.reverse_query_map(topk.to(DEV), cu_q.to(DEV), cu_sb.to(DEV), nb)
+    ref_cu, ref_lists = reverse_query_map_ref(topk.numpy(), cu_q.numpy(), cu_sb.numpy(), nb)
+    np.testing.assert_array_equal(cu_rev.cpu().numpy(), ref_cu)
+    np.testing.assert_array_equal(rev[0, : int(ref_cu[0, -1])].cpu().numpy(), ref_lists[0])

@@ -1,0 +1,128 @@
+"""GPU parity: block mean pooling and per-query-block selection, bit-exact
+against the CPU oracle (through the C ABI via lsrm_hip)."""
+
+import numpy as np
+import pytest
+import torch
+
+import lsrm_hip as H
+from lsrm_hip import workloads as W
+from oracle.pool import block_mean_pool_ref
+from oracle.select import expand_per_token, select_blocks_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _f32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def _pool_case(n, c, dtype, out_dtype, lo=16, hi=300, seed=0):
+    rng = np.random.default_rng(seed)
+    sizes = W.uniform_partition(n, lo, hi, rng)
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32))
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n, c, generator=g).to(dtype)
+    out = H.block_mean_pool(x.to(DEV), cu.to(DEV), out_dtype)
+    ref = block_mean_pool_ref(_f32(x), cu.numpy())
+    ref_t = torch.from_numpy(ref).to(out_dtype or dtype)
+    return out.cpu(), ref_t
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("out_dtype", [None, torch.float32])
+def test_pool_bitexact(dtype, out_dtype):
+    out, ref = _pool_case(5000, 256, dtype, out_dtype)
+    assert torch.equal(out.view(torch.int16 if out.element_size() == 2 else torch.int32),
+                       ref.view(torch.int16 if ref.element_size() == 2 else torch.int32))
+
+
+def test_pool_scalar_path_and_long_blocks():
+    # C not a multiple of 8 -> scalar path; blocks longer than several pieces.
+    out, ref = _pool_case(3001, 12, torch.bfloat16, torch.float32, lo=100, hi=1000, seed=3)
+    assert torch.equal(out, ref)
+
+
+def test_pool_cfg3_shape_bitexact():
+    w = W.config(3)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    x = (0.5 * torch.randn(w.n, w.hkv * w.d, generator=g, device=DEV)).to(torch.bfloat16)
+    out = H.block_mean_pool(x, w.cu_block_tokens.to(DEV))
+    ref = block_mean_pool_ref(_f32(x), w.cu_block_tokens.numpy())
+    ref = torch.from_numpy(ref).to(torch.bfloat16)
+    assert torch.equal(out.cpu().view(torch.int16), ref.view(torch.int16))
+
+
+def test_pool_matches_segment_reduce_and_empty_block():
+    cu = torch.tensor([0, 5, 5, 70, 200], dtype=torch.int32)
+    x = torch.randn(200, 64)
+    out = H.block_mean_pool(x.to(DEV), cu.to(DEV)).cpu()
+    ref = torch.segment_reduce(x, "mean", lengths=(cu[1:] - cu[:-1]).long(), axis=0)
+    assert torch.isnan(out[1]).all() and torch.isnan(ref[1]).all()
+    keep = torch.tensor([0, 2, 3])
+    torch.testing.assert_close(out[keep], ref[keep], rtol=1e-6, atol=1e-6)
+
+
+def _select_case(w, forced=None, hq=None, hkv=None, dtype=None):
+    dtype = dtype or w.dtype
+    g = torch.Generator().manual_seed(w.seed)
+    hq = hq or w.hq
+    hkv = hkv or w.hkv
+    q = torch.randn(w.n, hq, w.d, generator=g).to(dtype)
+    k = torch.randn(w.n, hkv, w.d, generator=g).to(dtype)
+    if w.lowrank:
+        u = torch.randn(w.n, 4, generator=g)
+        q = (0.95 * q.float() + 0.3 * (u @ torch.randn(4, hq * w.d, generator=g)).view(q.shape)).to(dtype)
+        k = (0.95 * k.float() + 0.3 * (u @ torch.randn(4, hkv * w.d, generator=g)).view(k.shape)).to(dtype)
+    forced = w.forced_blocks if forced is None else forced
+    topk_idx, compact = H.select_blocks(q.to(DEV), k.to(DEV), w.cu_seqblocks.to(DEV),
+                                        w.cu_block_tokens.to(DEV), w.topk, forced, w.force_self)
+    cu = w.cu_block_tokens.numpy()
+    pq = block_mean_pool_ref(_f32(q).reshape(w.n, -1), cu).reshape(-1, hq, w.d)
+    pk = block_mean_pool_ref(_f32(k).reshape(w.n, -1), cu).reshape(-1, hkv, w.d)
+    ref = select_blocks_ref(pq, pk, w.cu_seqblocks.numpy(), w.topk, forced, w.force_self)
+    return topk_idx.cpu().numpy(), compact.cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("cfg,n,heads", [(1, None, None), (2, 8192, 4), (3, 16384, 4), (5, 65536, 4)])
+def test_select_bitexact(cfg, n, heads):
+    w = W.config(cfg, n=n, heads=heads)
+    topk_idx, compact, ref = _select_case(w)
+    np.testing.assert_array_equal(compact, ref)
+    np.testing.assert_array_equal(topk_idx, expand_per_token(ref, w.cu_block_tokens.numpy(), w.n))
+    # forced blocks are always selected
+    for f in w.forced_blocks:
+        assert (compact == f).any(-1).all()
+    # self block is always selected
+    nb = w.n_blocks
+    assert (compact == np.arange(nb)[None, :, None]).any(-1).all()
+
+
+def test_select_gqa_bitexact():
+    w = W.config(2, n=4096)
+    topk_idx, compact, ref = _select_case(w, hq=8, hkv=2)
+    np.testing.assert_array_equal(compact, ref)
+
+
+def test_select_topk_ge_blocks_selects_all():
+    w = W.config(1, n=600, heads=2)
+    w.topk = w.n_blocks + 3
+    _, compact, ref = _select_case(w)
+    np.testing.assert_array_equal(compact, ref)
+    assert (compact[..., : w.n_blocks] == np.arange(w.n_blocks)).all()
+    assert (compact[..., w.n_blocks:] == -1).all()
+
+
+def test_select_ties_lowest_index():
+    # Every block has the same pooled key -> all scores tie -> lowest ids win.
+    n, d = 640, 64
+    cu = torch.arange(0, n + 1, 64, dtype=torch.int32)
+    q = torch.randn(n, 2, d).to(torch.bfloat16)
+    k = torch.ones(n, 2, d, dtype=torch.bfloat16)
+    _, compact = H.select_blocks(q.to(DEV), k.to(DEV), torch.tensor([0, 10], dtype=torch.int32, device=DEV),
+                                 cu.to(DEV), 3, None, True)
+    compact = compact.cpu()
+    for b in range(10):
+        expect = sorted(set([b] + [x for x in range(10) if x != b][:2]))
+        assert compact[:, b].tolist() == [expect, expect]
