@@ -1,0 +1,219 @@
+#!/usr/bin/env python3
+"""One sparse-attention decoder layer on one MI355X.
+
+A step is one layer over synthetic, HBM-resident inputs (B=1, N=131072
+tokens: 8 image blocks of 1024 + 122880 Morton-ordered voxel tokens in runs of
+32-512, H=24, D=64, bf16, top-16 with the image blocks and the own block
+forced):
+  1. key and value block compression (lsrm_block_mean_pool, x2),
+  2. per-query-block selection (pool Q/K in fp32, fp64 scores, top-k),
+  3. selected-block attention forward (device plan + MFMA kernel).
+`value` is the layer's effective TFLOP/s on the attended FLOPs
+(4 * D * sum over heads and queries of the attended key count).  The
+roofline object describes the attention forward kernel alone, timed with HIP
+events on the stream it is launched on.  cpu_baseline times the CPU oracle
+(PyTorch fp32) on a bounded sample of the same workload on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "large-sparse-reconstruction-model_amd"))
+sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+import lsrm_hip as H  # noqa: E402
+from lsrm_hip import workloads as W  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def event_time_ms(fn, reps: int) -> float:
+    """Average ms per call of fn() measured with HIP events on torch's
+    current stream (the stream every lsrm_hip call launches on)."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(w, q, k, v, topk_idx, flops_per_head_q, budget_s: float):
+    """Times the CPU oracle head by head until the budget is spent."""
+    from oracle.attention import sel_attn_ref  # the checker, timed as the CPU baseline
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    cu_sb, cu_blk, cu_q = w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens
+    heads, flops, elapsed = 0, 0.0, 0.0
+    g = w.hq // w.hkv
+    for h in range(w.hkv):
+        qh = q[:, h * g:(h + 1) * g].float().cpu()
+        kh = k[:, h:h + 1].float().cpu()
+        vh = v[:, h:h + 1].float().cpu()
+        th = topk_idx[h:h + 1].cpu()
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            sel_attn_ref(qh, kh, vh, th, cu_sb, cu_blk, cu_q, w.scale)
+        elapsed += time.perf_counter() - t0
+        flops += flops_per_head_q[h]
+        heads += 1
+        if elapsed >= budget_s:
+            break
+    tflops = flops / elapsed / 1e12
+    total_flops = sum(flops_per_head_q)
+    return {
+        "value": round(tflops, 5),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"{w.name}: attention forward of kv heads 0..{heads - 1} of {w.hkv} "
+                   f"(all {w.n} queries, same selection) with the fp32 PyTorch oracle, "
+                   f"{elapsed:.1f} s; extrapolated full-layer attention "
+                   f"{total_flops / (tflops * 1e12) * 1e3:.0f} ms"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 5])
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--cpu-budget", type=float, default=15.0,
+                    help="seconds of CPU oracle time for cpu_baseline (0 = skip)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the layer "
+              "shards by kv head with no exchange); run with --gpus 1", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = W.config(args.config)
+    q, k, v = W.tensors(w, dev)
+    cu_blk = w.cu_block_tokens.to(dev)
+    cu_sb = w.cu_seqblocks.to(dev)
+    cu_q = w.cu_seqlens.to(dev)
+    n, hq, hkv, d = w.n, w.hq, w.hkv, w.d
+    k2 = k.view(n, hkv * d)
+    v2 = v.view(n, hkv * d)
+
+    def layer():
+        ck = H.block_mean_pool(k2, cu_blk)
+        cv = H.block_mean_pool(v2, cu_blk)
+        topk_idx, compact = H.select_blocks(q, k, cu_sb, cu_blk, w.topk, w.forced_blocks, True)
+        o, lse = H.sel_attn_fwd(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, w.scale)
+        return ck, cv, topk_idx, compact, o, lse
+
+    # Work count from the actual selection.
+    _, _, topk_idx, compact, _, _ = layer()
+    torch.cuda.synchronize()
+    g = hq // hkv
+    per_head = []
+    cu_cpu = w.cu_block_tokens.long()
+    lens = cu_cpu[1:] - cu_cpu[:-1]
+    comp = compact.cpu().long()
+    valid = comp >= 0
+    att_per_block = torch.where(valid, lens[comp.clamp(min=0)], torch.zeros_like(comp)).sum(-1)
+    for h in range(hkv):
+        per_head.append(4.0 * d * g * float((att_per_block[h] * lens).sum()))
+    flops = sum(per_head)
+
+    for _ in range(args.warmup):
+        layer()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        layer()
+    torch.cuda.synchronize()
+    ms_layer = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # Per-kernel times (HIP events on the launch stream).
+    reps = args.kernel_reps
+    plan = H.SelAttnPlan(q.shape, k.shape, topk_idx, cu_sb, cu_blk, cu_q)
+    out = torch.empty_like(q)
+    lse = torch.empty(hq, n, dtype=torch.float32, device=dev)
+    plan.fwd(q, k, v, w.scale, out, lse)
+    ms_attn = event_time_ms(lambda: plan.fwd(q, k, v, w.scale, out, lse), reps)
+    ms_plan = event_time_ms(
+        lambda: H.SelAttnPlan(q.shape, k.shape, topk_idx, cu_sb, cu_blk, cu_q), reps)
+    ms_pool = event_time_ms(lambda: H.block_mean_pool(k2, cu_blk), reps)
+    ms_select = event_time_ms(
+        lambda: H.select_blocks(q, k, cu_sb, cu_blk, w.topk, w.forced_blocks, True), reps)
+    nb = w.n_blocks
+    pool_bytes = n * hkv * d * 2 + nb * hkv * d * 2 + 4 * (nb + 1)
+    attn_tflops = flops / (ms_attn * 1e-3) / 1e12
+    pool_gbs = pool_bytes / (ms_pool * 1e-3) / 1e9
+
+    result = {
+        "metric": "sparse-attn ms/layer + effective TFLOP/s @131K tok, H24 D64; % MFMA/HBM peak",
+        "value": round(flops / (ms_layer * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_layer, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded Q/K/V ~ 0.5 N(0,1), block metadata per the config)",
+        "config": {
+            "workload": f"{w.name}: sparse-attention layer (K/V compression + block "
+                        f"selection + selected attention fwd)",
+            "tokens": n, "heads_q": hq, "heads_kv": hkv, "head_dim": d, "topk": w.topk,
+            "blocks": nb, "forced_blocks": len(w.forced_blocks),
+            "attended_fwd_flops": flops,
+        },
+        "ms_per_layer": round(ms_layer, 4),
+        "kernels": {
+            "attn_fwd": {"ms": round(ms_attn, 4), "tflops": round(attn_tflops, 2),
+                         "frac_bf16_peak": round(attn_tflops / PEAK_BF16_TFLOPS, 4)},
+            "attn_plan": {"ms": round(ms_plan, 4)},
+            "pool_k": {"ms": round(ms_pool, 4), "bytes": pool_bytes,
+                       "gbs": round(pool_gbs, 1),
+                       "frac_hbm_peak": round(pool_gbs / PEAK_HBM_GBS, 4)},
+            "select": {"ms": round(ms_select, 4)},
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(attn_tflops, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+    }
+    if args.cpu_budget > 0:
+        result["cpu_baseline"] = cpu_baseline(w, q, k, v, topk_idx, per_head, args.cpu_budget)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

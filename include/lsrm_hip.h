@@ -158,6 +158,36 @@ int lsrm_sel_attn_fwd(const void* q, const void* k, const void* v, int dtype,
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Split form of the two calls above and below, for callers that reuse one
+ * selection across launches (timing loops, activation-checkpoint recompute,
+ * forward followed by backward on the same top-k).  lsrm_sel_attn_plan
+ * builds the device plan (query tiles; with backward != 0 also the reverse
+ * map and key chunks) in the workspace; the *_run variants take the same
+ * arguments as lsrm_sel_attn_fwd / lsrm_sel_attn_bwd, expect that workspace
+ * (same sizes, same topk_idx and metadata) and launch only the attention
+ * kernels.  The plan's work queues reset themselves at the end of each
+ * launch, so a plan can be replayed any number of times on one stream.
+ * lsrm_sel_attn_fwd == lsrm_sel_attn_plan + lsrm_sel_attn_fwd_run.
+ * ---------------------------------------------------------------------- */
+int lsrm_sel_attn_plan(const int32_t* topk_idx, int64_t n_q, int64_t n_k,
+                       int64_t hq, int64_t hkv, int64_t topk,
+                       const int32_t* cu_seqblocks,
+                       const int32_t* cu_block_tokens, int64_t n_blocks,
+                       const int32_t* cu_seqlens_q, int64_t batch,
+                       int backward, void* workspace, size_t workspace_bytes,
+                       void* stream);
+int lsrm_sel_attn_fwd_run(const void* q, const void* k, const void* v,
+                          int dtype, int64_t n_q, int64_t n_k, int64_t hq,
+                          int64_t hkv, int64_t head_dim,
+                          const int32_t* topk_idx, int64_t topk,
+                          const int32_t* cu_seqblocks,
+                          const int32_t* cu_block_tokens, int64_t n_blocks,
+                          const int32_t* cu_seqlens_q, int64_t batch,
+                          float softmax_scale, void* out, float* lse,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* ------------------------------------------------------------------------
  * Selected-block attention, backward.  Inputs as for the forward plus
  * dout [n_q, hq, head_dim] and the forward's out and lse.  Writes
  * dq [n_q, hq, head_dim], dk/dv [n_k, hkv, head_dim] (dtype) and
@@ -177,6 +207,17 @@ int lsrm_sel_attn_bwd(const void* dout, const void* q, const void* k,
                       float softmax_scale, void* dq, void* dk, void* dv,
                       float* delta, void* workspace, size_t workspace_bytes,
                       void* stream);
+int lsrm_sel_attn_bwd_run(const void* dout, const void* q, const void* k,
+                          const void* v, const void* out, const float* lse,
+                          int dtype, int64_t n_q, int64_t n_k, int64_t hq,
+                          int64_t hkv, int64_t head_dim,
+                          const int32_t* topk_idx, int64_t topk,
+                          const int32_t* cu_seqblocks,
+                          const int32_t* cu_block_tokens, int64_t n_blocks,
+                          const int32_t* cu_seqlens_q, int64_t batch,
+                          float softmax_scale, void* dq, void* dk, void* dv,
+                          float* delta, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Reverse (CSR) query map of a top-k selection: for each kv head h and

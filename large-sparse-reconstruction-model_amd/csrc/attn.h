@@ -158,6 +158,19 @@ __device__ inline int fetch_work(int32_t* counter, int* s_slot) {
   return *s_slot;
 }
 
+// Called by every workgroup once it has drained the queue `work`: the last
+// one to leave resets the queue and the exit count `exits`, so the plan can
+// be replayed by later launches without a host-side memset.
+__device__ inline void leave_queue(int32_t* work, int32_t* exits) {
+  if (threadIdx.x == 0) {
+    __threadfence();
+    if (atomicAdd(exits, 1) == (int)(gridDim.x * gridDim.y * gridDim.z) - 1) {
+      atomicExch(work, 0);
+      atomicExch(exits, 0);
+    }
+  }
+}
+
 // Kv head owning global tile index w (head_off ascending, hkv small).
 __device__ inline int head_of(const int32_t* head_off, int hkv, int w) {
   int h = 0;

@@ -192,6 +192,7 @@ __global__ __launch_bounds__(256) void sel_attn_dq_kernel(AttnArgs a) {
         }
     }
   }
+  leave_queue(a.plan.counter, a.plan.counter + 2);
 }
 
 // ----------------------------------------------------------------- dK/dV --
@@ -407,6 +408,7 @@ __global__ __launch_bounds__(256) void sel_attn_dkdv_kernel(AttnArgs a) {
     }
     __syncthreads();
   }
+  leave_queue(a.plan.counter + 1, a.plan.counter + 3);
 }
 
 template <int DT, int D>

@@ -202,6 +202,7 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
             l_tot > 0.0f ? m_run + log2f(l_tot) : -__builtin_inf();
     }
   }
+  leave_queue(a.plan.counter, a.plan.counter + 2);
 }
 
 template <int DT, int D>

@@ -128,98 +128,51 @@ extern "C" size_t lsrm_sel_attn_workspace_size(int64_t n_q, int64_t n_k,
   return ws.used + 256;
 }
 
-extern "C" int lsrm_sel_attn_fwd(
-    const void* q, const void* k, const void* v, int dtype, int64_t n_q,
-    int64_t n_k, int64_t hq, int64_t hkv, int64_t head_dim,
-    const int32_t* topk_idx, int64_t topk, const int32_t* cu_seqblocks,
-    const int32_t* cu_block_tokens, int64_t n_blocks,
-    const int32_t* cu_seqlens_q, int64_t batch, float softmax_scale, void* out,
-    float* lse, void* workspace, size_t workspace_bytes, void* stream) {
-  int rc = check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk, n_blocks,
-                           batch);
-  if (rc) return rc;
-  if (n_q == 0) return LSRM_OK;
-  if (!q || !k || !v || !out || !lse || !topk_idx || !cu_seqblocks ||
-      !cu_block_tokens || !cu_seqlens_q || !aligned16(q) || !aligned16(k) ||
-      !aligned16(v) || !aligned16(out) || !(softmax_scale > 0.0f))
-    return LSRM_ERR_INVALID_ARG;
-  const size_t need =
-      lsrm_sel_attn_workspace_size(n_q, n_k, hq, hkv, topk, n_blocks, 0);
-  if (workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
-  hipStream_t st = (hipStream_t)stream;
-  Carver ws{reinterpret_cast<char*>(align_up((size_t)workspace, 256)), 0,
-            workspace_bytes - 256};
-  const int g = (int)(hq / hkv);
-  AttnWs w{};
-  rc = attn_plan(ws, topk_idx, n_q, n_k, hkv, topk, cu_seqblocks,
-                 cu_block_tokens, n_blocks, cu_seqlens_q, batch, g, false, w,
-                 st);
-  if (rc) return rc;
-  AttnArgs a{};
-  a.q = static_cast<const uint16_t*>(q);
-  a.k = static_cast<const uint16_t*>(k);
-  a.v = static_cast<const uint16_t*>(v);
-  a.out = static_cast<uint16_t*>(out);
-  a.lse = lse;
-  a.topk = topk_idx;
-  a.cu_sb = cu_seqblocks;
-  a.cu_blk = cu_block_tokens;
-  a.cu_q = cu_seqlens_q;
-  a.nb = n_blocks;
-  a.batch = batch;
-  a.nq = n_q;
-  a.nk = n_k;
-  a.topk_n = (int)topk;
-  a.hq = (int)hq;
-  a.hkv = (int)hkv;
-  a.g = g;
-  a.scale = softmax_scale;
-  a.scale_log2 = softmax_scale * 1.44269504f;  // as the reference (kvcentric:125)
-  a.plan = w.plan;
-  return launch_fwd(dtype, (int)head_dim, a, st);
-}
+namespace {
 
-extern "C" int lsrm_sel_attn_bwd(
-    const void* dout, const void* q, const void* k, const void* v,
-    const void* out, const float* lse, int dtype, int64_t n_q, int64_t n_k,
-    int64_t hq, int64_t hkv, int64_t head_dim, const int32_t* topk_idx,
-    int64_t topk, const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
-    int64_t n_blocks, const int32_t* cu_seqlens_q, int64_t batch,
-    float softmax_scale, void* dq, void* dk, void* dv, float* delta,
-    void* workspace, size_t workspace_bytes, void* stream) {
+// Validates the arguments shared by every attention entry point and fills
+// AttnArgs; `plan` builds the device plan, otherwise the workspace must
+// already hold the plan lsrm_sel_attn_plan built for the same inputs.
+int attn_setup(const void* q, const void* k, const void* v, int dtype,
+               int64_t n_q, int64_t n_k, int64_t hq, int64_t hkv,
+               int64_t head_dim, const int32_t* topk_idx, int64_t topk,
+               const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
+               int64_t n_blocks, const int32_t* cu_seqlens_q, int64_t batch,
+               float softmax_scale, bool backward, bool plan,
+               void* workspace, size_t workspace_bytes, hipStream_t st,
+               AttnArgs& a) {
   int rc = check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk, n_blocks,
                            batch);
   if (rc) return rc;
-  if (n_q == 0) return LSRM_OK;
-  if (!dout || !q || !k || !v || !out || !lse || !dq || !dk || !dv || !delta ||
-      !topk_idx || !cu_seqblocks || !cu_block_tokens || !cu_seqlens_q ||
-      !aligned16(dout) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
-      !aligned16(out) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
+  if (!q || !k || !v || !topk_idx || !cu_seqblocks || !cu_block_tokens ||
+      !cu_seqlens_q || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
       !(softmax_scale > 0.0f))
     return LSRM_ERR_INVALID_ARG;
-  const size_t need =
-      lsrm_sel_attn_workspace_size(n_q, n_k, hq, hkv, topk, n_blocks, 1);
+  const size_t need = lsrm_sel_attn_workspace_size(n_q, n_k, hq, hkv, topk,
+                                                   n_blocks, backward ? 1 : 0);
   if (workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
-  hipStream_t st = (hipStream_t)stream;
   Carver ws{reinterpret_cast<char*>(align_up((size_t)workspace, 256)), 0,
             workspace_bytes - 256};
   const int g = (int)(hq / hkv);
   AttnWs w{};
-  rc = attn_plan(ws, topk_idx, n_q, n_k, hkv, topk, cu_seqblocks,
-                 cu_block_tokens, n_blocks, cu_seqlens_q, batch, g, true, w,
-                 st);
-  if (rc) return rc;
-  AttnArgs a{};
+  if (plan) {
+    rc = attn_plan(ws, topk_idx, n_q, n_k, hkv, topk, cu_seqblocks,
+                   cu_block_tokens, n_blocks, cu_seqlens_q, batch, g, backward,
+                   w, st);
+    if (rc) return rc;
+  } else {
+    // Same carving, no launches: recover the plan built earlier.
+    Carver dry{ws.base, 0, ws.cap, true};
+    rc = attn_plan(dry, topk_idx, n_q, n_k, hkv, topk, cu_seqblocks,
+                   cu_block_tokens, n_blocks, cu_seqlens_q, batch, g, backward,
+                   w, st);
+    if (rc) return rc;
+    if (!dry.ok()) return LSRM_ERR_WORKSPACE;
+  }
+  a = AttnArgs{};
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);
-  a.o = static_cast<const uint16_t*>(out);
-  a.dout = static_cast<const uint16_t*>(dout);
-  a.lse_in = lse;
-  a.out = static_cast<uint16_t*>(dq);
-  a.lse = delta;
-  a.dk = static_cast<uint16_t*>(dk);
-  a.dv = static_cast<uint16_t*>(dv);
   a.topk = topk_idx;
   a.cu_sb = cu_seqblocks;
   a.cu_blk = cu_block_tokens;
@@ -237,5 +190,141 @@ extern "C" int lsrm_sel_attn_bwd(
   a.plan = w.plan;
   a.rev = w.rev;
   a.items = w.items;
+  return LSRM_OK;
+}
+
+}  // namespace
+
+extern "C" int lsrm_sel_attn_plan(
+    const int32_t* topk_idx, int64_t n_q, int64_t n_k, int64_t hq, int64_t hkv,
+    int64_t topk, const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
+    int64_t n_blocks, const int32_t* cu_seqlens_q, int64_t batch, int backward,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_attn_args(LSRM_BF16, n_q, n_k, hq, hkv, 64, topk, n_blocks,
+                           batch);
+  if (rc) return rc;
+  if (n_q == 0) return LSRM_OK;
+  if (!topk_idx || !cu_seqblocks || !cu_block_tokens || !cu_seqlens_q)
+    return LSRM_ERR_INVALID_ARG;
+  const size_t need = lsrm_sel_attn_workspace_size(n_q, n_k, hq, hkv, topk,
+                                                   n_blocks, backward ? 1 : 0);
+  if (workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
+  Carver ws{reinterpret_cast<char*>(align_up((size_t)workspace, 256)), 0,
+            workspace_bytes - 256};
+  AttnWs w{};
+  return attn_plan(ws, topk_idx, n_q, n_k, hkv, topk, cu_seqblocks,
+                   cu_block_tokens, n_blocks, cu_seqlens_q, batch,
+                   (int)(hq / hkv), backward != 0, w, (hipStream_t)stream);
+}
+
+static int fwd_impl(const void* q, const void* k, const void* v, int dtype,
+                    int64_t n_q, int64_t n_k, int64_t hq, int64_t hkv,
+                    int64_t head_dim, const int32_t* topk_idx, int64_t topk,
+                    const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
+                    int64_t n_blocks, const int32_t* cu_seqlens_q,
+                    int64_t batch, float softmax_scale, void* out, float* lse,
+                    void* workspace, size_t workspace_bytes, void* stream,
+                    bool plan) {
+  if (n_q == 0)
+    return check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk, n_blocks,
+                           batch);
+  if (!out || !lse || !aligned16(out)) return LSRM_ERR_INVALID_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  AttnArgs a;
+  int rc = attn_setup(q, k, v, dtype, n_q, n_k, hq, hkv, head_dim, topk_idx,
+                      topk, cu_seqblocks, cu_block_tokens, n_blocks,
+                      cu_seqlens_q, batch, softmax_scale, false, plan,
+                      workspace, workspace_bytes, st, a);
+  if (rc) return rc;
+  a.out = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  return launch_fwd(dtype, (int)head_dim, a, st);
+}
+
+extern "C" int lsrm_sel_attn_fwd(
+    const void* q, const void* k, const void* v, int dtype, int64_t n_q,
+    int64_t n_k, int64_t hq, int64_t hkv, int64_t head_dim,
+    const int32_t* topk_idx, int64_t topk, const int32_t* cu_seqblocks,
+    const int32_t* cu_block_tokens, int64_t n_blocks,
+    const int32_t* cu_seqlens_q, int64_t batch, float softmax_scale, void* out,
+    float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  return fwd_impl(q, k, v, dtype, n_q, n_k, hq, hkv, head_dim, topk_idx, topk,
+                  cu_seqblocks, cu_block_tokens, n_blocks, cu_seqlens_q, batch,
+                  softmax_scale, out, lse, workspace, workspace_bytes, stream,
+                  true);
+}
+
+extern "C" int lsrm_sel_attn_fwd_run(
+    const void* q, const void* k, const void* v, int dtype, int64_t n_q,
+    int64_t n_k, int64_t hq, int64_t hkv, int64_t head_dim,
+    const int32_t* topk_idx, int64_t topk, const int32_t* cu_seqblocks,
+    const int32_t* cu_block_tokens, int64_t n_blocks,
+    const int32_t* cu_seqlens_q, int64_t batch, float softmax_scale, void* out,
+    float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  return fwd_impl(q, k, v, dtype, n_q, n_k, hq, hkv, head_dim, topk_idx, topk,
+                  cu_seqblocks, cu_block_tokens, n_blocks, cu_seqlens_q, batch,
+                  softmax_scale, out, lse, workspace, workspace_bytes, stream,
+                  false);
+}
+
+static int bwd_impl(const void* dout, const void* q, const void* k,
+                    const void* v, const void* out, const float* lse,
+                    int dtype, int64_t n_q, int64_t n_k, int64_t hq,
+                    int64_t hkv, int64_t head_dim, const int32_t* topk_idx,
+                    int64_t topk, const int32_t* cu_seqblocks,
+                    const int32_t* cu_block_tokens, int64_t n_blocks,
+                    const int32_t* cu_seqlens_q, int64_t batch,
+                    float softmax_scale, void* dq, void* dk, void* dv,
+                    float* delta, void* workspace, size_t workspace_bytes,
+                    void* stream, bool plan) {
+  if (n_q == 0)
+    return check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk, n_blocks,
+                           batch);
+  if (!dout || !out || !lse || !dq || !dk || !dv || !delta ||
+      !aligned16(dout) || !aligned16(out) || !aligned16(dq) || !aligned16(dk) ||
+      !aligned16(dv))
+    return LSRM_ERR_INVALID_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  AttnArgs a;
+  int rc = attn_setup(q, k, v, dtype, n_q, n_k, hq, hkv, head_dim, topk_idx,
+                      topk, cu_seqblocks, cu_block_tokens, n_blocks,
+                      cu_seqlens_q, batch, softmax_scale, true, plan,
+                      workspace, workspace_bytes, st, a);
+  if (rc) return rc;
+  a.o = static_cast<const uint16_t*>(out);
+  a.dout = static_cast<const uint16_t*>(dout);
+  a.lse_in = lse;
+  a.out = static_cast<uint16_t*>(dq);
+  a.lse = delta;
+  a.dk = static_cast<uint16_t*>(dk);
+  a.dv = static_cast<uint16_t*>(dv);
   return launch_bwd(dtype, (int)head_dim, a, st);
+}
+
+extern "C" int lsrm_sel_attn_bwd(
+    const void* dout, const void* q, const void* k, const void* v,
+    const void* out, const float* lse, int dtype, int64_t n_q, int64_t n_k,
+    int64_t hq, int64_t hkv, int64_t head_dim, const int32_t* topk_idx,
+    int64_t topk, const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
+    int64_t n_blocks, const int32_t* cu_seqlens_q, int64_t batch,
+    float softmax_scale, void* dq, void* dk, void* dv, float* delta,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  return bwd_impl(dout, q, k, v, out, lse, dtype, n_q, n_k, hq, hkv, head_dim,
+                  topk_idx, topk, cu_seqblocks, cu_block_tokens, n_blocks,
+                  cu_seqlens_q, batch, softmax_scale, dq, dk, dv, delta,
+                  workspace, workspace_bytes, stream, true);
+}
+
+extern "C" int lsrm_sel_attn_bwd_run(
+    const void* dout, const void* q, const void* k, const void* v,
+    const void* out, const float* lse, int dtype, int64_t n_q, int64_t n_k,
+    int64_t hq, int64_t hkv, int64_t head_dim, const int32_t* topk_idx,
+    int64_t topk, const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
+    int64_t n_blocks, const int32_t* cu_seqlens_q, int64_t batch,
+    float softmax_scale, void* dq, void* dk, void* dv, float* delta,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  return bwd_impl(dout, q, k, v, out, lse, dtype, n_q, n_k, hq, hkv, head_dim,
+                  topk_idx, topk, cu_seqblocks, cu_block_tokens, n_blocks,
+                  cu_seqlens_q, batch, softmax_scale, dq, dk, dv, delta,
+                  workspace, workspace_bytes, stream, false);
 }

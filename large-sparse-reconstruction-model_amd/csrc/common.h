@@ -139,6 +139,7 @@ struct Carver {
   char* base;
   size_t used;
   size_t cap;
+  bool dry = false;  // carve real pointers but launch nothing
   template <typename T>
   T* take(size_t count) {
     used = align_up(used, 256);

@@ -238,6 +238,8 @@ __global__ void head_offsets_kernel(const int32_t* counts, int hkv,
     }
     counter[0] = 0;
     counter[1] = 0;
+    counter[2] = 0;
+    counter[3] = 0;
   }
 }
 
@@ -253,7 +255,7 @@ int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
   plan.tile_count = ws.take<int32_t>((size_t)hkv);
   plan.head_off = ws.take<int32_t>((size_t)(hkv + 1));
   plan.counter = ws.take<int32_t>(64);
-  if (!ws.base) return LSRM_OK;
+  if (!ws.base || ws.dry) return LSRM_OK;
   if (!ws.ok()) return LSRM_ERR_WORKSPACE;
 
   if (nq > 0) {
@@ -451,7 +453,7 @@ int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
   if (!map.cu_rev) map.cu_rev = ws.take<int32_t>((size_t)(hkv * (nb + 1)));
   if (!map.rev) map.rev = ws.take<int32_t>((size_t)(hkv * (map.cap > 0 ? map.cap : 1)));
   if (!map.totals) map.totals = ws.take<int32_t>((size_t)hkv);
-  if (!ws.base) return LSRM_OK;
+  if (!ws.base || ws.dry) return LSRM_OK;
   if (!ws.ok()) return LSRM_ERR_WORKSPACE;
 
   RowSrc rows{rows_are_tiles ? plan->tiles : nullptr,
@@ -524,7 +526,7 @@ int build_key_items(const int32_t* cu_blk, int64_t nb, int64_t nk, Carver& ws,
   ki.items = ws.take<int4>((size_t)cap);
   ki.n_items = ws.take<int32_t>(64);
   int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, 1));
-  if (!ws.base) return LSRM_OK;
+  if (!ws.base || ws.dry) return LSRM_OK;
   if (!ws.ok()) return LSRM_ERR_WORKSPACE;
   int rc = launch_zero_i32(ki.n_items, 1, st);
   if (rc) return rc;

@@ -63,6 +63,18 @@ _SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P,
          _I64, _P, _I64, _F, _P, _P, _P, _P, _P, _SZ, _P],
     ),
+    "lsrm_sel_attn_plan": (
+        _I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I, _P, _SZ, _P]),
+    "lsrm_sel_attn_fwd_run": (
+        _I,
+        [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P,
+         _I64, _F, _P, _P, _P, _SZ, _P],
+    ),
+    "lsrm_sel_attn_bwd_run": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P,
+         _I64, _P, _I64, _F, _P, _P, _P, _P, _P, _SZ, _P],
+    ),
     "lsrm_reverse_query_map_workspace_size": (_SZ, [_I64, _I64, _I64, _I64]),
     "lsrm_reverse_query_map": (
         _I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _SZ, _P]),
@@ -285,6 +297,66 @@ def sel_attn_bwd(do, q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens,
             float(softmax_scale), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta),
             _ptr(ws), ws.numel(), _stream(dev)), "lsrm_sel_attn_bwd")
     return dq, dk, dv, delta
+
+
+class SelAttnPlan:
+    """Device plan of one selection (lsrm_sel_attn_plan), replayable by
+    fwd()/bwd() any number of times on the current stream.  The tensors given
+    here must stay alive and unchanged while the plan is used."""
+
+    def __init__(self, q_shape, k_shape, topk_idx, cu_seqblocks, cu_block_tokens,
+                 cu_seqlens_q, backward: bool = False):
+        dev = _dev_check(topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q)
+        self.dev = dev
+        self.nq, self.hq, self.d = q_shape
+        self.nk, self.hkv = k_shape[0], k_shape[1]
+        self.topk_idx = topk_idx
+        self.cu_seqblocks = cu_seqblocks
+        self.cu_block_tokens = cu_block_tokens
+        self.cu_seqlens_q = cu_seqlens_q
+        self.topk = topk_idx.shape[-1]
+        self.nb = cu_block_tokens.numel() - 1
+        self.batch = cu_seqlens_q.numel() - 1
+        self.backward = backward
+        with torch.cuda.device(dev):
+            n = lib().lsrm_sel_attn_workspace_size(self.nq, self.nk, self.hq, self.hkv,
+                                                   self.topk, self.nb, int(backward))
+            self.ws = _workspace(n, dev)
+            _check(lib().lsrm_sel_attn_plan(
+                _ptr(topk_idx), self.nq, self.nk, self.hq, self.hkv, self.topk,
+                _ptr(cu_seqblocks), _ptr(cu_block_tokens), self.nb, _ptr(cu_seqlens_q),
+                self.batch, int(backward), _ptr(self.ws), self.ws.numel(), _stream(dev)),
+                "lsrm_sel_attn_plan")
+
+    def fwd(self, q, k, v, softmax_scale: float, out=None, lse=None):
+        out = torch.empty_like(q) if out is None else out
+        lse = torch.empty(self.hq, self.nq, dtype=torch.float32, device=self.dev) \
+            if lse is None else lse
+        with torch.cuda.device(self.dev):
+            _check(lib().lsrm_sel_attn_fwd_run(
+                _ptr(q), _ptr(k), _ptr(v), _DTYPE_CODE[q.dtype], self.nq, self.nk, self.hq,
+                self.hkv, self.d, _ptr(self.topk_idx), self.topk, _ptr(self.cu_seqblocks),
+                _ptr(self.cu_block_tokens), self.nb, _ptr(self.cu_seqlens_q), self.batch,
+                float(softmax_scale), _ptr(out), _ptr(lse), _ptr(self.ws), self.ws.numel(),
+                _stream(self.dev)), "lsrm_sel_attn_fwd_run")
+        return out, lse
+
+    def bwd(self, do, q, k, v, o, lse, softmax_scale: float):
+        if not self.backward:
+            raise RuntimeError("plan was built without backward=True")
+        dq = torch.empty_like(q)
+        dk = torch.zeros_like(k)
+        dv = torch.zeros_like(v)
+        delta = torch.empty(self.hq, self.nq, dtype=torch.float32, device=self.dev)
+        with torch.cuda.device(self.dev):
+            _check(lib().lsrm_sel_attn_bwd_run(
+                _ptr(do), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _DTYPE_CODE[q.dtype],
+                self.nq, self.nk, self.hq, self.hkv, self.d, _ptr(self.topk_idx), self.topk,
+                _ptr(self.cu_seqblocks), _ptr(self.cu_block_tokens), self.nb,
+                _ptr(self.cu_seqlens_q), self.batch, float(softmax_scale), _ptr(dq), _ptr(dk),
+                _ptr(dv), _ptr(delta), _ptr(self.ws), self.ws.numel(), _stream(self.dev)),
+                "lsrm_sel_attn_bwd_run")
+        return dq, dk, dv, delta
 
 
 def reverse_query_map(topk_idx: torch.Tensor, cu_seqlens_q: torch.Tensor,
