@@ -225,9 +225,9 @@ static int fwd_impl(const void* q, const void* k, const void* v, int dtype,
                     int64_t batch, float softmax_scale, void* out, float* lse,
                     void* workspace, size_t workspace_bytes, void* stream,
                     bool plan) {
-  if (n_q == 0)
-    return check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk, n_blocks,
-                           batch);
+  const int arc = check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk,
+                                  n_blocks, batch);
+  if (arc || n_q == 0) return arc;
   if (!out || !lse || !aligned16(out)) return LSRM_ERR_INVALID_ARG;
   hipStream_t st = (hipStream_t)stream;
   AttnArgs a;
@@ -277,9 +277,9 @@ static int bwd_impl(const void* dout, const void* q, const void* k,
                     float softmax_scale, void* dq, void* dk, void* dv,
                     float* delta, void* workspace, size_t workspace_bytes,
                     void* stream, bool plan) {
-  if (n_q == 0)
-    return check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk, n_blocks,
-                           batch);
+  const int arc = check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk,
+                                  n_blocks, batch);
+  if (arc || n_q == 0) return arc;
   if (!dout || !out || !lse || !dq || !dk || !dv || !delta ||
       !aligned16(dout) || !aligned16(out) || !aligned16(dq) || !aligned16(dk) ||
       !aligned16(dv))

@@ -67,15 +67,15 @@ def normalized_rows(topk_idx: torch.Tensor, cu_seqblocks: torch.Tensor,
 def sel_attn_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, topk_idx: torch.Tensor,
                  cu_seqblocks: torch.Tensor, cu_block_tokens: torch.Tensor,
                  cu_seqlens_q: torch.Tensor, scale: float):
-    """q [Nq, Hq, D], k/v [Nk, Hkv, D] (fp32, CPU; may require grad) ->
-    (o [Nq, Hq, D] fp32, lse [Hq, Nq] fp32 log2 units)."""
+    """q [Nq, Hq, D], k/v [Nk, Hkv, D] (fp32 or fp64, CPU; may require grad) ->
+    (o [Nq, Hq, D], lse [Hq, Nq] log2 units), both in q's dtype."""
     nq, hq, d = q.shape
     hkv = k.shape[1]
     g = hq // hkv
     cu = cu_block_tokens.to(torch.int64)
     rows, base, starts = normalized_rows(topk_idx, cu_seqblocks, cu_seqlens_q)
-    lse = torch.full((hq, nq), -math.inf, dtype=torch.float32)
-    o = torch.zeros(nq, hq, d, dtype=torch.float32)
+    lse = torch.full((hq, nq), -math.inf, dtype=q.dtype)
+    o = torch.zeros(nq, hq, d, dtype=q.dtype)
     pieces = []  # (h, a, b, o_run [L, G, D])
     for h in range(hkv):
         for a, b in _row_runs(rows[h], starts):
