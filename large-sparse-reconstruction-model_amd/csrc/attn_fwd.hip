@@ -17,6 +17,10 @@
 
 namespace lsrm {
 
+// Largest growth (log2 units) of a row maximum over the running reference
+// before O and l are rescaled.
+constexpr float RESCALE_LOG2 = 8.0f;
+
 template <int DT, int D>
 __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
   constexpr int KS = D + 8;   // sK row stride (elements)
@@ -94,10 +98,12 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
       sstore<NW>(&sK[buf][(2 * kp) * KS + dg * (D / 8)], kr[0]);
       sstore<NW>(&sK[buf][(2 * kp + 1) * KS + dg * (D / 8)], kr[1]);
 #pragma unroll
-      for (int i = 0; i < D / 8; ++i) {
-        const int d = dg * (D / 8) + i;
+      for (int j = 0; j < NW; ++j) {
+        const int d = dg * (D / 8) + 2 * j;
         *reinterpret_cast<uint32_t*>(&sV[buf][d * VS + 2 * kp]) =
-            half_of(vr[0], i) | (half_of(vr[1], i) << 16);
+            pair_lo(vr[0][j], vr[1][j]);
+        *reinterpret_cast<uint32_t*>(&sV[buf][(d + 1) * VS + 2 * kp]) =
+            pair_hi(vr[0][j], vr[1][j]);
       }
     };
 
@@ -140,32 +146,40 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
           for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sacc[blk][v]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx * a.scale_log2);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        float lsum = 0.0f;
+        // Lazy rescaling: the running reference m_run only moves when a row
+        // maximum exceeds it by more than RESCALE_LOG2 (so p <= 2^8); the
+        // final O = acc / l is the same for any reference.
+        const float m_tile = mx * a.scale_log2;
+        if (__builtin_amdgcn_ballot_w64(m_tile > m_run + RESCALE_LOG2) != 0) {
+          const float m_new = fmaxf(m_run, m_tile);
+          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+          m_run = m_new;
+          l_run *= alpha;
+#pragma unroll
+          for (int db = 0; db < ND; ++db)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) oacc[db][v] *= alpha;
+        }
         u32x4 pb[2][2];
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
           float p[16];
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
+          for (int v = 0; v < 16; ++v)
             p[v] = __builtin_amdgcn_exp2f(
-                __builtin_fmaf(sacc[blk][v], a.scale_log2, -m_new));
-            lsum += p[v];
-          }
+                __builtin_fmaf(sacc[blk][v], a.scale_log2, -m_run));
 #pragma unroll
-          for (int c = 0; c < 2; ++c)
+          for (int c = 0; c < 2; ++c) {
             pb[blk][c] = u32x4{pack2<DT>(p[c * 8 + 0], p[c * 8 + 1]),
                                pack2<DT>(p[c * 8 + 2], p[c * 8 + 3]),
                                pack2<DT>(p[c * 8 + 4], p[c * 8 + 5]),
                                pack2<DT>(p[c * 8 + 6], p[c * 8 + 7])};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) l_run = sum2<DT>(pb[blk][c][w], l_run);
+          }
         }
-        l_run = l_run * alpha + lsum;
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) oacc[db][v] *= alpha;
 #pragma unroll
           for (int blk = 0; blk < 2; ++blk)
 #pragma unroll

@@ -27,35 +27,8 @@ __device__ __host__ inline float bf16_bits_to_f32(uint16_t h) {
   return c.f;
 }
 
-// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
-__device__ __host__ inline uint16_t f32_to_bf16_bits(float f) {
-  union {
-    uint32_t u;
-    float f;
-  } c;
-  c.f = f;
-  uint32_t u = c.u;
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
 __device__ inline float f16_bits_to_f32(uint16_t h) {
-  union {
-    uint16_t u;
-    _Float16 f;
-  } c;
-  c.u = h;
-  return (float)c.f;
-}
-
-__device__ inline uint16_t f32_to_f16_bits(float f) {
-  union {
-    uint16_t u;
-    _Float16 f;
-  } c;
-  c.f = (_Float16)f;  // IEEE round to nearest even
-  return c.u;
+  return (float)__builtin_bit_cast(_Float16, h);
 }
 
 template <int DT>
@@ -69,21 +42,57 @@ __device__ inline float to_f32<LSRM_F16>(uint16_t h) {
   return f16_bits_to_f32(h);
 }
 
+// fp32 -> 16-bit, round to nearest even (gfx950 v_cvt_pk_{bf16,f16}_f32).
 template <int DT>
 __device__ inline uint16_t from_f32(float f);
 template <>
 __device__ inline uint16_t from_f32<LSRM_BF16>(float f) {
-  return f32_to_bf16_bits(f);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 template <>
 __device__ inline uint16_t from_f32<LSRM_F16>(float f) {
-  return f32_to_f16_bits(f);
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
-// Two floats -> two packed 16-bit values (lo = a, hi = b), round to nearest.
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+
+// Two floats -> two packed 16-bit values (lo = a, hi = b), round to nearest
+// even: one v_cvt_pk_*_f32.
 template <int DT>
-__device__ inline uint32_t pack2(float a, float b) {
-  return (uint32_t)from_f32<DT>(a) | ((uint32_t)from_f32<DT>(b) << 16);
+__device__ inline uint32_t pack2(float a, float b);
+template <>
+__device__ inline uint32_t pack2<LSRM_BF16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, bf16x2{(__bf16)a, (__bf16)b});
+}
+template <>
+__device__ inline uint32_t pack2<LSRM_F16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, f16x2{(_Float16)a, (_Float16)b});
+}
+
+// acc + lo(w) + hi(w) for a packed pair w, exact products (v_dot2c_f32_*).
+template <int DT>
+__device__ inline float sum2(uint32_t w, float acc);
+template <>
+__device__ inline float sum2<LSRM_BF16>(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                         bf16x2{(__bf16)1.0f, (__bf16)1.0f},
+                                         acc, false);
+}
+template <>
+__device__ inline float sum2<LSRM_F16>(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w),
+                                f16x2{(_Float16)1.0f, (_Float16)1.0f}, acc,
+                                false);
+}
+
+// {lo16(lo), lo16(hi)} and {hi16(lo), hi16(hi)} of two packed words
+// (one v_perm_b32 each).
+__device__ inline uint32_t pair_lo(uint32_t lo, uint32_t hi) {
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+__device__ inline uint32_t pair_hi(uint32_t lo, uint32_t hi) {
+  return __builtin_amdgcn_perm(hi, lo, 0x07060302u);
 }
 
 // ------------------------------------------------------------------ MFMA --

@@ -25,13 +25,17 @@ LIB_PATH = PKG_DIR / LIB_NAME
 ARCH = "gfx950"
 
 # Packed fp32 VALU forms are disabled: the compiler would otherwise form
-# v_pk_{add,mul,fma}_f32 from plain float code.
+# v_pk_{add,mul,fma}_f32 from plain float code.  MFMA results are kept in
+# ordinary VGPRs (gfx950 reads and writes MFMA operands from the unified
+# register file); the AGPR form made the compiler copy every score and output
+# accumulator between register files on each key tile.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
