@@ -6,13 +6,24 @@
 // exponent) over the tokens of its selected blocks, P rounded to the input
 // type before P.V, O = acc / l and LSE = m + log2(l) in log2 units.
 //
-// Design: a persistent grid pulls query tiles (128 rows of one kv head that
-// share one selection) from an atomic queue.  Each wave owns 32 rows.  The
-// tile's key stream is gathered through LDS 64 keys at a time (K row-major,
-// V transposed), double buffered with a register prefetch of the next tile.
-// Scores are computed transposed, S^T = K Q^T, so that a lane owns one query
-// row through the whole softmax and the accumulator O^T = V^T P^T; the
-// softmax statistics stay in-lane except one cross-half exchange.
+// Design: a persistent grid pulls query tiles (up to 128 rows of one kv head
+// that share one selection) from an atomic queue.  Each wave owns 32 rows.
+// The tile's key stream (the concatenated token ranges of its selected
+// blocks) is staged through LDS 64 keys at a time:
+//   * K and V tiles are copied global -> LDS by the load unit
+//     (global_load_lds_dwordx4, no register staging), both row-major with a
+//     16-byte-chunk XOR swizzle that keeps the MFMA operand reads free of
+//     bank conflicts;
+//   * scores are computed transposed, S^T = K Q^T (32x32x16 MFMA, K from LDS,
+//     Q in registers), so that a lane owns one query row through the whole
+//     softmax; O^T = V^T P^T takes its V^T operand straight from the
+//     row-major V tile with ds_read_b64_tr_b16 and P^T from the score
+//     registers, so V is never transposed in memory;
+//   * the loop is software pipelined: the score MFMAs of key tile t+1 are
+//     issued before the softmax of tile t, K runs two tiles ahead of the
+//     softmax and V one tile ahead, one barrier per tile.
+#include <type_traits>
+
 #include "attn.h"
 
 namespace lsrm {
@@ -21,25 +32,105 @@ namespace lsrm {
 // before O and l are rescaled.
 constexpr float RESCALE_LOG2 = 8.0f;
 
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// LDS byte address of a __shared__ object.
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)((__attribute__((address_space(3))) const char*)p);
+}
+
+// One 16-byte-per-lane global -> LDS copy: lane l's bytes base + voff land at
+// LDS address lds + 16 * l.  Issued as inline assembly so that the compiler
+// does not order every later LDS read behind it (it cannot tell which LDS
+// buffer the copy targets); completion is awaited explicitly with
+// wait_copies() before the barrier that publishes the buffer.
+// `base` and `lds` must be wave-uniform values held in SGPRs.
+__device__ inline void copy16_to_lds(const void* base, uint32_t voff,
+                                     uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 4\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(base), "s"(lds)
+      : "memory");
+}
+
+__device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// s_waitcnt vmcnt(0) as a compiler-visible instruction: the compiler then
+// knows every earlier vector-memory load (Q rows included) has completed and
+// does not insert its own vmcnt(0) waits inside the key loop, which would
+// also stall on the tile copies issued ahead.
+__device__ inline void wait_copies() {
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0), expcnt/lgkmcnt untouched
+}
+
+// Key-row geometry of one LDS tile (64 keys x D): 16-byte chunks per row,
+// keys per 1 KB direct-load instruction, and the chunk swizzle of a row.
+template <int D>
+struct KvTile {
+  static constexpr int CH = D / 8;          // 16-byte chunks per key row
+  static constexpr int KPL = 64 / CH;       // keys per 1 KB load
+  static constexpr int LPW = (KT / KPL) / 4;  // loads per wave per tile
+  static constexpr int BYTES = KT * D * 2;
+  // Physical chunk = logical chunk ^ swz(row).  Rows that fall on the same
+  // LDS banks (256-byte period) get distinct chunk positions both for the
+  // 16-lane row-strided K reads and the 4-row transposed V reads.
+  __device__ static constexpr int swz(int r) {
+    if constexpr (D == 32)
+      return (r >> 2) & 3;
+    else if constexpr (D == 64)
+      return (r & 7) ^ ((r >> 3) & 1);
+    else
+      return ((r & 7) << 1) | ((r >> 3) & 1);
+  }
+  // Byte offset of (row, logical chunk) inside a tile.
+  __device__ static constexpr int off(int r, int c) {
+    return r * (D * 2) + ((c ^ swz(r)) << 4);
+  }
+};
+
+// Per-lane cursor over the key stream: the token of stream position p and
+// the end of its segment.  Advanced by one tile (64 positions) at a time.
+struct StreamCursor {
+  int p, seg, tok, segend;
+};
+
+__device__ inline void cursor_seek(const SelLds& s, StreamCursor& c) {
+  while (c.seg + 1 < s.n && s.cum[c.seg + 1] <= c.p) ++c.seg;
+  c.tok = s.tok[c.seg] + (c.p - s.cum[c.seg]);
+  c.segend = s.cum[c.seg + 1];
+}
+
 template <int DT, int D>
 __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
-  constexpr int KS = D + 8;   // sK row stride (elements)
-  constexpr int VS = KT + 4;  // sV row stride (elements, 8-byte rows)
+  using G = KvTile<D>;
   constexpr int NS = D / 16;  // MFMA k-steps over the head dim
   constexpr int ND = D / 32;  // 32-wide output blocks over the head dim
-  constexpr int NW = D / 16;  // 32-bit words a loader moves per key
-  __shared__ __align__(16) uint16_t sK[2][KT * KS];
-  __shared__ __align__(16) uint16_t sV[2][D * VS];
+  __shared__ __align__(1024) char sK[2][G::BYTES];
+  __shared__ __align__(1024) char sV[2][G::BYTES];
   __shared__ SelLds sel;
   __shared__ int s_slot;
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
-  const int kp = tid >> 3, dg = tid & 7;  // loader: keys 2kp, 2kp+1; d group
   const int total = a.plan.head_off[a.hkv];
 
+  // Loader geometry: load j of this wave covers keys (wv*LPW + j)*KPL + ...
+  int ld_key[G::LPW], ld_byte[G::LPW];
+#pragma unroll
+  for (int j = 0; j < G::LPW; ++j) {
+    ld_key[j] = (wv * G::LPW + j) * G::KPL + lane / G::CH;
+    ld_byte[j] = (((lane % G::CH) ^ G::swz(ld_key[j])) << 4);
+  }
+  // Bytes between consecutive tokens; K and V are below 4 GiB (checked by
+  // the host), so token offsets fit 32 bits.
+  const uint32_t row_bytes = (uint32_t)a.hkv * D * 2;
+
   for (;;) {
-    const int w = fetch_work(a.plan.counter, &s_slot);
+    const int w = uniform(fetch_work(a.plan.counter, &s_slot));
     if (w >= total) break;
     const int h = head_of(a.plan.head_off, a.hkv, w);
     const int2 tile = a.plan.tiles[(int64_t)h * a.nq + (w - a.plan.head_off[h])];
@@ -47,6 +138,7 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
     load_selection(a, h, q0, sel);
     const int nkeys = sel.cum[sel.n];
     const int ntiles = (nkeys + KT - 1) / KT;
+    const int t_safe = sel.n > 0 ? sel.tok[0] : 0;  // in-bounds filler token
 
     // This wave's row and its Q operand (B of S^T = K Q^T).
     const int r = wv * 32 + l32;
@@ -64,6 +156,43 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
         qb[s] = u32x4{0u, 0u, 0u, 0u};
     }
 
+    const char* kbase = reinterpret_cast<const char*>(a.k + (int64_t)h * D);
+    const char* vbase = reinterpret_cast<const char*>(a.v + (int64_t)h * D);
+
+    // Cursors of the K loads (two tiles ahead); V reuses the K offsets of
+    // the previous tile.
+    StreamCursor cur[G::LPW];
+    uint32_t koff[G::LPW], voff[G::LPW];
+#pragma unroll
+    for (int j = 0; j < G::LPW; ++j) {
+      cur[j].p = ld_key[j] - KT;  // advanced before first use
+      cur[j].seg = 0;
+      cur[j].tok = 0;
+      cur[j].segend = 0;
+    }
+    // Moves every cursor to the next tile and returns the byte offsets of
+    // its keys' rows.
+    auto advance = [&](uint32_t* off) {
+#pragma unroll
+      for (int j = 0; j < G::LPW; ++j) {
+        StreamCursor& c = cur[j];
+        c.p += KT;
+        int t = t_safe;
+        if (c.p < nkeys) {
+          c.tok += KT;
+          if (c.p >= c.segend) cursor_seek(sel, c);
+          t = c.tok;
+        }
+        off[j] = (uint32_t)t * row_bytes + ld_byte[j];
+      }
+    };
+    auto load_tile = [&](const char* base, const uint32_t* off, char* dst) {
+      const uint32_t d0 = lds_addr(dst) + wv * G::LPW * 1024;
+#pragma unroll
+      for (int j = 0; j < G::LPW; ++j)
+        copy16_to_lds(base, off[j], d0 + j * 1024);
+    };
+
     f32x16 oacc[ND];
 #pragma unroll
     for (int i = 0; i < ND; ++i)
@@ -71,80 +200,66 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
       for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
     float m_run = -__builtin_inf(), l_run = 0.0f;
 
-    int cur0 = 0, cur1 = 0;
-    uint32_t kr[2][NW], vr[2][NW];
-    auto gather = [&](int kt) {
-      const int p0 = kt * KT + 2 * kp, p1 = p0 + 1;
-      if (p0 < nkeys) {
-        const int t = stream_token(sel, p0, cur0);
-        const int64_t off = ((int64_t)t * a.hkv + h) * D + dg * (D / 8);
-        gload<NW>(kr[0], a.k + off);
-        gload<NW>(vr[0], a.v + off);
-      } else {
+    auto scores = [&](const char* ks, f32x16* sacc) {
 #pragma unroll
-        for (int i = 0; i < NW; ++i) kr[0][i] = vr[0][i] = 0u;
-      }
-      if (p1 < nkeys) {
-        const int t = stream_token(sel, p1, cur1);
-        const int64_t off = ((int64_t)t * a.hkv + h) * D + dg * (D / 8);
-        gload<NW>(kr[1], a.k + off);
-        gload<NW>(vr[1], a.v + off);
-      } else {
+      for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
-        for (int i = 0; i < NW; ++i) kr[1][i] = vr[1][i] = 0u;
-      }
-    };
-    auto stage = [&](int buf) {
-      sstore<NW>(&sK[buf][(2 * kp) * KS + dg * (D / 8)], kr[0]);
-      sstore<NW>(&sK[buf][(2 * kp + 1) * KS + dg * (D / 8)], kr[1]);
+        for (int v = 0; v < 16; ++v) sacc[blk][v] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < NW; ++j) {
-        const int d = dg * (D / 8) + 2 * j;
-        *reinterpret_cast<uint32_t*>(&sV[buf][d * VS + 2 * kp]) =
-            pair_lo(vr[0][j], vr[1][j]);
-        *reinterpret_cast<uint32_t*>(&sV[buf][(d + 1) * VS + 2 * kp]) =
-            pair_hi(vr[0][j], vr[1][j]);
-      }
-    };
-
-    if (ntiles > 0) {
-      gather(0);
-      stage(0);
-    }
-    __syncthreads();
-
-    for (int kt = 0; kt < ntiles; ++kt) {
-      const int buf = kt & 1;
-      if (kt + 1 < ntiles) gather(kt + 1);
-      if (wave_on) {
-        const uint16_t* k_s = sK[buf];
-        const uint16_t* v_s = sV[buf];
-        f32x16 sacc[2];
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) sacc[blk][v] = 0.0f;
-#pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const u32x4 ka = *reinterpret_cast<const u32x4*>(
-                k_s + (blk * 32 + l32) * KS + s * 16 + hb * 8);
-            sacc[blk] = mfma32<DT>(ka, qb[s], sacc[blk]);
-          }
+        for (int s = 0; s < NS; ++s) {
+          const u32x4 ka = *reinterpret_cast<const u32x4*>(
+              ks + G::off(blk * 32 + l32, 2 * s + hb));
+          sacc[blk] = mfma32<DT>(ka, qb[s], sacc[blk]);
         }
-        const int kbase = kt * KT;
-        if (kbase + KT > nkeys) {
+      }
+    };
+
+    // Prologue: K(0), V(0), K(1) in flight, then S(0).
+    if (ntiles > 0) {
+      advance(koff);
+      load_tile(kbase, koff, sK[0]);
+      load_tile(vbase, koff, sV[0]);
+      advance(voff);  // voff <- offsets of tile 1 (used for K(1) and V(1))
+      if (ntiles > 1) load_tile(kbase, voff, sK[1]);
+    }
+    wait_copies();
+    __syncthreads();
+    f32x16 sA[2], sB[2];
+    if (wave_on && ntiles > 0) scores(sK[0], sA);
+    __syncthreads();  // sK[0] is refilled below
+
+    // One key tile: parity P = kt & 1 selects the buffers at compile time;
+    // sc holds S(kt) on entry, sn receives S(kt+1).
+    auto step = [&](auto parity, int kt, f32x16* sc, f32x16* sn) {
+      constexpr int P = decltype(parity)::value;
+      // K(kt+2) -> sK[P] (read last as S(kt)); V(kt+1) -> sV[P^1].
+      if (kt + 2 < ntiles) {
+        advance(koff);
+        load_tile(kbase, koff, sK[P]);
+      }
+      if (kt + 1 < ntiles) load_tile(vbase, voff, sV[P ^ 1]);
+#pragma unroll
+      for (int j = 0; j < G::LPW; ++j) voff[j] = koff[j];
+
+      if (wave_on) {
+        // S(kt+1); on the last tile this scores stale keys and is discarded,
+        // which keeps the score registers free of a select per element.
+        scores(sK[P ^ 1], sn);
+
+        const int kb0 = kt * KT;
+        if (kb0 + KT > nkeys) {
 #pragma unroll
           for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
             for (int v = 0; v < 16; ++v)
-              if (kbase + blk * 32 + acc_row(v, hb) >= nkeys)
-                sacc[blk][v] = -__builtin_inf();
+              if (kb0 + blk * 32 + acc_row(v, hb) >= nkeys)
+                sc[blk][v] = -__builtin_inf();
         }
-        float mx = sacc[0][0];
+        float mx = sc[0][0];
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sacc[blk][v]);
+          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[blk][v]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         // Lazy rescaling: the running reference m_run only moves when a row
         // maximum exceeds it by more than RESCALE_LOG2 (so p <= 2^8); the
@@ -167,7 +282,7 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
           for (int v = 0; v < 16; ++v)
             p[v] = __builtin_amdgcn_exp2f(
-                __builtin_fmaf(sacc[blk][v], a.scale_log2, -m_run));
+                __builtin_fmaf(sc[blk][v], a.scale_log2, -m_run));
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
             pb[blk][c] = u32x4{pack2<DT>(p[c * 8 + 0], p[c * 8 + 1]),
@@ -175,27 +290,45 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
                                pack2<DT>(p[c * 8 + 4], p[c * 8 + 5]),
                                pack2<DT>(p[c * 8 + 6], p[c * 8 + 7])};
 #pragma unroll
-            for (int w = 0; w < 4; ++w) l_run = sum2<DT>(pb[blk][c][w], l_run);
+            for (int e = 0; e < 4; ++e) l_run = sum2<DT>(pb[blk][c][e], l_run);
           }
         }
+        // O^T += V^T P^T.  Slot e of lane (hb, row d) holds key
+        // blk*32 + c*16 + (e/4)*8 + hb*4 + e%4 (the score layout); the two
+        // transposed reads return those keys' column d.
+        const char* vs = sV[P];
+        const int gi = lane & 15, dh = (lane >> 4) & 1;
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
+          const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;  // 4 d values
 #pragma unroll
           for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
-              const uint16_t* vp =
-                  v_s + (db * 32 + l32) * VS + blk * 32 + c * 16 + hb * 4;
-              const u32x2 lo = *reinterpret_cast<const u32x2*>(vp);
-              const u32x2 hi = *reinterpret_cast<const u32x2*>(vp + 8);
-              oacc[db] = mfma32<DT>(u32x4{lo[0], lo[1], hi[0], hi[1]},
+              const int k0 = blk * 32 + c * 16 + hb * 4 + (gi >> 2);
+              const int cb = dcol >> 3, half = (dcol & 4) * 2;
+              const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_s16x4*)(vs + G::off(k0, cb) + half));
+              const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_s16x4*)(vs + G::off(k0 + 8, cb) + half));
+              const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+              const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+              oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]},
                                     pb[blk][c], oacc[db]);
             }
         }
       }
-      if (kt + 1 < ntiles) stage(buf ^ 1);
+      wait_copies();  // this wave's copies of K(kt+2) / V(kt+1) landed
       __syncthreads();
+    };
+    const std::integral_constant<int, 0> even;
+    const std::integral_constant<int, 1> odd;
+    int kt = 0;
+    for (; kt + 1 < ntiles; kt += 2) {
+      step(even, kt, sA, sB);
+      step(odd, kt + 1, sB, sA);
     }
+    if (kt < ntiles) step(even, kt, sA, sB);
 
     // Epilogue: normalise, store O rows and LSE.
     const float l_tot = l_run + __shfl_xor(l_run, 32);

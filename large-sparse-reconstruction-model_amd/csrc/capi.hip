@@ -94,6 +94,9 @@ int check_attn_args(int dtype, int64_t n_q, int64_t n_k, int64_t hq,
   if (hq / hkv > 64 || topk > MAXSEL) return LSRM_ERR_UNSUPPORTED;
   if (n_q > INT32_MAX / (topk > 0 ? topk : 1) || n_k > INT32_MAX)
     return LSRM_ERR_UNSUPPORTED;
+  // The attention kernels address K and V rows with 32-bit byte offsets.
+  if ((uint64_t)n_k * (uint64_t)hkv * (uint64_t)head_dim * 2u >= (1ull << 32))
+    return LSRM_ERR_UNSUPPORTED;
   return LSRM_OK;
 }
 
