@@ -46,7 +46,9 @@ struct AttnArgs {
 // their lengths (the key stream).
 struct SelLds {
   int tok[MAXSEL];
-  int cum[MAXSEL + 1];
+  int cum[MAXSEL + 2];  // cum[n] = total keys, cum[n + 1] = INT_MAX sentinel
+  int tb[MAXSEL + 1];   // tok[i] - cum[i]: token of stream position p in
+                        // segment i is p + tb[i]; tb[n] = 0
   int len_tmp[MAXSEL];
   int tok_tmp[MAXSEL];
   int n;
@@ -96,12 +98,15 @@ __device__ inline void load_selection(const AttnArgs& a, int h, int64_t q,
       if (keep) {
         s.tok[pos] = t0;
         s.cum[pos + 1] = cc + x;
+        s.tb[pos] = t0 - (cc + x - len);
       }
       cn += __popcll(m);
       cc += __shfl(x, 63);
     }
     if (lane == 0) {
       s.cum[0] = 0;
+      s.cum[cn + 1] = 0x7fffffff;
+      s.tb[cn] = 0;
       s.n = cn;
     }
   }

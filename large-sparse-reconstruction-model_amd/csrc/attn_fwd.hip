@@ -20,10 +20,9 @@
 //     row-major V tile with ds_read_b64_tr_b16 and P^T from the score
 //     registers, so V is never transposed in memory;
 //   * the loop is software pipelined: the score MFMAs of key tile t+1 are
-//     issued before the softmax of tile t, K runs two tiles ahead of the
-//     softmax and V one tile ahead, one barrier per tile.
-#include <type_traits>
-
+//     issued before the softmax of tile t; K and V live in three-slot LDS
+//     rings whose copies are issued two steps before they are read, one
+//     barrier per tile.
 #include "attn.h"
 
 namespace lsrm {
@@ -67,6 +66,14 @@ __device__ inline void wait_copies() {
   __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0), expcnt/lgkmcnt untouched
 }
 
+// s_waitcnt vmcnt(N): all but this wave's N most recent vector-memory loads
+// have completed (loads complete in issue order).
+template <int N>
+__device__ inline void wait_prev_copies() {
+  static_assert(N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | N);
+}
+
 // Key-row geometry of one LDS tile (64 keys x D): 16-byte chunks per row,
 // keys per 1 KB direct-load instruction, and the chunk swizzle of a row.
 template <int D>
@@ -92,25 +99,61 @@ struct KvTile {
   }
 };
 
-// Per-lane cursor over the key stream: the token of stream position p and
-// the end of its segment.  Advanced by one tile (64 positions) at a time.
+// Per-lane cursor over the key stream: the token of stream position p, the
+// end of its segment, and (prefetched) the next segment's token base
+// (token of position q in it = q + ntb) and end.  Advanced by one tile (64
+// positions) at a time; crossing one boundary uses the prefetched values, so
+// the common step has no dependent LDS read.
 struct StreamCursor {
-  int p, seg, tok, segend;
+  int p, seg, tok, segend, ntb, nend;
 };
 
+// Plain LDS reads (seg < n, so both indices are in range thanks to the
+// sentinels); their results are first needed at the next crossing.
+__device__ inline void cursor_prefetch(const SelLds& s, StreamCursor& c) {
+  c.ntb = s.tb[c.seg + 1];
+  c.nend = s.cum[c.seg + 2];
+}
+
+// Walks forward to the segment containing c.p (several boundaries crossed;
+// c.p < total keys, so the walk stops at the last segment at the latest).
 __device__ inline void cursor_seek(const SelLds& s, StreamCursor& c) {
-  while (c.seg + 1 < s.n && s.cum[c.seg + 1] <= c.p) ++c.seg;
-  c.tok = s.tok[c.seg] + (c.p - s.cum[c.seg]);
+  while (s.cum[c.seg + 1] <= c.p) ++c.seg;
+  c.tok = c.p + s.tb[c.seg];
   c.segend = s.cum[c.seg + 1];
 }
 
+// Maximum of a lane's 32 scores (a max3 tree), combined with the lane
+// holding the other 16 keys of the same row (v_permlane32_swap).
+__device__ inline float row_max(const f32x16* sc) {
+  float t[11];
+#pragma unroll
+  for (int i = 0; i < 10; ++i) {
+    const int a = 3 * i, b = 3 * i + 1, c = 3 * i + 2;
+    t[i] = __builtin_fmaxf(__builtin_fmaxf(sc[a >> 4][a & 15], sc[b >> 4][b & 15]),
+                           sc[c >> 4][c & 15]);
+  }
+  t[10] = __builtin_fmaxf(sc[1][14], sc[1][15]);
+  const float u0 = __builtin_fmaxf(__builtin_fmaxf(t[0], t[1]), t[2]);
+  const float u1 = __builtin_fmaxf(__builtin_fmaxf(t[3], t[4]), t[5]);
+  const float u2 = __builtin_fmaxf(__builtin_fmaxf(t[6], t[7]), t[8]);
+  const float u3 = __builtin_fmaxf(t[9], t[10]);
+  const float m = __builtin_fmaxf(__builtin_fmaxf(u0, u1), __builtin_fmaxf(u2, u3));
+  const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, m),
+                                                   __builtin_bit_cast(unsigned, m),
+                                                   false, false);
+  return __builtin_fmaxf(__builtin_bit_cast(float, (unsigned)sw[0]),
+                         __builtin_bit_cast(float, (unsigned)sw[1]));
+}
+
 template <int DT, int D>
-__global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+sel_attn_fwd_kernel(AttnArgs a) {
   using G = KvTile<D>;
   constexpr int NS = D / 16;  // MFMA k-steps over the head dim
   constexpr int ND = D / 32;  // 32-wide output blocks over the head dim
-  __shared__ __align__(1024) char sK[2][G::BYTES];
-  __shared__ __align__(1024) char sV[2][G::BYTES];
+  __shared__ __align__(1024) char sK[3][G::BYTES];
+  __shared__ __align__(1024) char sV[3][G::BYTES];
   __shared__ SelLds sel;
   __shared__ int s_slot;
 
@@ -146,21 +189,27 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
     const bool wave_on = wv * 32 < rows;
     const int64_t qi = q0 + (row_ok ? r / a.g : 0);
     const int hh = h * a.g + (row_ok ? r % a.g : 0);
+    // Q is pre-multiplied by scale*log2(e) (and rounded back to the input
+    // type), so the score MFMAs produce the exponent of the base-2 softmax
+    // directly.
     u32x4 qb[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
+      u32x4 raw = u32x4{0u, 0u, 0u, 0u};
       if (row_ok)
-        qb[s] = *reinterpret_cast<const u32x4*>(
+        raw = *reinterpret_cast<const u32x4*>(
             a.q + (qi * a.hq + hh) * D + s * 16 + hb * 8);
-      else
-        qb[s] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        qb[s][e] = pack2<DT>(to_f32<DT>((uint16_t)(raw[e] & 0xffffu)) * a.scale_log2,
+                             to_f32<DT>((uint16_t)(raw[e] >> 16)) * a.scale_log2);
     }
 
     const char* kbase = reinterpret_cast<const char*>(a.k + (int64_t)h * D);
     const char* vbase = reinterpret_cast<const char*>(a.v + (int64_t)h * D);
 
-    // Cursors of the K loads (two tiles ahead); V reuses the K offsets of
-    // the previous tile.
+    // Cursors of the K copies (three tiles ahead); the V copies (two tiles
+    // ahead) reuse the K offsets of the previous tile.
     StreamCursor cur[G::LPW];
     uint32_t koff[G::LPW], voff[G::LPW];
 #pragma unroll
@@ -168,7 +217,9 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
       cur[j].p = ld_key[j] - KT;  // advanced before first use
       cur[j].seg = 0;
       cur[j].tok = 0;
-      cur[j].segend = 0;
+      cur[j].segend = -1;         // forces a seek on the first advance
+      cur[j].ntb = 0;
+      cur[j].nend = -1;
     }
     // Moves every cursor to the next tile and returns the byte offsets of
     // its keys' rows.
@@ -180,11 +231,24 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
         int t = t_safe;
         if (c.p < nkeys) {
           c.tok += KT;
-          if (c.p >= c.segend) cursor_seek(sel, c);
+          if (c.p >= c.segend) {
+            if (c.p < c.nend) {  // exactly one boundary crossed
+              ++c.seg;
+              c.tok = c.p + c.ntb;
+              c.segend = c.nend;
+            } else {
+              cursor_seek(sel, c);
+            }
+            cursor_prefetch(sel, c);
+          }
           t = c.tok;
         }
         off[j] = (uint32_t)t * row_bytes + ld_byte[j];
       }
+    };
+    auto voff_keep = [&](const uint32_t* off) {
+#pragma unroll
+      for (int j = 0; j < G::LPW; ++j) voff[j] = off[j];
     };
     auto load_tile = [&](const char* base, const uint32_t* off, char* dst) {
       const uint32_t d0 = lds_addr(dst) + wv * G::LPW * 1024;
@@ -198,13 +262,18 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
     for (int i = 0; i < ND; ++i)
 #pragma unroll
       for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
-    float m_run = -__builtin_inf(), l_run = 0.0f;
+    // Online softmax state of this lane's row: the running reference m_run
+    // (log2 units) and the partial row sum.  The score accumulators start
+    // from tmpl = -m_run, so S holds exponents relative to m_run.
+    float m_run = 0.0f, l_run = 0.0f;
+    f32x16 tmpl;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) tmpl[v] = 0.0f;
 
     auto scores = [&](const char* ks, f32x16* sacc) {
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) sacc[blk][v] = 0.0f;
+        sacc[blk] = tmpl;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
           const u32x4 ka = *reinterpret_cast<const u32x4*>(
@@ -214,38 +283,41 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
       }
     };
 
-    // Prologue: K(0), V(0), K(1) in flight, then S(0).
+    // Prologue: K(0), V(0), K(1) resident, S(0) computed, then K(2) and
+    // V(1) in flight (the copies a step issues are consumed two steps later).
     if (ntiles > 0) {
       advance(koff);
       load_tile(kbase, koff, sK[0]);
       load_tile(vbase, koff, sV[0]);
-      advance(voff);  // voff <- offsets of tile 1 (used for K(1) and V(1))
-      if (ntiles > 1) load_tile(kbase, voff, sK[1]);
+      advance(koff);
+      load_tile(kbase, koff, sK[1]);
+      voff_keep(koff);
     }
     wait_copies();
     __syncthreads();
     f32x16 sA[2], sB[2];
     if (wave_on && ntiles > 0) scores(sK[0], sA);
-    __syncthreads();  // sK[0] is refilled below
+    if (ntiles > 0) {
+      advance(koff);
+      load_tile(kbase, koff, sK[2]);
+      load_tile(vbase, voff, sV[1]);
+      voff_keep(koff);
+    }
+    __syncthreads();  // sK[0] is refilled by step 0
 
-    // One key tile: parity P = kt & 1 selects the buffers at compile time;
-    // sc holds S(kt) on entry, sn receives S(kt+1).
-    auto step = [&](auto parity, int kt, f32x16* sc, f32x16* sn) {
-      constexpr int P = decltype(parity)::value;
-      // K(kt+2) -> sK[P] (read last as S(kt)); V(kt+1) -> sV[P^1].
-      if (kt + 2 < ntiles) {
-        advance(koff);
-        load_tile(kbase, koff, sK[P]);
-      }
-      if (kt + 1 < ntiles) load_tile(vbase, voff, sV[P ^ 1]);
-#pragma unroll
-      for (int j = 0; j < G::LPW; ++j) voff[j] = koff[j];
+    // One key tile kt: sc holds S(kt) on entry, sn receives S(kt+1).  The
+    // step reads K(kt+1) and V(kt) and copies K(kt+3) and V(kt+2) into the
+    // ring slots last read one step earlier.  Every step issues the same
+    // number of copies (positions past the stream load a resident token), so
+    // one counted wait retires exactly the previous step's copies.
+    auto step = [&](int kt, f32x16* sc, f32x16* sn) {
+      const int s0 = kt % 3, s1 = (kt + 1) % 3, s2 = (kt + 2) % 3;
+      advance(koff);
+      load_tile(kbase, koff, sK[s0]);
+      load_tile(vbase, voff, sV[s2]);
+      voff_keep(koff);
 
       if (wave_on) {
-        // S(kt+1); on the last tile this scores stale keys and is discarded,
-        // which keeps the score registers free of a select per element.
-        scores(sK[P ^ 1], sn);
-
         const int kb0 = kt * KT;
         if (kb0 + KT > nkeys) {
 #pragma unroll
@@ -255,34 +327,39 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
               if (kb0 + blk * 32 + acc_row(v, hb) >= nkeys)
                 sc[blk][v] = -__builtin_inf();
         }
-        float mx = sc[0][0];
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[blk][v]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        // Lazy rescaling: the running reference m_run only moves when a row
-        // maximum exceeds it by more than RESCALE_LOG2 (so p <= 2^8); the
-        // final O = acc / l is the same for any reference.
-        const float m_tile = mx * a.scale_log2;
-        if (__builtin_amdgcn_ballot_w64(m_tile > m_run + RESCALE_LOG2) != 0) {
-          const float m_new = fmaxf(m_run, m_tile);
-          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-          m_run = m_new;
+        const float mx = row_max(sc);
+        // Lazy rescaling: m_run is set to the row maximum on the first tile
+        // and afterwards only moves when a row maximum exceeds it by more
+        // than RESCALE_LOG2 (so p <= 2^8); the final O = acc / l is the same
+        // for any reference.
+        const bool first = kt == 0;
+        if (first || __builtin_amdgcn_ballot_w64(mx > RESCALE_LOG2) != 0) {
+          const float delta = first ? mx : fmaxf(mx, 0.0f);
+          const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(-delta);
+          m_run += delta;
           l_run *= alpha;
 #pragma unroll
           for (int db = 0; db < ND; ++db)
 #pragma unroll
             for (int v = 0; v < 16; ++v) oacc[db][v] *= alpha;
+#pragma unroll
+          for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sc[blk][v] -= delta;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) tmpl[v] = -m_run;
         }
+        // S(kt+1); on the last tile this scores stale keys and is discarded,
+        // which keeps the score registers free of a select per element.
+        scores(sK[s1], sn);
+
         u32x4 pb[2][2];
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
           float p[16];
 #pragma unroll
           for (int v = 0; v < 16; ++v)
-            p[v] = __builtin_amdgcn_exp2f(
-                __builtin_fmaf(sc[blk][v], a.scale_log2, -m_run));
+            p[v] = __builtin_amdgcn_exp2f(sc[blk][v]);
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
             pb[blk][c] = u32x4{pack2<DT>(p[c * 8 + 0], p[c * 8 + 1]),
@@ -296,7 +373,7 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
         // O^T += V^T P^T.  Slot e of lane (hb, row d) holds key
         // blk*32 + c*16 + (e/4)*8 + hb*4 + e%4 (the score layout); the two
         // transposed reads return those keys' column d.
-        const char* vs = sV[P];
+        const char* vs = sV[s0];
         const int gi = lane & 15, dh = (lane >> 4) & 1;
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
@@ -318,17 +395,15 @@ __global__ __launch_bounds__(256) void sel_attn_fwd_kernel(AttnArgs a) {
             }
         }
       }
-      wait_copies();  // this wave's copies of K(kt+2) / V(kt+1) landed
+      wait_prev_copies<2 * G::LPW>();  // the previous step's copies landed
       __syncthreads();
     };
-    const std::integral_constant<int, 0> even;
-    const std::integral_constant<int, 1> odd;
     int kt = 0;
     for (; kt + 1 < ntiles; kt += 2) {
-      step(even, kt, sA, sB);
-      step(odd, kt + 1, sB, sA);
+      step(kt, sA, sB);
+      step(kt + 1, sB, sA);
     }
-    if (kt < ntiles) step(even, kt, sA, sB);
+    if (kt < ntiles) step(kt, sA, sB);
 
     // Epilogue: normalise, store O rows and LSE.
     const float l_tot = l_run + __shfl_xor(l_run, 32);
