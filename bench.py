@@ -54,6 +54,19 @@ def event_time_ms(fn, reps: int) -> float:
     return start.elapsed_time(end) / reps
 
 
+def measured_traffic():
+    """HBM bytes per attention-forward launch at config 3, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (already scaled by the
+    plain-copy calibration recorded there), or None when absent."""
+    path = ROOT / "profiles" / "attn_fwd_cfg3_hbm_traffic.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch"):
+            return float(line.split()[1])
+    return None
+
+
 def cpu_baseline(w, q, k, v, topk_idx, flops_per_head_q, budget_s: float):
     """Times the CPU oracle head by head until the budget is spent."""
     from oracle.attention import sel_attn_ref  # the checker, timed as the CPU baseline
@@ -99,7 +112,18 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU oracle time for cpu_baseline (0 = skip)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run three 1 GiB device-to-device copies (the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        x = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0").fill_(1)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print("copied 3 x 1 GiB")
+        return 0
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -163,6 +187,13 @@ def main() -> int:
     ms_pool = event_time_ms(lambda: H.block_mean_pool(k2, cu_blk), reps)
     ms_select = event_time_ms(
         lambda: H.select_blocks(q, k, cu_sb, cu_blk, w.topk, w.forced_blocks, True), reps)
+    # Backward (training path) on the same selection: dQ, reverse map, dK/dV.
+    bplan = H.SelAttnPlan(q.shape, k.shape, topk_idx, cu_sb, cu_blk, cu_q, backward=True)
+    do = torch.randn_like(q)
+    bplan.bwd(do, q, k, v, out, lse, w.scale)
+    ms_bwd = event_time_ms(lambda: bplan.bwd(do, q, k, v, out, lse, w.scale),
+                           max(2, reps // 4))
+    del bplan, do
     nb = w.n_blocks
     pool_bytes = n * hkv * d * 2 + nb * hkv * d * 2 + 4 * (nb + 1)
     attn_tflops = flops / (ms_attn * 1e-3) / 1e12
@@ -197,6 +228,10 @@ def main() -> int:
                        "gbs": round(pool_gbs, 1),
                        "frac_hbm_peak": round(pool_gbs / PEAK_HBM_GBS, 4)},
             "select": {"ms": round(ms_select, 4)},
+            "attn_bwd": {"ms": round(ms_bwd, 4),
+                         "tflops": round(2.5 * flops / (ms_bwd * 1e-3) / 1e12, 2),
+                         "frac_bf16_peak": round(2.5 * flops / (ms_bwd * 1e-3) / 1e12
+                                                 / PEAK_BF16_TFLOPS, 4)},
         },
         "roofline": {
             "bound": "mfma",
@@ -204,7 +239,7 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
     }
     if args.cpu_budget > 0:

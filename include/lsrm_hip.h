@@ -142,7 +142,8 @@ int lsrm_sel_attn_validate(const int32_t* topk_idx, int64_t hkv, int64_t n_q,
  *   out [n_q, hq, head_dim] dtype; lse [hq, n_q] fp32 in log2 units
  *   (lse = log2 sum exp2(scale*log2(e)*q.k)).  A row with no valid entry
  *   gives out = 0 and lse = -inf.
- * head_dim in {32, 64, 128}; hq % hkv == 0 and hq / hkv <= 64.
+ * head_dim in {32, 64, 128}; hq % hkv == 0 and hq / hkv <= 64; topk <= 256;
+ * k and v each below 4 GiB (rows are addressed with 32-bit byte offsets).
  * Replaces: ..._impl_kvcentric.py:931-1010 (forward_kernel_varblock 55-247).
  * ---------------------------------------------------------------------- */
 size_t lsrm_sel_attn_workspace_size(int64_t n_q, int64_t n_k, int64_t hq,
