@@ -2,8 +2,11 @@
 // compression of LSRM, sparse/module/spatial_sparse_attention.py:27-37, which
 // calls torch.segment_reduce(reduce="mean") on a [N, H*D] tensor).
 //
-// Two streaming kernels:
+// Streaming kernels:
+//   pool_chunk_first : the block owning each chunk's first row (one binary
+//                  search per chunk).
 //   pool_pieces  : one thread per (64-row chunk, 8-channel group) sums its rows
+//                  (16-bit rows: 16 packed 16-byte loads in flight per thread)
 //                  in fp32, emitting a partial sum each time a block boundary
 //                  is crossed.  Partial (block b, chunk j) lives at row b + j
 //                  of the partial buffer (unique because blocks are
@@ -52,23 +55,39 @@ __device__ inline float load1(const void* x, int64_t off) {
 }
 
 // VEC channels per thread (8 on the 16-byte path, 1 on the scalar path).
-template <int DT, int VEC>
+// first[j] = last block whose start is <= 64 j (the block owning chunk j's
+// first row, or -1 / nb outside the blocks): one binary search per chunk
+// instead of one per thread.
+__global__ __launch_bounds__(256) void pool_chunk_first(
+    const int32_t* __restrict__ cu, int64_t nb, int64_t n_chunks,
+    int32_t* __restrict__ first) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n_chunks) return;
+  int64_t b = upper_index(cu, 0, nb + 1, j * POOL_CHUNK);
+  first[j] = (int32_t)(b > nb ? nb : b);
+}
+
+// WU: every wave's items share one chunk (channel groups a multiple of 64),
+// so the chunk index is made wave-uniform and all row / block-boundary control
+// flow runs on the scalar unit.
+template <int DT, int VEC, bool WU>
 __global__ __launch_bounds__(256) void pool_pieces(
     const void* __restrict__ x, int64_t n, int64_t ch,
-    const int32_t* __restrict__ cu, int64_t nb, float* __restrict__ partial) {
+    const int32_t* __restrict__ cu, int64_t nb,
+    const int32_t* __restrict__ first, float* __restrict__ partial) {
   const int64_t n_vec = ch / VEC;
   const int64_t n_chunks = (n + POOL_CHUNK - 1) / POOL_CHUNK;
   const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= n_chunks * n_vec) return;
-  const int64_t j = item / n_vec;
+  int64_t j = item / n_vec;
   const int64_t c0 = (item - j * n_vec) * VEC;
+  if constexpr (WU) j = __builtin_amdgcn_readfirstlane((int)j);
   const int64_t r0 = j * POOL_CHUNK;
   const int64_t r1 = r0 + POOL_CHUNK < n ? r0 + POOL_CHUNK : n;
 
   // b = last block whose start is <= r0 (-1: before the first block,
   // nb: past the last).  bs/be bound the rows block b owns.
-  int64_t b = upper_index(cu, 0, nb + 1, r0);
-  if (b > nb) b = nb;
+  int64_t b = first[j];
   int64_t be = b < 0 ? (int64_t)cu[0] : (b < nb ? (int64_t)cu[b + 1] : INT64_MAX);
   int64_t bs = (b >= 0 && b < nb) ? (int64_t)cu[b] : INT64_MAX;
 
@@ -83,17 +102,26 @@ __global__ __launch_bounds__(256) void pool_pieces(
     for (int i = 0; i < VEC; ++i) dst[i] = acc[i];
   };
 
-  constexpr int U = VEC == 8 ? 8 : 16;  // rows in flight per thread
+  constexpr int U = 16;  // rows in flight per thread
   for (int64_t r = r0; r < r1; r += U) {
-    float v[U][VEC];
+    // 16-bit rows stay packed until they are added (fewer registers, more
+    // loads in flight); all U loads are issued (rows past the chunk re-read
+    // its last row and are skipped below) before any is used.
+    u32x4 raw[U];
+    float v1[U];
+    if constexpr (VEC == 8 && DT != LSRM_F32) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (r + u < r1) {
-        if constexpr (VEC == 8)
-          Vec8<DT>::load(x, (r + u) * ch + c0, v[u]);
-        else
-          v[u][0] = load1<DT>(x, (r + u) * ch + c0);
+      for (int u = 0; u < U; ++u) {
+        const int64_t rr = r + u < r1 ? r + u : r1 - 1;
+        raw[u] = *reinterpret_cast<const u32x4*>(
+            reinterpret_cast<const uint16_t*>(x) + rr * ch + c0);
       }
+#pragma unroll
+      for (int u = 0; u < U; ++u) asm volatile("" ::"v"(raw[u]));
+    } else if constexpr (VEC == 1) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        v1[u] = r + u < r1 ? load1<DT>(x, (r + u) * ch + c0) : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -109,8 +137,20 @@ __global__ __launch_bounds__(256) void pool_pieces(
           be = b < nb ? (int64_t)cu[b + 1] : INT64_MAX;
         }
         if (b >= 0 && b < nb && row >= bs) {
+          float v[VEC];
+          if constexpr (VEC == 8 && DT != LSRM_F32) {
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) acc[i] = acc[i] + v[u][i];
+            for (int i = 0; i < 4; ++i) {
+              v[2 * i] = to_f32<DT>((uint16_t)(raw[u][i] & 0xffffu));
+              v[2 * i + 1] = to_f32<DT>((uint16_t)(raw[u][i] >> 16));
+            }
+          } else if constexpr (VEC == 8) {
+            Vec8<DT>::load(x, row * ch + c0, v);
+          } else {
+            v[0] = v1[u];
+          }
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[i] = acc[i] + v[i];
           have = true;
         }
       }
@@ -160,26 +200,36 @@ int64_t pool_partial_rows(int64_t n, int64_t nb) {
   return nb + (n + POOL_CHUNK - 1) / POOL_CHUNK;
 }
 
-// Launches the two pooling kernels; partial needs pool_partial_rows * ch floats.
+// Entries of the chunk -> first-block table.
+int64_t pool_first_count(int64_t n) { return (n + POOL_CHUNK - 1) / POOL_CHUNK; }
+
+// Launches the pooling kernels; partial needs pool_partial_rows * ch floats
+// and first pool_first_count ints.
 int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
                            const int32_t* cu, int64_t nb, void* out,
-                           int out_dtype, float* partial, hipStream_t st) {
+                           int out_dtype, float* partial, int32_t* first,
+                           hipStream_t st) {
   if (nb == 0) return LSRM_OK;
   const bool vec = (ch % POOL_VEC) == 0 && ((uintptr_t)x % 16) == 0 &&
                    ((uintptr_t)partial % 16) == 0;
   const int64_t n_vec = vec ? ch / POOL_VEC : ch;
   const int64_t n_chunks = (n + POOL_CHUNK - 1) / POOL_CHUNK;
   if (n > 0) {
+    hipLaunchKernelGGL(pool_chunk_first, dim3((unsigned)((n_chunks + 255) / 256)),
+                       dim3(256), 0, st, cu, nb, n_chunks, first);
     const int64_t items = n_chunks * n_vec;
     dim3 grid((unsigned)((items + 255) / 256));
 #define LSRM_POOL_P(DT)                                                      \
   do {                                                                       \
-    if (vec)                                                                 \
-      hipLaunchKernelGGL((pool_pieces<DT, 8>), grid, dim3(256), 0, st, x, n, \
-                         ch, cu, nb, partial);                               \
+    if (vec && n_vec % 64 == 0)                                              \
+      hipLaunchKernelGGL((pool_pieces<DT, 8, true>), grid, dim3(256), 0, st, \
+                         x, n, ch, cu, nb, first, partial);                  \
+    else if (vec)                                                            \
+      hipLaunchKernelGGL((pool_pieces<DT, 8, false>), grid, dim3(256), 0,    \
+                         st, x, n, ch, cu, nb, first, partial);              \
     else                                                                     \
-      hipLaunchKernelGGL((pool_pieces<DT, 1>), grid, dim3(256), 0, st, x, n, \
-                         ch, cu, nb, partial);                               \
+      hipLaunchKernelGGL((pool_pieces<DT, 1, false>), grid, dim3(256), 0,    \
+                         st, x, n, ch, cu, nb, first, partial);              \
   } while (0)
     switch (x_dtype) {
       case LSRM_F32: LSRM_POOL_P(LSRM_F32); break;
@@ -222,7 +272,7 @@ extern "C" size_t lsrm_block_mean_pool_workspace_size(int64_t n_tokens,
   if (n_tokens < 0 || channels < 0 || n_blocks < 0) return 0;
   return (size_t)lsrm::pool_partial_rows(n_tokens, n_blocks) *
              (size_t)channels * sizeof(float) +
-         256;
+         256 + (size_t)lsrm::pool_first_count(n_tokens) * 4 + 256;
 }
 
 extern "C" int lsrm_block_mean_pool(const void* x, int x_dtype,
@@ -240,7 +290,9 @@ extern "C" int lsrm_block_mean_pool(const void* x, int x_dtype,
       lsrm_block_mean_pool_workspace_size(n_tokens, channels, n_blocks);
   if (workspace_bytes < need || (need > 256 && !workspace)) return LSRM_ERR_WORKSPACE;
   float* partial = reinterpret_cast<float*>(lsrm::align_up((size_t)workspace, 256));
+  int32_t* first = reinterpret_cast<int32_t*>(lsrm::align_up(
+      (size_t)(partial + lsrm::pool_partial_rows(n_tokens, n_blocks) * channels), 256));
   return lsrm::launch_block_mean_pool(x, x_dtype, n_tokens, channels,
                                       cu_block_tokens, n_blocks, out, out_dtype,
-                                      partial, (hipStream_t)stream);
+                                      partial, first, (hipStream_t)stream);
 }

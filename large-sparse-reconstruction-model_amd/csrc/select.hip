@@ -15,8 +15,10 @@ namespace lsrm {
 
 int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
                            const int32_t* cu, int64_t nb, void* out,
-                           int out_dtype, float* partial, hipStream_t st);
+                           int out_dtype, float* partial, int32_t* first,
+                           hipStream_t st);
 int64_t pool_partial_rows(int64_t n, int64_t nb);
+int64_t pool_first_count(int64_t n);
 
 constexpr int SCORE_TILE = 64;
 constexpr int SEL_MAXD = 128;
@@ -201,6 +203,7 @@ struct SelectWs {
   float* pq;
   float* pk;
   float* partial;
+  int32_t* first;
   double* scores;
 };
 
@@ -211,6 +214,7 @@ void carve_select(Carver& ws, int64_t n, int64_t nb, int64_t hq, int64_t hkv,
   s.pk = ws.take<float>((size_t)(nbc * hkv * d));
   s.partial = ws.take<float>((size_t)(pool_partial_rows(n, nbc) *
                                       (hq > hkv ? hq : hkv) * d));
+  s.first = ws.take<int32_t>((size_t)pool_first_count(n));
   s.scores = ws.take<double>((size_t)(hkv * nbc * nbc));
 }
 
@@ -264,11 +268,11 @@ extern "C" int lsrm_select_blocks(const void* q, const void* k, int dtype,
 
   int rc = launch_block_mean_pool(q, dtype, n_tokens, hq * head_dim,
                                   cu_block_tokens, n_blocks, s.pq, LSRM_F32,
-                                  s.partial, st);
+                                  s.partial, s.first, st);
   if (rc) return rc;
   rc = launch_block_mean_pool(k, dtype, n_tokens, hkv * head_dim,
                               cu_block_tokens, n_blocks, s.pk, LSRM_F32,
-                              s.partial, st);
+                              s.partial, s.first, st);
   if (rc) return rc;
   const unsigned nt = (unsigned)ceil_div(n_blocks, SCORE_TILE);
   hipLaunchKernelGGL(score_kernel, dim3(nt, nt, (unsigned)hkv), dim3(256), 0,
