@@ -199,6 +199,101 @@ __global__ __launch_bounds__(256) void topk_kernel(
   for (int64_t i = tid; i < total; i += 256) dst[i] = s_out[i % topk];
 }
 
+// One wave per (kv head, query block) row when the candidates fit the
+// registers (M per lane, blocks per batch <= 64 M): the row's scores stay in
+// registers, forced blocks are taken first, then k rounds of a lane-local
+// scan plus a wave butterfly pick the best (score descending, id ascending).
+// No LDS candidate cache and no workgroup barriers.
+template <int M>
+__global__ __launch_bounds__(256) void topk_wave_kernel(
+    const double* __restrict__ scores, int64_t nb,
+    const int32_t* __restrict__ cu_sb, int64_t batch,
+    const int32_t* __restrict__ cu_blk, int64_t n_tokens, int hkv, int topk,
+    const int32_t* __restrict__ forced, int n_forced, int force_self,
+    int32_t* __restrict__ topk_idx, int32_t* __restrict__ compact) {
+  __shared__ int s_sel[4][SEL_MAXK];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t rowid = (int64_t)blockIdx.x * 4 + wv;
+  if (rowid >= (int64_t)hkv * nb) return;  // whole wave
+  const int h = (int)(rowid / nb);
+  const int64_t b = rowid - (int64_t)h * nb;
+  int* sel = s_sel[wv];
+  const int64_t e = upper_index(cu_sb, 0, batch + 1, b);
+  int32_t* crow = compact + ((int64_t)h * nb + b) * topk;
+  if (e < 0 || e >= batch || b >= cu_sb[e + 1]) {
+    for (int j = lane; j < topk; j += 64) crow[j] = -1;
+    return;
+  }
+  const int64_t cs = cu_sb[e];
+  const int nbb = (int)(cu_sb[e + 1] - cs);
+  const double* row = scores + ((int64_t)h * nb + b) * nb + cs;
+
+  double v[M];
+  uint32_t taken = 0u;  // bit m: candidate lane + 64 m is unavailable
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int i = lane + 64 * m;
+    if (i < nbb) {
+      const double x = row[i];
+      v[m] = (x != x) ? -__builtin_inf() : x;
+    } else {
+      v[m] = -__builtin_inf();
+      taken |= 1u << m;
+    }
+  }
+  const int kmax = topk < nbb ? topk : nbb;
+  int n = 0;
+  auto take = [&](int id) {  // wave-uniform id
+    if (n >= kmax || id < 0 || id >= nbb) return;
+    const bool mine = (id & 63) == lane;
+    const bool was = mine && ((taken >> (id >> 6)) & 1u);
+    if (__builtin_amdgcn_ballot_w64(was) != 0) return;
+    if (mine) taken |= 1u << (id >> 6);
+    if (lane == 0) sel[n] = id;
+    ++n;
+  };
+  if (force_self) take((int)(b - cs));
+  for (int f = 0; f < n_forced; ++f) take(forced[f]);
+  for (; n < kmax;) {
+    double bs = -__builtin_inf();
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      if (!((taken >> m) & 1u) && sel_better(v[m], lane + 64 * m, bs, bi)) {
+        bs = v[m];
+        bi = lane + 64 * m;
+      }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const double os = __shfl_xor(bs, o);
+      const int oi = __shfl_xor(bi, o);
+      if (sel_better(os, oi, bs, bi)) {
+        bs = os;
+        bi = oi;
+      }
+    }
+    take(__builtin_amdgcn_readfirstlane(bi));
+  }
+  // Ascending ids (distinct), -1 padding: id -> its rank among the chosen.
+  __shared__ int s_out[4][SEL_MAXK];
+  int* ord = s_out[wv];
+  for (int j = lane; j < topk; j += 64) ord[j] = -1;
+  for (int j = lane; j < kmax; j += 64) {
+    const int id = sel[j];
+    int r = 0;
+    for (int t = 0; t < kmax; ++t) r += sel[t] < id;
+    ord[r] = id;
+  }
+  for (int j = lane; j < topk; j += 64) crow[j] = ord[j];
+  int64_t t0 = cu_blk[b], t1 = cu_blk[b + 1];
+  t0 = t0 < 0 ? 0 : (t0 > n_tokens ? n_tokens : t0);
+  t1 = t1 < t0 ? t0 : (t1 > n_tokens ? n_tokens : t1);
+  int32_t* dst = topk_idx + ((int64_t)h * n_tokens + t0) * topk;
+  const int64_t total = (t1 - t0) * topk;
+  for (int64_t i = lane; i < total; i += 64) dst[i] = ord[i % topk];
+}
+
 struct SelectWs {
   float* pq;
   float* pk;
@@ -279,10 +374,27 @@ extern "C" int lsrm_select_blocks(const void* q, const void* k, int dtype,
                      st, s.pq, s.pk, n_blocks, (int)hq, (int)hkv,
                      (int)head_dim, s.scores);
   LSRM_CHECK_LAUNCH();
-  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)n_blocks, (unsigned)hkv),
-                     dim3(256), 0, st, s.scores, n_blocks, cu_seqblocks, batch,
-                     cu_block_tokens, n_tokens, (int)topk, forced_blocks,
-                     (int)n_forced, force_self, topk_idx, topk_compact);
+  const unsigned rows4 = (unsigned)ceil_div(n_blocks * hkv, 4);
+#define LSRM_TOPK_WAVE(M)                                                     \
+  hipLaunchKernelGGL(topk_wave_kernel<M>, dim3(rows4), dim3(256), 0, st,      \
+                     s.scores, n_blocks, cu_seqblocks, batch, cu_block_tokens, \
+                     n_tokens, (int)hkv, (int)topk, forced_blocks,            \
+                     (int)n_forced, force_self, topk_idx, topk_compact)
+  if (n_blocks <= 64 * 4)
+    LSRM_TOPK_WAVE(4);
+  else if (n_blocks <= 64 * 8)
+    LSRM_TOPK_WAVE(8);
+  else if (n_blocks <= 64 * 16)
+    LSRM_TOPK_WAVE(16);
+  else if (n_blocks <= 64 * 32)
+    LSRM_TOPK_WAVE(32);
+  else
+    hipLaunchKernelGGL(topk_kernel, dim3((unsigned)n_blocks, (unsigned)hkv),
+                       dim3(256), 0, st, s.scores, n_blocks, cu_seqblocks,
+                       batch, cu_block_tokens, n_tokens, (int)topk,
+                       forced_blocks, (int)n_forced, force_self, topk_idx,
+                       topk_compact);
+#undef LSRM_TOPK_WAVE
   LSRM_CHECK_LAUNCH();
   return LSRM_OK;
 }
