@@ -178,6 +178,38 @@ __global__ __launch_bounds__(256) void breaks_kernel(
   brk[(int64_t)h * nq + i] = br ? 1 : 0;
 }
 
+// Same as breaks_kernel for k % 4 == 0 and 16-byte-aligned rows: each
+// thread reads its row with 16-byte loads (a wave reads 64 consecutive rows
+// contiguously) and takes the previous row from the neighbouring lane.
+__global__ __launch_bounds__(256) void breaks_vec_kernel(
+    const int32_t* __restrict__ topk, int64_t nq, int k,
+    const int32_t* __restrict__ cu_q, int64_t batch,
+    const int32_t* __restrict__ cu_sb, uint8_t* __restrict__ brk) {
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = i < nq;
+  int b = 0, bs = 0, nbb = 0;
+  bool start = true;
+  if (live) query_batch(cu_q, batch, cu_sb, i, &b, &bs, &nbb, &start);
+  const int64_t ii = live ? i : nq - 1;
+  const u32x4* r1 = reinterpret_cast<const u32x4*>(topk + ((int64_t)h * nq + ii) * k);
+  const u32x4* r0 = reinterpret_cast<const u32x4*>(
+      topk + ((int64_t)h * nq + (ii > 0 ? ii - 1 : 0)) * k);
+  bool diff = false;
+  for (int c = 0; c < k / 4; ++c) {
+    const u32x4 cur = r1[c];
+    u32x4 prev;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) prev[e] = (uint32_t)__shfl_up((int)cur[e], 1);
+    if (lane == 0) prev = r0[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      diff |= norm_entry((int)cur[e], nbb) != norm_entry((int)prev[e], nbb);
+  }
+  if (live) brk[(int64_t)h * nq + i] = (i == 0 || start || diff) ? 1 : 0;
+}
+
 struct BrkF {
   const uint8_t* brk;
   int64_t nq;
@@ -260,8 +292,12 @@ int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
 
   if (nq > 0) {
     dim3 grid(ceil_div(nq, 256), (unsigned)hkv);
-    hipLaunchKernelGGL(breaks_kernel, grid, dim3(256), 0, st, topk, nq,
-                       (int)topk_n, cu_q, batch, cu_sb, brk);
+    if (topk_n % 4 == 0 && ((uintptr_t)topk % 16) == 0)
+      hipLaunchKernelGGL(breaks_vec_kernel, grid, dim3(256), 0, st, topk, nq,
+                         (int)topk_n, cu_q, batch, cu_sb, brk);
+    else
+      hipLaunchKernelGGL(breaks_kernel, grid, dim3(256), 0, st, topk, nq,
+                         (int)topk_n, cu_q, batch, cu_sb, brk);
     LSRM_CHECK_LAUNCH();
     int rc = run_scan(BrkF{brk, nq}, RunStartW{run_start, nq}, nq, (int)hkv,
                       sums, n_runs, st);
