@@ -16,7 +16,7 @@
 //     bank conflicts;
 //   * scores are computed transposed, S^T = K Q^T (32x32x16 MFMA, K from LDS,
 //     Q in registers), so that a lane owns one query row through the whole
-//     softmax; O^T = V^T P^T takes its V^T operand straight from the
+//     softmax (base 2, scale folded into one FMA per score, lazy rescaling); O^T = V^T P^T takes its V^T operand straight from the
 //     row-major V tile with ds_read_b64_tr_b16 and P^T from the score
 //     registers, so V is never transposed in memory;
 //   * the loop is software pipelined: the score MFMAs of key tile t+1 are
@@ -27,8 +27,11 @@
 
 namespace lsrm {
 
-// Largest growth (log2 units) of a row maximum over the running reference
-// before O and l are rescaled.
+// Softmax reference: p = exp2(scale*log2(e)*s - m_run) with a per-row
+// reference m_run (log2 units) that is the row maximum after the first tile
+// and afterwards only moves when a row maximum exceeds it by more than
+// RESCALE_LOG2 (so p <= 2^8); the final O = acc / l is the same for any
+// reference.
 constexpr float RESCALE_LOG2 = 8.0f;
 
 typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
@@ -123,27 +126,26 @@ __device__ inline void cursor_seek(const SelLds& s, StreamCursor& c) {
   c.segend = s.cum[c.seg + 1];
 }
 
-// Maximum of a lane's 32 scores (a max3 tree), combined with the lane
+// Maximum of a lane's 32 scores (a v_maximum3 tree), combined with the lane
 // holding the other 16 keys of the same row (v_permlane32_swap).
+__device__ inline float max3f(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
 __device__ inline float row_max(const f32x16* sc) {
   float t[11];
 #pragma unroll
   for (int i = 0; i < 10; ++i) {
     const int a = 3 * i, b = 3 * i + 1, c = 3 * i + 2;
-    t[i] = __builtin_fmaxf(__builtin_fmaxf(sc[a >> 4][a & 15], sc[b >> 4][b & 15]),
-                           sc[c >> 4][c & 15]);
+    t[i] = max3f(sc[a >> 4][a & 15], sc[b >> 4][b & 15], sc[c >> 4][c & 15]);
   }
-  t[10] = __builtin_fmaxf(sc[1][14], sc[1][15]);
-  const float u0 = __builtin_fmaxf(__builtin_fmaxf(t[0], t[1]), t[2]);
-  const float u1 = __builtin_fmaxf(__builtin_fmaxf(t[3], t[4]), t[5]);
-  const float u2 = __builtin_fmaxf(__builtin_fmaxf(t[6], t[7]), t[8]);
-  const float u3 = __builtin_fmaxf(t[9], t[10]);
-  const float m = __builtin_fmaxf(__builtin_fmaxf(u0, u1), __builtin_fmaxf(u2, u3));
+  t[10] = __builtin_elementwise_maximum(sc[1][14], sc[1][15]);
+  const float m = max3f(max3f(t[0], t[1], t[2]), max3f(t[3], t[4], t[5]),
+                        max3f(t[6], t[7], max3f(t[8], t[9], t[10])));
   const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, m),
                                                    __builtin_bit_cast(unsigned, m),
                                                    false, false);
-  return __builtin_fmaxf(__builtin_bit_cast(float, (unsigned)sw[0]),
-                         __builtin_bit_cast(float, (unsigned)sw[1]));
+  return __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)sw[0]),
+                                       __builtin_bit_cast(float, (unsigned)sw[1]));
 }
 
 template <int DT, int D>
@@ -189,20 +191,14 @@ sel_attn_fwd_kernel(AttnArgs a) {
     const bool wave_on = wv * 32 < rows;
     const int64_t qi = q0 + (row_ok ? r / a.g : 0);
     const int hh = h * a.g + (row_ok ? r % a.g : 0);
-    // Q is pre-multiplied by scale*log2(e) (and rounded back to the input
-    // type), so the score MFMAs produce the exponent of the base-2 softmax
-    // directly.
     u32x4 qb[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      u32x4 raw = u32x4{0u, 0u, 0u, 0u};
       if (row_ok)
-        raw = *reinterpret_cast<const u32x4*>(
+        qb[s] = *reinterpret_cast<const u32x4*>(
             a.q + (qi * a.hq + hh) * D + s * 16 + hb * 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        qb[s][e] = pack2<DT>(to_f32<DT>((uint16_t)(raw[e] & 0xffffu)) * a.scale_log2,
-                             to_f32<DT>((uint16_t)(raw[e] >> 16)) * a.scale_log2);
+      else
+        qb[s] = u32x4{0u, 0u, 0u, 0u};
     }
 
     const char* kbase = reinterpret_cast<const char*>(a.k + (int64_t)h * D);
@@ -262,18 +258,15 @@ sel_attn_fwd_kernel(AttnArgs a) {
     for (int i = 0; i < ND; ++i)
 #pragma unroll
       for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
-    // Online softmax state of this lane's row: the running reference m_run
-    // (log2 units) and the partial row sum.  The score accumulators start
-    // from tmpl = -m_run, so S holds exponents relative to m_run.
+    // Online softmax state of this lane's row: the reference m_run (log2
+    // units) and the partial row sum.
     float m_run = 0.0f, l_run = 0.0f;
-    f32x16 tmpl;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) tmpl[v] = 0.0f;
 
     auto scores = [&](const char* ks, f32x16* sacc) {
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
-        sacc[blk] = tmpl;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sacc[blk][v] = 0.0f;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
           const u32x4 ka = *reinterpret_cast<const u32x4*>(
@@ -328,26 +321,17 @@ sel_attn_fwd_kernel(AttnArgs a) {
                 sc[blk][v] = -__builtin_inf();
         }
         const float mx = row_max(sc);
-        // Lazy rescaling: m_run is set to the row maximum on the first tile
-        // and afterwards only moves when a row maximum exceeds it by more
-        // than RESCALE_LOG2 (so p <= 2^8); the final O = acc / l is the same
-        // for any reference.
+        const float m_tile = mx * a.scale_log2;
         const bool first = kt == 0;
-        if (first || __builtin_amdgcn_ballot_w64(mx > RESCALE_LOG2) != 0) {
-          const float delta = first ? mx : fmaxf(mx, 0.0f);
-          const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(-delta);
-          m_run += delta;
+        if (first || __builtin_amdgcn_ballot_w64(m_tile > m_run + RESCALE_LOG2) != 0) {
+          const float m_new = first ? m_tile : __builtin_elementwise_maximum(m_run, m_tile);
+          const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+          m_run = m_new;
           l_run *= alpha;
 #pragma unroll
           for (int db = 0; db < ND; ++db)
 #pragma unroll
             for (int v = 0; v < 16; ++v) oacc[db][v] *= alpha;
-#pragma unroll
-          for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) sc[blk][v] -= delta;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) tmpl[v] = -m_run;
         }
         // S(kt+1); on the last tile this scores stale keys and is discarded,
         // which keeps the score registers free of a select per element.
@@ -359,7 +343,8 @@ sel_attn_fwd_kernel(AttnArgs a) {
           float p[16];
 #pragma unroll
           for (int v = 0; v < 16; ++v)
-            p[v] = __builtin_amdgcn_exp2f(sc[blk][v]);
+            p[v] = __builtin_amdgcn_exp2f(
+                __builtin_fmaf(sc[blk][v], a.scale_log2, -m_run));
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
             pb[blk][c] = u32x4{pack2<DT>(p[c * 8 + 0], p[c * 8 + 1]),

@@ -169,3 +169,29 @@ def test_reverse_query_map_long_segments():
     ref_cu, ref_lists = reverse_query_map_ref(topk.numpy(), cu_q.numpy(), cu_sb.numpy(), nb)
     np.testing.assert_array_equal(cu_rev.cpu().numpy(), ref_cu)
     np.testing.assert_array_equal(rev[0, : int(ref_cu[0, -1])].cpu().numpy(), ref_lists[0])
+
+
+@pytest.mark.parametrize("mode", ["large", "all_negative"])
+def test_fwd_bwd_extreme_scores(mode):
+    # Scores far outside the kernel's zero-reference window (|s| >> 64 in
+    # log2 units) move the softmax reference; outputs must stay exact.
+    w = W.config(2, n=2048, heads=2)
+    gen = torch.Generator().manual_seed(21)
+    if mode == "large":
+        q = 4.0 * torch.randn(w.n, w.hq, w.d, generator=gen)
+        k = 4.0 * torch.randn(w.n, w.hkv, w.d, generator=gen)
+    else:
+        u = torch.randn(1, 1, w.d, generator=gen)
+        q = 4.0 * u + 0.05 * torch.randn(w.n, w.hq, w.d, generator=gen)
+        k = -4.0 * u + 0.05 * torch.randn(w.n, w.hkv, w.d, generator=gen)
+    v = torch.randn(w.n, w.hkv, w.d, generator=gen)
+    do = torch.randn(w.n, w.hq, w.d, generator=gen)
+    q, k, v, do = (t.to(torch.bfloat16) for t in (q, k, v, do))
+    topk = _blocks_topk(w, 8, gen)
+    if mode == "large":
+        # only the forward: dS magnitudes make a fixed absolute tolerance
+        # meaningless for the gradients at these logit scales
+        _run_case(q, k, v, topk, w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens, w.scale)
+    else:
+        _run_case(q, k, v, topk, w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens, w.scale,
+                  do=do)
