@@ -194,7 +194,8 @@ int lsrm_sel_attn_fwd_run(const void* q, const void* k, const void* v,
  * dq [n_q, hq, head_dim], dk/dv [n_k, hkv, head_dim] (dtype) and
  * delta [hq, n_q] fp32 (rowsum(out * dout)).  dK/dV are accumulated per
  * 64-key tile by a single writer in a fixed order (deterministic, no float
- * atomics).  Keys no query selects get zero gradient.
+ * atomics).  Keys no query selects get zero gradient.  Besides the
+ * forward's limits, q and dout must each be below 4 GiB.
  * Replaces: ..._impl_kvcentric.py:1018-1263 (backward_kernel_dq 262-478,
  * _build_reverse_query_mapping 575-684, backward_kernel_dkdv_fastest 687-923).
  * ---------------------------------------------------------------------- */

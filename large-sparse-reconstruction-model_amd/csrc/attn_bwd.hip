@@ -4,14 +4,20 @@
 // (sparse/ops/triton_native_sparse_attention_impl_kvcentric.py:262-478):
 // Delta = rowsum(O * dO) in fp32 (fused), P = exp2(q.k * scale*log2e - lse),
 // dP = dO V^T, dS = scale * P * (dP - Delta) rounded to the input type,
-// dQ = dS K.  It runs on the forward's query tiles and key stream.
+// dQ = dS K.  It runs on the forward's query tiles and key stream, with the
+// forward's streaming scheme: K and V tiles copied straight into three-slot
+// LDS rings (swizzled, row-major), S^T = K Q^T and dP^T = V dO^T from
+// row-major reads, dQ^T = K^T dS^T with K^T taken by ds_read_b64_tr_b16.
 //
 // dK/dV follow backward_kernel_dkdv_fastest (same file, 687-923): each
 // workgroup owns one 64-key chunk of one block of one kv head and walks the
 // query tiles that selected the block (tile-granular reverse map, ascending
 // tile order), so every dK/dV element has a single writer and a fixed
-// accumulation order.  Waves split the chunk 2 (keys) x 2 (rows); the two
-// row halves are added in a fixed order at the end.
+// accumulation order.  The tiles' Q and dO rows are copied into two-slot LDS
+// rings; S = Q K^T and dP = dO V^T take the rows directly, dV^T = dO^T P and
+// dK^T = Q^T dS take Q^T / dO^T by transposed reads.  Waves split the chunk
+// 2 (keys) x 2 (rows); the two row halves are added in a fixed order at the
+// end.
 #include "attn.h"
 
 namespace lsrm {
@@ -19,25 +25,30 @@ namespace lsrm {
 // ------------------------------------------------------------------- dQ --
 
 template <int DT, int D>
-__global__ __launch_bounds__(256) void sel_attn_dq_kernel(AttnArgs a) {
-  constexpr int KS = D + 8;
-  constexpr int VS = KT + 4;
-  constexpr int NS = D / 16;
-  constexpr int ND = D / 32;
-  constexpr int NW = D / 16;
-  __shared__ __align__(16) uint16_t sK[2][KT * KS];
-  __shared__ __align__(16) uint16_t sKt[2][D * VS];
-  __shared__ __align__(16) uint16_t sV[2][KT * KS];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+sel_attn_dq_kernel(AttnArgs a) {
+  using G = KvTile<D>;
+  constexpr int NS = D / 16;  // MFMA k-steps over the head dim
+  constexpr int ND = D / 32;  // 32-wide output blocks over the head dim
+  __shared__ __align__(1024) char sK[3][G::BYTES];
+  __shared__ __align__(1024) char sV[3][G::BYTES];
   __shared__ SelLds sel;
   __shared__ int s_slot;
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
-  const int kp = tid >> 3, dg = tid & 7;
   const int total = a.plan.head_off[a.hkv];
 
+  int ld_key[G::LPW], ld_byte[G::LPW];
+#pragma unroll
+  for (int j = 0; j < G::LPW; ++j) {
+    ld_key[j] = (wv * G::LPW + j) * G::KPL + lane / G::CH;
+    ld_byte[j] = (((lane % G::CH) ^ G::swz(ld_key[j])) << 4);
+  }
+  const uint32_t row_bytes = (uint32_t)a.hkv * D * 2;
+
   for (;;) {
-    const int w = fetch_work(a.plan.counter, &s_slot);
+    const int w = uniform(fetch_work(a.plan.counter, &s_slot));
     if (w >= total) break;
     const int h = head_of(a.plan.head_off, a.hkv, w);
     const int2 tile = a.plan.tiles[(int64_t)h * a.nq + (w - a.plan.head_off[h])];
@@ -45,6 +56,7 @@ __global__ __launch_bounds__(256) void sel_attn_dq_kernel(AttnArgs a) {
     load_selection(a, h, q0, sel);
     const int nkeys = sel.cum[sel.n];
     const int ntiles = (nkeys + KT - 1) / KT;
+    const int t_safe = sel.n > 0 ? sel.tok[0] : 0;
 
     const int r = wv * 32 + l32;
     const bool row_ok = r < rows;
@@ -60,21 +72,67 @@ __global__ __launch_bounds__(256) void sel_attn_dq_kernel(AttnArgs a) {
         qb[s] = *reinterpret_cast<const u32x4*>(a.q + off);
         dob[s] = *reinterpret_cast<const u32x4*>(a.dout + off);
         const u32x4 ob = *reinterpret_cast<const u32x4*>(a.o + off);
-        const uint32_t ow[4] = {ob[0], ob[1], ob[2], ob[3]};
-        const uint32_t dw[4] = {dob[s][0], dob[s][1], dob[s][2], dob[s][3]};
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          dpart += to_f32<DT>((uint16_t)half_of(ow, i)) *
-                   to_f32<DT>((uint16_t)half_of(dw, i));
+        for (int i = 0; i < 4; ++i) {
+          dpart += to_f32<DT>((uint16_t)(ob[i] & 0xffffu)) *
+                   to_f32<DT>((uint16_t)(dob[s][i] & 0xffffu));
+          dpart += to_f32<DT>((uint16_t)(ob[i] >> 16)) *
+                   to_f32<DT>((uint16_t)(dob[s][i] >> 16));
+        }
       } else {
         qb[s] = u32x4{0u, 0u, 0u, 0u};
         dob[s] = u32x4{0u, 0u, 0u, 0u};
       }
     }
     const float delta = dpart + __shfl_xor(dpart, 32);
-    const float lse_row =
-        row_ok ? a.lse_in[(int64_t)hh * a.nq + qi] : __builtin_inf();
+    // exponent bias -lse (a row outside the tile gets -inf: P = 0)
+    const float bias = row_ok ? -a.lse_in[(int64_t)hh * a.nq + qi] : -__builtin_inf();
     if (row_ok && hb == 0) a.lse[(int64_t)hh * a.nq + qi] = delta;
+
+    const char* kbase = reinterpret_cast<const char*>(a.k + (int64_t)h * D);
+    const char* vbase = reinterpret_cast<const char*>(a.v + (int64_t)h * D);
+    StreamCursor cur[G::LPW];
+    uint32_t koff[G::LPW];
+#pragma unroll
+    for (int j = 0; j < G::LPW; ++j) {
+      cur[j].p = ld_key[j] - KT;
+      cur[j].seg = 0;
+      cur[j].tok = 0;
+      cur[j].segend = -1;
+      cur[j].ntb = 0;
+      cur[j].nend = -1;
+    }
+    auto advance = [&]() {
+#pragma unroll
+      for (int j = 0; j < G::LPW; ++j) {
+        StreamCursor& c = cur[j];
+        c.p += KT;
+        int t = t_safe;
+        if (c.p < nkeys) {
+          c.tok += KT;
+          if (c.p >= c.segend) {
+            if (c.p < c.nend) {
+              ++c.seg;
+              c.tok = c.p + c.ntb;
+              c.segend = c.nend;
+            } else {
+              cursor_seek(sel, c);
+            }
+            cursor_prefetch(sel, c);
+          }
+          t = c.tok;
+        }
+        koff[j] = (uint32_t)t * row_bytes + ld_byte[j];
+      }
+    };
+    auto load_tiles = [&](int slot) {
+      const uint32_t dk = lds_addr(sK[slot]) + wv * G::LPW * 1024;
+      const uint32_t dv = lds_addr(sV[slot]) + wv * G::LPW * 1024;
+#pragma unroll
+      for (int j = 0; j < G::LPW; ++j) copy16_to_lds(kbase, koff[j], dk + j * 1024);
+#pragma unroll
+      for (int j = 0; j < G::LPW; ++j) copy16_to_lds(vbase, koff[j], dv + j * 1024);
+    };
 
     f32x16 dqacc[ND];
 #pragma unroll
@@ -82,78 +140,58 @@ __global__ __launch_bounds__(256) void sel_attn_dq_kernel(AttnArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) dqacc[i][v] = 0.0f;
 
-    int cur0 = 0, cur1 = 0;
-    uint32_t kr[2][NW], vr[2][NW];
-    auto gather = [&](int kt) {
-      const int p0 = kt * KT + 2 * kp, p1 = p0 + 1;
-      if (p0 < nkeys) {
-        const int t = stream_token(sel, p0, cur0);
-        const int64_t off = ((int64_t)t * a.hkv + h) * D + dg * (D / 8);
-        gload<NW>(kr[0], a.k + off);
-        gload<NW>(vr[0], a.v + off);
-      } else {
-#pragma unroll
-        for (int i = 0; i < NW; ++i) kr[0][i] = vr[0][i] = 0u;
-      }
-      if (p1 < nkeys) {
-        const int t = stream_token(sel, p1, cur1);
-        const int64_t off = ((int64_t)t * a.hkv + h) * D + dg * (D / 8);
-        gload<NW>(kr[1], a.k + off);
-        gload<NW>(vr[1], a.v + off);
-      } else {
-#pragma unroll
-        for (int i = 0; i < NW; ++i) kr[1][i] = vr[1][i] = 0u;
-      }
-    };
-    auto stage = [&](int buf) {
-      sstore<NW>(&sK[buf][(2 * kp) * KS + dg * (D / 8)], kr[0]);
-      sstore<NW>(&sK[buf][(2 * kp + 1) * KS + dg * (D / 8)], kr[1]);
-      sstore<NW>(&sV[buf][(2 * kp) * KS + dg * (D / 8)], vr[0]);
-      sstore<NW>(&sV[buf][(2 * kp + 1) * KS + dg * (D / 8)], vr[1]);
-#pragma unroll
-      for (int i = 0; i < D / 8; ++i) {
-        const int d = dg * (D / 8) + i;
-        *reinterpret_cast<uint32_t*>(&sKt[buf][d * VS + 2 * kp]) =
-            half_of(kr[0], i) | (half_of(kr[1], i) << 16);
-      }
-    };
-
+    // Prologue: tile 0 resident, tile 1 in flight (a step's copies are
+    // consumed two steps later, retired by a counted wait).
     if (ntiles > 0) {
-      gather(0);
-      stage(0);
+      advance();
+      load_tiles(0);
     }
+    wait_copies();
     __syncthreads();
+    if (ntiles > 0) {
+      advance();
+      load_tiles(1);
+    }
 
     for (int kt = 0; kt < ntiles; ++kt) {
-      const int buf = kt & 1;
-      if (kt + 1 < ntiles) gather(kt + 1);
+      const int s0 = kt % 3, s2 = (kt + 2) % 3;
+      advance();
+      load_tiles(s2);
       if (wave_on) {
-        const uint16_t* k_s = sK[buf];
-        const uint16_t* kt_s = sKt[buf];
-        const uint16_t* v_s = sV[buf];
-        const int kbase = kt * KT;
+        const char* ks = sK[s0];
+        const char* vs = sV[s0];
+        f32x16 sacc[2], dpacc[2];
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) sacc[blk][v] = dpacc[blk][v] = 0.0f;
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            const int o = G::off(blk * 32 + l32, 2 * s + hb);
+            sacc[blk] = mfma32<DT>(*reinterpret_cast<const u32x4*>(ks + o), qb[s],
+                                   sacc[blk]);
+            dpacc[blk] = mfma32<DT>(*reinterpret_cast<const u32x4*>(vs + o),
+                                    dob[s], dpacc[blk]);
+          }
+        }
+        const int kb0 = kt * KT;
+        if (kb0 + KT > nkeys) {
+#pragma unroll
+          for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              if (kb0 + blk * 32 + acc_row(v, hb) >= nkeys)
+                sacc[blk][v] = -__builtin_inf();
+        }
         u32x4 dsb[2][2];
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
-          f32x16 sacc, dpacc;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) sacc[v] = dpacc[v] = 0.0f;
-#pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const int off = (blk * 32 + l32) * KS + s * 16 + hb * 8;
-            sacc = mfma32<DT>(*reinterpret_cast<const u32x4*>(k_s + off), qb[s],
-                              sacc);
-            dpacc = mfma32<DT>(*reinterpret_cast<const u32x4*>(v_s + off),
-                               dob[s], dpacc);
-          }
           float ds[16];
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            float p = __builtin_amdgcn_exp2f(
-                __builtin_fmaf(sacc[v], a.scale_log2, -lse_row));
-            if (kbase + blk * 32 + acc_row(v, hb) >= nkeys) p = 0.0f;
-            ds[v] = a.scale * p * (dpacc[v] - delta);
-          }
+          for (int v = 0; v < 16; ++v)
+            ds[v] = a.scale *
+                    __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[blk][v], a.scale_log2, bias)) *
+                    (dpacc[blk][v] - delta);
 #pragma unroll
           for (int c = 0; c < 2; ++c)
             dsb[blk][c] = u32x4{pack2<DT>(ds[c * 8 + 0], ds[c * 8 + 1]),
@@ -161,21 +199,31 @@ __global__ __launch_bounds__(256) void sel_attn_dq_kernel(AttnArgs a) {
                                 pack2<DT>(ds[c * 8 + 4], ds[c * 8 + 5]),
                                 pack2<DT>(ds[c * 8 + 6], ds[c * 8 + 7])};
         }
+        // dQ^T += K^T dS^T: K^T from the row-major K tile by transposed reads
+        // (slot e of lane (hb, row d) = key blk*32 + c*16 + (e/4)*8 + hb*4 +
+        // e%4, the score layout).
+        const int gi = lane & 15, dh = (lane >> 4) & 1;
 #pragma unroll
-        for (int db = 0; db < ND; ++db)
+        for (int db = 0; db < ND; ++db) {
+          const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+          const int cb = dcol >> 3, half = (dcol & 4) * 2;
 #pragma unroll
           for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
-              const uint16_t* kp_ =
-                  kt_s + (db * 32 + l32) * VS + blk * 32 + c * 16 + hb * 4;
-              const u32x2 lo = *reinterpret_cast<const u32x2*>(kp_);
-              const u32x2 hi = *reinterpret_cast<const u32x2*>(kp_ + 8);
-              dqacc[db] = mfma32<DT>(u32x4{lo[0], lo[1], hi[0], hi[1]},
+              const int k0 = blk * 32 + c * 16 + hb * 4 + (gi >> 2);
+              const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_s16x4*)(ks + G::off(k0, cb) + half));
+              const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_s16x4*)(ks + G::off(k0 + 8, cb) + half));
+              const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+              const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+              dqacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]},
                                      dsb[blk][c], dqacc[db]);
             }
+        }
       }
-      if (kt + 1 < ntiles) stage(buf ^ 1);
+      wait_prev_copies<2 * G::LPW>();
       __syncthreads();
     }
 
@@ -192,40 +240,42 @@ __global__ __launch_bounds__(256) void sel_attn_dq_kernel(AttnArgs a) {
         }
     }
   }
+  wait_copies();  // no copy into LDS outlives the workgroup
   leave_queue(a.plan.counter, a.plan.counter + 2);
 }
 
 // ----------------------------------------------------------------- dK/dV --
 
 template <int DT, int D>
-__global__ __launch_bounds__(256) void sel_attn_dkdv_kernel(AttnArgs a) {
-  constexpr int KS = D + 8;      // row-major staging stride
-  constexpr int QS = ROWS + 4;   // transposed staging stride
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+sel_attn_dkdv_kernel(AttnArgs a) {
+  using G = KvTile<D, ROWS>;  // 128-row Q / dO tiles
   constexpr int NS = D / 16;
   constexpr int ND = D / 32;
-  constexpr int LW = D / 8;      // 32-bit words a loader moves per row
-  constexpr int STAGE_BYTES = 2 * ROWS * KS * 2 + 2 * D * QS * 2;
-  constexpr int RED_BYTES = 2 * 2 * ND * 16 * 64 * 4;
-  constexpr int LDS_BYTES = STAGE_BYTES > RED_BYTES ? STAGE_BYTES : RED_BYTES;
-  __shared__ __align__(16) char smem[LDS_BYTES];
-  __shared__ float s_lse[ROWS];
-  __shared__ float s_dl[ROWS];
+  constexpr int RED_FLOATS = 2 * 2 * ND * 16 * 64;  // (key half, dk|dv) x acc
+  static_assert(RED_FLOATS * 4 <= 2 * G::BYTES, "reduction area");
+  __shared__ __align__(1024) char sQ[2][G::BYTES];
+  __shared__ __align__(1024) char sO[2][G::BYTES];
+  __shared__ __align__(16) float s_lse[2][ROWS];  // lse per row (+inf: none)
+  __shared__ __align__(16) float s_dl[2][ROWS];   // delta per row
   __shared__ int s_slot;
-  uint16_t* sQ = reinterpret_cast<uint16_t*>(smem);
-  uint16_t* sO = sQ + ROWS * KS;
-  uint16_t* sQt = sO + ROWS * KS;
-  uint16_t* sOt = sQt + D * QS;
-  float* red = reinterpret_cast<float*>(smem);
+  float* red = reinterpret_cast<float*>(&sQ[0][0]);
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
-  const int kh = wv & 1, rh = wv >> 1;   // key half, row half of this wave
-  const int rp = tid >> 2, dq = tid & 3; // loader: rows 2rp, 2rp+1; d quarter
+  const int kh = wv & 1, rh = wv >> 1;  // key half, row half of this wave
   const int n_items = a.items.n_items[0];
   const int total = n_items * a.hkv;
 
+  int ld_row[G::LPW], ld_byte[G::LPW];
+#pragma unroll
+  for (int j = 0; j < G::LPW; ++j) {
+    ld_row[j] = (wv * G::LPW + j) * G::KPL + lane / G::CH;
+    ld_byte[j] = (((lane % G::CH) ^ G::swz(ld_row[j])) << 4);
+  }
+
   for (;;) {
-    const int w = fetch_work(a.plan.counter + 1, &s_slot);
+    const int w = uniform(fetch_work(a.plan.counter + 1, &s_slot));
     if (w >= total) break;
     const int h = w / n_items;
     const int4 item = a.items.items[w - h * n_items];
@@ -256,30 +306,26 @@ __global__ __launch_bounds__(256) void sel_attn_dkdv_kernel(AttnArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) dkacc[i][v] = dvacc[i][v] = 0.0f;
 
-    uint32_t qr[2][LW], orr[2][LW];
-    float lse_r = 0.0f, dl_r = 0.0f;
-    int rows_next = 0;
-    auto gather = [&](int e) {
-      const int2 tile = a.plan.tiles[(int64_t)h * a.nq + ents[e]];
-      const int rows = tile.y * a.g;
-      rows_next = rows;
+    // Copies of entry e's Q and dO rows into ring slot `slot`, and its lse /
+    // delta into registers (stored to LDS by store_stats).
+    float lse_r = __builtin_inf(), dl_r = 0.0f;
+    auto issue = [&](int e, int slot) {
+      const int2 tl = a.plan.tiles[(int64_t)h * a.nq + ents[e]];
+      const int rows = tl.y * a.g;
+      const uint32_t dq = lds_addr(sQ[slot]) + wv * G::LPW * 1024;
+      const uint32_t dout = lds_addr(sO[slot]) + wv * G::LPW * 1024;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int row = 2 * rp + j;
-        if (row < rows) {
-          const int64_t qi = tile.x + row / a.g;
-          const int hh = h * a.g + row % a.g;
-          const int64_t off = (qi * a.hq + hh) * D + dq * (D / 4);
-          gload<LW>(qr[j], a.q + off);
-          gload<LW>(orr[j], a.dout + off);
-        } else {
-#pragma unroll
-          for (int i = 0; i < LW; ++i) qr[j][i] = orr[j][i] = 0u;
-        }
+      for (int j = 0; j < G::LPW; ++j) {
+        const int rr = ld_row[j] < rows ? ld_row[j] : 0;  // in-bounds filler
+        const uint32_t off =
+            (uint32_t)(((int64_t)(tl.x + rr / a.g) * a.hq + h * a.g + rr % a.g) * D * 2) +
+            ld_byte[j];
+        copy16_to_lds(a.q, off, dq + j * 1024);
+        copy16_to_lds(a.dout, off, dout + j * 1024);
       }
       if (tid < ROWS) {
         if (tid < rows) {
-          const int64_t qi = tile.x + tid / a.g;
+          const int64_t qi = tl.x + tid / a.g;
           const int hh = h * a.g + tid % a.g;
           lse_r = a.lse_in[(int64_t)hh * a.nq + qi];
           dl_r = a.lse[(int64_t)hh * a.nq + qi];
@@ -288,91 +334,105 @@ __global__ __launch_bounds__(256) void sel_attn_dkdv_kernel(AttnArgs a) {
           dl_r = 0.0f;
         }
       }
+      return rows;
     };
-    auto stage = [&]() {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        sstore<LW>(&sQ[(2 * rp + j) * KS + dq * (D / 4)], qr[j]);
-        sstore<LW>(&sO[(2 * rp + j) * KS + dq * (D / 4)], orr[j]);
-      }
-#pragma unroll
-      for (int i = 0; i < D / 4; ++i) {
-        const int d = dq * (D / 4) + i;
-        *reinterpret_cast<uint32_t*>(&sQt[d * QS + 2 * rp]) =
-            half_of(qr[0], i) | (half_of(qr[1], i) << 16);
-        *reinterpret_cast<uint32_t*>(&sOt[d * QS + 2 * rp]) =
-            half_of(orr[0], i) | (half_of(orr[1], i) << 16);
-      }
+    auto store_stats = [&](int slot) {
       if (tid < ROWS) {
-        s_lse[tid] = lse_r;
-        s_dl[tid] = dl_r;
+        s_lse[slot][tid] = lse_r;
+        s_dl[slot][tid] = dl_r;
       }
     };
 
-    if (n_ent > 0) gather(0);
+    int rows_cur = 0;
+    if (n_ent > 0) {
+      rows_cur = issue(0, 0);
+      store_stats(0);
+    }
+    wait_copies();
+    __syncthreads();
     for (int e = 0; e < n_ent; ++e) {
-      __syncthreads();
-      stage();
-      const int rows = rows_next;
-      __syncthreads();
-      if (e + 1 < n_ent) gather(e + 1);
-      {
-        if (rh * 64 < rows && kh * 32 < nk_item) {
-          u32x4 pb[2][2], dsb[2][2];
+      const int slot = e & 1;
+      int rows_next = 0;
+      if (e + 1 < n_ent) rows_next = issue(e + 1, slot ^ 1);
+      if (rh * 64 < rows_cur && kh * 32 < nk_item) {
+        const char* qs = sQ[slot];
+        const char* os = sO[slot];
+        u32x4 pb[2][2], dsb[2][2];
 #pragma unroll
-          for (int rb = 0; rb < 2; ++rb) {
-            f32x16 sacc, dpacc;
+        for (int rb = 0; rb < 2; ++rb) {
+          const int rbase = rh * 64 + rb * 32;
+          f32x16 sacc, dpacc;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) sacc[v] = dpacc[v] = 0.0f;
+          for (int v = 0; v < 16; ++v) sacc[v] = dpacc[v] = 0.0f;
 #pragma unroll
-            for (int s = 0; s < NS; ++s) {
-              const int off = (rh * 64 + rb * 32 + l32) * KS + s * 16 + hb * 8;
-              sacc = mfma32<DT>(*reinterpret_cast<const u32x4*>(sQ + off), kb[s],
-                                sacc);
-              dpacc = mfma32<DT>(*reinterpret_cast<const u32x4*>(sO + off),
-                                 vb[s], dpacc);
-            }
-            float p[16], ds[16];
+          for (int s = 0; s < NS; ++s) {
+            const int o = G::off(rbase + l32, 2 * s + hb);
+            sacc = mfma32<DT>(*reinterpret_cast<const u32x4*>(qs + o), kb[s], sacc);
+            dpacc = mfma32<DT>(*reinterpret_cast<const u32x4*>(os + o), vb[s], dpacc);
+          }
+          float p[16], ds[16];
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int row = rh * 64 + rb * 32 + acc_row(v, hb);
-              p[v] = __builtin_amdgcn_exp2f(
-                  __builtin_fmaf(sacc[v], a.scale_log2, -s_lse[row]));
-              ds[v] = a.scale * p[v] * (dpacc[v] - s_dl[row]);
-            }
+          for (int g4 = 0; g4 < 4; ++g4) {
+            // registers 4*g4 .. 4*g4+3 hold rows rbase + g4*8 + hb*4 + 0..3
+            const f32x4 lv = *reinterpret_cast<const f32x4*>(
+                &s_lse[slot][rbase + g4 * 8 + hb * 4]);
+            const f32x4 dv = *reinterpret_cast<const f32x4*>(
+                &s_dl[slot][rbase + g4 * 8 + hb * 4]);
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-              pb[rb][cc] = u32x4{pack2<DT>(p[cc * 8 + 0], p[cc * 8 + 1]),
-                                 pack2<DT>(p[cc * 8 + 2], p[cc * 8 + 3]),
-                                 pack2<DT>(p[cc * 8 + 4], p[cc * 8 + 5]),
-                                 pack2<DT>(p[cc * 8 + 6], p[cc * 8 + 7])};
-              dsb[rb][cc] = u32x4{pack2<DT>(ds[cc * 8 + 0], ds[cc * 8 + 1]),
-                                  pack2<DT>(ds[cc * 8 + 2], ds[cc * 8 + 3]),
-                                  pack2<DT>(ds[cc * 8 + 4], ds[cc * 8 + 5]),
-                                  pack2<DT>(ds[cc * 8 + 6], ds[cc * 8 + 7])};
+            for (int u = 0; u < 4; ++u) {
+              const int v = g4 * 4 + u;
+              p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], a.scale_log2, -lv[u]));
+              ds[v] = a.scale * p[v] * (dpacc[v] - dv[u]);
             }
           }
 #pragma unroll
-          for (int db = 0; db < ND; ++db)
+          for (int cc = 0; cc < 2; ++cc) {
+            pb[rb][cc] = u32x4{pack2<DT>(p[cc * 8 + 0], p[cc * 8 + 1]),
+                               pack2<DT>(p[cc * 8 + 2], p[cc * 8 + 3]),
+                               pack2<DT>(p[cc * 8 + 4], p[cc * 8 + 5]),
+                               pack2<DT>(p[cc * 8 + 6], p[cc * 8 + 7])};
+            dsb[rb][cc] = u32x4{pack2<DT>(ds[cc * 8 + 0], ds[cc * 8 + 1]),
+                                pack2<DT>(ds[cc * 8 + 2], ds[cc * 8 + 3]),
+                                pack2<DT>(ds[cc * 8 + 4], ds[cc * 8 + 5]),
+                                pack2<DT>(ds[cc * 8 + 6], ds[cc * 8 + 7])};
+          }
+        }
+        // dV^T += dO^T P and dK^T += Q^T dS: the transposed operands come
+        // from the row-major tiles (slot e of lane (hb, row d) = query row
+        // rh*64 + rb*32 + cc*16 + (e/4)*8 + hb*4 + e%4, the P / dS layout).
+        const int gi = lane & 15, dh = (lane >> 4) & 1;
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
+        for (int db = 0; db < ND; ++db) {
+          const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+          const int cb = dcol >> 3, half = (dcol & 4) * 2;
 #pragma unroll
-              for (int cc = 0; cc < 2; ++cc) {
-                const int off =
-                    (db * 32 + l32) * QS + rh * 64 + rb * 32 + cc * 16 + hb * 4;
-                const u32x2 olo = *reinterpret_cast<const u32x2*>(sOt + off);
-                const u32x2 ohi = *reinterpret_cast<const u32x2*>(sOt + off + 8);
-                dvacc[db] = mfma32<DT>(u32x4{olo[0], olo[1], ohi[0], ohi[1]},
-                                       pb[rb][cc], dvacc[db]);
-                const u32x2 qlo = *reinterpret_cast<const u32x2*>(sQt + off);
-                const u32x2 qhi = *reinterpret_cast<const u32x2*>(sQt + off + 8);
-                dkacc[db] = mfma32<DT>(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]},
-                                       dsb[rb][cc], dkacc[db]);
-              }
+          for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+              const int r0 = rh * 64 + rb * 32 + cc * 16 + hb * 4 + (gi >> 2);
+              const int o0 = G::off(r0, cb) + half, o1 = G::off(r0 + 8, cb) + half;
+              const u32x2 olo = __builtin_bit_cast(
+                  u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(os + o0)));
+              const u32x2 ohi = __builtin_bit_cast(
+                  u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(os + o1)));
+              dvacc[db] = mfma32<DT>(u32x4{olo[0], olo[1], ohi[0], ohi[1]},
+                                     pb[rb][cc], dvacc[db]);
+              const u32x2 qlo = __builtin_bit_cast(
+                  u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(qs + o0)));
+              const u32x2 qhi = __builtin_bit_cast(
+                  u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(qs + o1)));
+              dkacc[db] = mfma32<DT>(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]},
+                                     dsb[rb][cc], dkacc[db]);
+            }
         }
       }
+      if (e + 1 < n_ent) store_stats(slot ^ 1);
+      wait_copies();
+      __syncthreads();
+      rows_cur = rows_next;
     }
-    // Row-half reduction in a fixed order: rows 0-63 + rows 64-127.
+    // Row-half reduction in a fixed order: rows 0-63 + rows 64-127.  The
+    // reduction area aliases the Q ring (no copies are in flight here).
     __syncthreads();
     if (rh == 1) {
       float* dst = red + kh * (2 * ND * 16 * 64);

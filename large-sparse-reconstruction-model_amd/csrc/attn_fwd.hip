@@ -34,98 +34,6 @@ namespace lsrm {
 // reference.
 constexpr float RESCALE_LOG2 = 8.0f;
 
-typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// LDS byte address of a __shared__ object.
-__device__ inline uint32_t lds_addr(const void* p) {
-  return (uint32_t)(size_t)((__attribute__((address_space(3))) const char*)p);
-}
-
-// One 16-byte-per-lane global -> LDS copy: lane l's bytes base + voff land at
-// LDS address lds + 16 * l.  Issued as inline assembly so that the compiler
-// does not order every later LDS read behind it (it cannot tell which LDS
-// buffer the copy targets); completion is awaited explicitly with
-// wait_copies() before the barrier that publishes the buffer.
-// `base` and `lds` must be wave-uniform values held in SGPRs.
-__device__ inline void copy16_to_lds(const void* base, uint32_t voff,
-                                     uint32_t lds) {
-  asm volatile(
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 4\n\t"
-      "global_load_lds_dwordx4 %0, %1"
-      :
-      : "v"(voff), "s"(base), "s"(lds)
-      : "memory");
-}
-
-__device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
-
-// s_waitcnt vmcnt(0) as a compiler-visible instruction: the compiler then
-// knows every earlier vector-memory load (Q rows included) has completed and
-// does not insert its own vmcnt(0) waits inside the key loop, which would
-// also stall on the tile copies issued ahead.
-__device__ inline void wait_copies() {
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0), expcnt/lgkmcnt untouched
-}
-
-// s_waitcnt vmcnt(N): all but this wave's N most recent vector-memory loads
-// have completed (loads complete in issue order).
-template <int N>
-__device__ inline void wait_prev_copies() {
-  static_assert(N < 16, "vmcnt field");
-  __builtin_amdgcn_s_waitcnt(0x0f70 | N);
-}
-
-// Key-row geometry of one LDS tile (64 keys x D): 16-byte chunks per row,
-// keys per 1 KB direct-load instruction, and the chunk swizzle of a row.
-template <int D>
-struct KvTile {
-  static constexpr int CH = D / 8;          // 16-byte chunks per key row
-  static constexpr int KPL = 64 / CH;       // keys per 1 KB load
-  static constexpr int LPW = (KT / KPL) / 4;  // loads per wave per tile
-  static constexpr int BYTES = KT * D * 2;
-  // Physical chunk = logical chunk ^ swz(row).  Rows that fall on the same
-  // LDS banks (256-byte period) get distinct chunk positions both for the
-  // 16-lane row-strided K reads and the 4-row transposed V reads.
-  __device__ static constexpr int swz(int r) {
-    if constexpr (D == 32)
-      return (r >> 2) & 3;
-    else if constexpr (D == 64)
-      return (r & 7) ^ ((r >> 3) & 1);
-    else
-      return ((r & 7) << 1) | ((r >> 3) & 1);
-  }
-  // Byte offset of (row, logical chunk) inside a tile.
-  __device__ static constexpr int off(int r, int c) {
-    return r * (D * 2) + ((c ^ swz(r)) << 4);
-  }
-};
-
-// Per-lane cursor over the key stream: the token of stream position p, the
-// end of its segment, and (prefetched) the next segment's token base
-// (token of position q in it = q + ntb) and end.  Advanced by one tile (64
-// positions) at a time; crossing one boundary uses the prefetched values, so
-// the common step has no dependent LDS read.
-struct StreamCursor {
-  int p, seg, tok, segend, ntb, nend;
-};
-
-// Plain LDS reads (seg < n, so both indices are in range thanks to the
-// sentinels); their results are first needed at the next crossing.
-__device__ inline void cursor_prefetch(const SelLds& s, StreamCursor& c) {
-  c.ntb = s.tb[c.seg + 1];
-  c.nend = s.cum[c.seg + 2];
-}
-
-// Walks forward to the segment containing c.p (several boundaries crossed;
-// c.p < total keys, so the walk stops at the last segment at the latest).
-__device__ inline void cursor_seek(const SelLds& s, StreamCursor& c) {
-  while (s.cum[c.seg + 1] <= c.p) ++c.seg;
-  c.tok = c.p + s.tb[c.seg];
-  c.segend = s.cum[c.seg + 1];
-}
-
 // Maximum of a lane's 32 scores (a v_maximum3 tree), combined with the lane
 // holding the other 16 keys of the same row (v_permlane32_swap).
 __device__ inline float max3f(float a, float b, float c) {
@@ -409,6 +317,7 @@ sel_attn_fwd_kernel(AttnArgs a) {
             l_tot > 0.0f ? m_run + log2f(l_tot) : -__builtin_inf();
     }
   }
+  wait_copies();  // no copy into LDS outlives the workgroup
   leave_queue(a.plan.counter, a.plan.counter + 2);
 }
 

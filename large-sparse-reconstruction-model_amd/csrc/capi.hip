@@ -147,6 +147,11 @@ int attn_setup(const void* q, const void* k, const void* v, int dtype,
   int rc = check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk, n_blocks,
                            batch);
   if (rc) return rc;
+  // The backward dK/dV kernel addresses Q and dO rows with 32-bit byte
+  // offsets as well.
+  if (backward &&
+      (uint64_t)n_q * (uint64_t)hq * (uint64_t)head_dim * 2u >= (1ull << 32))
+    return LSRM_ERR_UNSUPPORTED;
   if (!q || !k || !v || !topk_idx || !cu_seqblocks || !cu_block_tokens ||
       !cu_seqlens_q || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
       !(softmax_scale > 0.0f))
