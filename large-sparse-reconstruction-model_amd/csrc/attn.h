@@ -42,6 +42,12 @@ struct AttnArgs {
   KeyItems items;    // backward: 64-key chunks of every block
 };
 
+// Compile-time value tag (e.g. a ring-slot phase).
+template <int V>
+struct Phase {
+  static constexpr int value = V;
+};
+
 // Valid selected blocks of one selection row, compacted, with the prefix of
 // their lengths (the key stream).
 struct SelLds {
@@ -281,6 +287,56 @@ __device__ inline void cursor_seek(const SelLds& s, StreamCursor& c) {
   while (s.cum[c.seg + 1] <= c.p) ++c.seg;
   c.tok = c.p + s.tb[c.seg];
   c.segend = s.cum[c.seg + 1];
+}
+
+// Wave-uniform cursor of one load group: the KPL consecutive stream
+// positions P .. P+KPL-1 that one 1 KB copy instruction of a wave covers (P
+// is wave-uniform).  The segment holding the group's last row -- index,
+// token base tb[seg] and end cum[seg+1] -- is kept in scalar registers, so a
+// group that lies inside that segment costs one vector add; a group that
+// crosses a boundary, or runs past the stream, takes the per-lane path.
+struct GroupCursor {
+  int seg, tbase, send;
+};
+
+__device__ inline void group_init(const SelLds& s, GroupCursor& c) {
+  c.seg = 0;
+  c.tbase = uniform(s.tb[0]);
+  c.send = uniform(s.cum[1]);  // INT_MAX sentinel when the stream is empty
+}
+
+// Byte offset of this lane's 16-byte piece for the group at stream position
+// P.  lane_row = lane's row in the group, lane_off = lane_row * row_bytes +
+// chunk_byte (precomputed).  Positions past the stream load token t_safe.
+// Groups must be visited in increasing P.
+template <int KPL>
+__device__ inline uint32_t group_offset(const SelLds& s, GroupCursor& c, int P,
+                                        int nkeys, int t_safe, uint32_t row_bytes,
+                                        int lane_row, uint32_t lane_off,
+                                        uint32_t chunk_byte) {
+  if (P + KPL <= c.send) {  // wave-uniform: the whole group is in segment c.seg
+    // Scalar row offset plus the lane's constant part: one vector add.
+    const uint32_t base = (uint32_t)uniform((int)((uint32_t)(P + c.tbase) * row_bytes));
+    return base + lane_off;
+  }
+  const int p = P + lane_row;
+  int tok = t_safe;
+  if (p < nkeys) {
+    int sg = c.seg;
+    while (s.cum[sg + 1] <= p) ++sg;  // stops at the last segment at latest
+    tok = p + s.tb[sg];
+  }
+  if (P < nkeys) {
+    // Advance the scalar state to the segment of the group's last row (the
+    // same scan on every lane, so the result is uniform).
+    const int last = (P + KPL - 1 < nkeys ? P + KPL - 1 : nkeys - 1);
+    int sg = c.seg;
+    while (s.cum[sg + 1] <= last) ++sg;
+    c.seg = uniform(sg);
+    c.tbase = uniform(s.tb[c.seg]);
+    c.send = uniform(s.cum[c.seg + 1]);
+  }
+  return (uint32_t)tok * row_bytes + chunk_byte;
 }
 
 }  // namespace lsrm

@@ -81,6 +81,10 @@ sel_attn_fwd_kernel(AttnArgs a) {
   // Bytes between consecutive tokens; K and V are below 4 GiB (checked by
   // the host), so token offsets fit 32 bits.
   const uint32_t row_bytes = (uint32_t)a.hkv * D * 2;
+  const int ld_row = lane / G::CH;  // row of this lane within a load group
+  uint32_t ld_lane_off[G::LPW];
+#pragma unroll
+  for (int j = 0; j < G::LPW; ++j) ld_lane_off[j] = (uint32_t)ld_row * row_bytes + ld_byte[j];
 
   for (;;) {
     const int w = uniform(fetch_work(a.plan.counter, &s_slot));
@@ -112,43 +116,23 @@ sel_attn_fwd_kernel(AttnArgs a) {
     const char* kbase = reinterpret_cast<const char*>(a.k + (int64_t)h * D);
     const char* vbase = reinterpret_cast<const char*>(a.v + (int64_t)h * D);
 
-    // Cursors of the K copies (three tiles ahead); the V copies (two tiles
-    // ahead) reuse the K offsets of the previous tile.
-    StreamCursor cur[G::LPW];
-    uint32_t koff[G::LPW], voff[G::LPW];
+    // Scalar cursors of the K copies (three tiles ahead, one per load
+    // group); the V copies (two tiles ahead) reuse the K offsets of the
+    // previous tile.
+    GroupCursor cur[G::LPW];
 #pragma unroll
-    for (int j = 0; j < G::LPW; ++j) {
-      cur[j].p = ld_key[j] - KT;  // advanced before first use
-      cur[j].seg = 0;
-      cur[j].tok = 0;
-      cur[j].segend = -1;         // forces a seek on the first advance
-      cur[j].ntb = 0;
-      cur[j].nend = -1;
-    }
-    // Moves every cursor to the next tile and returns the byte offsets of
-    // its keys' rows.
+    for (int j = 0; j < G::LPW; ++j) group_init(sel, cur[j]);
+    int ld_tile = 0;  // next tile whose K copies are issued
+    uint32_t koff[G::LPW], voff[G::LPW];
+    // Byte offsets of the rows of tile ld_tile for this lane's loads.
     auto advance = [&](uint32_t* off) {
 #pragma unroll
       for (int j = 0; j < G::LPW; ++j) {
-        StreamCursor& c = cur[j];
-        c.p += KT;
-        int t = t_safe;
-        if (c.p < nkeys) {
-          c.tok += KT;
-          if (c.p >= c.segend) {
-            if (c.p < c.nend) {  // exactly one boundary crossed
-              ++c.seg;
-              c.tok = c.p + c.ntb;
-              c.segend = c.nend;
-            } else {
-              cursor_seek(sel, c);
-            }
-            cursor_prefetch(sel, c);
-          }
-          t = c.tok;
-        }
-        off[j] = (uint32_t)t * row_bytes + ld_byte[j];
+        const int P = ld_tile * KT + (wv * G::LPW + j) * G::KPL;
+        off[j] = group_offset<G::KPL>(sel, cur[j], P, nkeys, t_safe, row_bytes,
+                                      ld_row, ld_lane_off[j], ld_byte[j]);
       }
+      ++ld_tile;
     };
     auto voff_keep = [&](const uint32_t* off) {
 #pragma unroll
@@ -211,8 +195,13 @@ sel_attn_fwd_kernel(AttnArgs a) {
     // ring slots last read one step earlier.  Every step issues the same
     // number of copies (positions past the stream load a resident token), so
     // one counted wait retires exactly the previous step's copies.
-    auto step = [&](int kt, f32x16* sc, f32x16* sn) {
-      const int s0 = kt % 3, s1 = (kt + 1) % 3, s2 = (kt + 2) % 3;
+    // `ph` is kt % 3 as a compile-time constant (ring slots then become
+    // immediate LDS offsets), or -1 to compute it at run time.
+    auto step = [&](auto ph, int kt, f32x16* sc, f32x16* sn) {
+      constexpr int PH = decltype(ph)::value;
+      const int s0 = PH >= 0 ? PH : kt % 3;
+      const int s1 = PH >= 0 ? (PH + 1) % 3 : (kt + 1) % 3;
+      const int s2 = PH >= 0 ? (PH + 2) % 3 : (kt + 2) % 3;
       advance(koff);
       load_tile(kbase, koff, sK[s0]);
       load_tile(vbase, voff, sV[s2]);
@@ -292,11 +281,19 @@ sel_attn_fwd_kernel(AttnArgs a) {
       __syncthreads();
     };
     int kt = 0;
-    for (; kt + 1 < ntiles; kt += 2) {
-      step(kt, sA, sB);
-      step(kt + 1, sB, sA);
+    for (; kt + 6 <= ntiles; kt += 6) {
+      step(Phase<0>{}, kt, sA, sB);
+      step(Phase<1>{}, kt + 1, sB, sA);
+      step(Phase<2>{}, kt + 2, sA, sB);
+      step(Phase<0>{}, kt + 3, sB, sA);
+      step(Phase<1>{}, kt + 4, sA, sB);
+      step(Phase<2>{}, kt + 5, sB, sA);
     }
-    if (kt < ntiles) step(kt, sA, sB);
+    for (; kt + 1 < ntiles; kt += 2) {
+      step(Phase<-1>{}, kt, sA, sB);
+      step(Phase<-1>{}, kt + 1, sB, sA);
+    }
+    if (kt < ntiles) step(Phase<-1>{}, kt, sA, sB);
 
     // Epilogue: normalise, store O rows and LSE.
     const float l_tot = l_run + __shfl_xor(l_run, 32);
