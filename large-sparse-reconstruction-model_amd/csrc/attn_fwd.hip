@@ -16,13 +16,19 @@
 //     bank conflicts;
 //   * scores are computed transposed, S^T = K Q^T (32x32x16 MFMA, K from LDS,
 //     Q in registers), so that a lane owns one query row through the whole
-//     softmax (base 2, scale folded into one FMA per score, lazy rescaling); O^T = V^T P^T takes its V^T operand straight from the
-//     row-major V tile with ds_read_b64_tr_b16 and P^T from the score
-//     registers, so V is never transposed in memory;
-//   * the loop is software pipelined: the score MFMAs of key tile t+1 are
-//     issued before the softmax of tile t; K and V live in three-slot LDS
-//     rings whose copies are issued two steps before they are read, one
-//     barrier per tile.
+//     softmax (base 2, scale folded into one FMA per score); O^T = V^T P^T
+//     takes its V^T operand straight from the row-major V tile with
+//     ds_read_b64_tr_b16 and P^T from the score registers, so V is never
+//     transposed in memory;
+//   * the loop is a three-stage software pipeline: step t issues the score
+//     MFMAs of tile t+1 and the P.V MFMAs of tile t-1 next to the softmax
+//     arithmetic of tile t, so matrix and vector work interleave inside one
+//     wave; K and V live in four-slot LDS rings whose copies are issued two
+//     or three steps before they are read, one barrier per tile;
+//   * the softmax reference is the row maximum of the first key tile and is
+//     not updated afterwards (no per-tile maximum, no rescaling); a tile
+//     whose row sums leave the safe range is recomputed with the exact
+//     online maximum.
 #include "attn.h"
 
 namespace lsrm {
@@ -62,8 +68,8 @@ sel_attn_fwd_kernel(AttnArgs a) {
   using G = KvTile<D>;
   constexpr int NS = D / 16;  // MFMA k-steps over the head dim
   constexpr int ND = D / 32;  // 32-wide output blocks over the head dim
-  __shared__ __align__(1024) char sK[3][G::BYTES];
-  __shared__ __align__(1024) char sV[3][G::BYTES];
+  __shared__ __align__(1024) char sK[4][G::BYTES];
+  __shared__ __align__(1024) char sV[4][G::BYTES];
   __shared__ SelLds sel;
   __shared__ int s_slot;
 
@@ -93,9 +99,9 @@ sel_attn_fwd_kernel(AttnArgs a) {
     const int2 tile = a.plan.tiles[(int64_t)h * a.nq + (w - a.plan.head_off[h])];
     const int q0 = tile.x, rows = tile.y * a.g;
     load_selection(a, h, q0, sel);
-    const int nkeys = sel.cum[sel.n];
+    const int nkeys = uniform(sel.cum[sel.n]);
     const int ntiles = (nkeys + KT - 1) / KT;
-    const int t_safe = sel.n > 0 ? sel.tok[0] : 0;  // in-bounds filler token
+    const int t_safe = uniform(sel.n > 0 ? sel.tok[0] : 0);  // in-bounds filler token
 
     // This wave's row and its Q operand (B of S^T = K Q^T).
     const int r = wv * 32 + l32;
@@ -125,7 +131,7 @@ sel_attn_fwd_kernel(AttnArgs a) {
     int ld_tile = 0;  // next tile whose K copies are issued
     uint32_t koff[G::LPW], voff[G::LPW];
     // Byte offsets of the rows of tile ld_tile for this lane's loads.
-    auto advance = [&](uint32_t* off) {
+    auto advance = [&](uint32_t* off) __attribute__((always_inline)) {
 #pragma unroll
       for (int j = 0; j < G::LPW; ++j) {
         const int P = ld_tile * KT + (wv * G::LPW + j) * G::KPL;
@@ -134,11 +140,11 @@ sel_attn_fwd_kernel(AttnArgs a) {
       }
       ++ld_tile;
     };
-    auto voff_keep = [&](const uint32_t* off) {
+    auto voff_keep = [&](const uint32_t* off) __attribute__((always_inline)) {
 #pragma unroll
       for (int j = 0; j < G::LPW; ++j) voff[j] = off[j];
     };
-    auto load_tile = [&](const char* base, const uint32_t* off, char* dst) {
+    auto load_tile = [&](const char* base, const uint32_t* off, char* dst) __attribute__((always_inline)) {
       const uint32_t d0 = lds_addr(dst) + wv * G::LPW * 1024;
 #pragma unroll
       for (int j = 0; j < G::LPW; ++j)
@@ -146,15 +152,11 @@ sel_attn_fwd_kernel(AttnArgs a) {
     };
 
     f32x16 oacc[ND];
-#pragma unroll
-    for (int i = 0; i < ND; ++i)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
     // Online softmax state of this lane's row: the reference m_run (log2
     // units) and the partial row sum.
     float m_run = 0.0f, l_run = 0.0f;
 
-    auto scores = [&](const char* ks, f32x16* sacc) {
+    auto scores = [&](const char* ks, f32x16* sacc) __attribute__((always_inline)) {
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
@@ -167,133 +169,188 @@ sel_attn_fwd_kernel(AttnArgs a) {
         }
       }
     };
+    // Keys past the stream (last tile only) score -inf.
+    auto mask_tail = [&](int kt, f32x16* sc) __attribute__((always_inline)) {
+      const int kb0 = kt * KT;
+      if (kb0 + KT > nkeys) {
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            if (kb0 + blk * 32 + acc_row(v, hb) >= nkeys) sc[blk][v] = -__builtin_inf();
+      }
+    };
 
-    // Prologue: K(0), V(0), K(1) resident, S(0) computed, then K(2) and
-    // V(1) in flight (the copies a step issues are consumed two steps later).
-    if (ntiles > 0) {
-      advance(koff);
-      load_tile(kbase, koff, sK[0]);
-      load_tile(vbase, koff, sV[0]);
-      advance(koff);
-      load_tile(kbase, koff, sK[1]);
-      voff_keep(koff);
-    }
-    wait_copies();
-    __syncthreads();
+    // Softmax of one score tile against m_run: P packed to the 16-bit type
+    // (the MFMA B operand of O^T += V^T P^T) and added to the row sum.
+    auto softmax = [&](const f32x16* sc, u32x4 (*pb)[2]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        float p[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v], a.scale_log2, -m_run));
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          pb[blk][c] = u32x4{pack2<DT>(p[c * 8 + 0], p[c * 8 + 1]),
+                             pack2<DT>(p[c * 8 + 2], p[c * 8 + 3]),
+                             pack2<DT>(p[c * 8 + 4], p[c * 8 + 5]),
+                             pack2<DT>(p[c * 8 + 6], p[c * 8 + 7])};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) l_run = sum2<DT>(pb[blk][c][e], l_run);
+        }
+      }
+    };
+    // O^T += V^T P^T.  Slot e of lane (hb, row d) holds key
+    // blk*32 + c*16 + (e/4)*8 + hb*4 + e%4 (the score layout); the two
+    // transposed reads return those keys' column d.
+    auto pv = [&](const char* vs, const u32x4 (*pb)[2]) __attribute__((always_inline)) {
+      const int gi = lane & 15, dh = (lane >> 4) & 1;
+#pragma unroll
+      for (int db = 0; db < ND; ++db) {
+        const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;  // 4 d values
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const int k0 = blk * 32 + c * 16 + hb * 4 + (gi >> 2);
+            const int cb = dcol >> 3, half = (dcol & 4) * 2;
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(vs + G::off(k0, cb) + half));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(vs + G::off(k0 + 8, cb) + half));
+            const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+            const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+            oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]}, pb[blk][c], oacc[db]);
+          }
+      }
+    };
+
+    // Pipeline over key tiles (K and V in four-slot LDS rings).  Step kt
+    // copies K(kt+3) and V(kt+2), computes S(kt+1) = K(kt+1) Q^T, adds
+    // P(kt-1) V(kt-1) into O and turns S(kt) into P(kt): the step's 16 MFMAs
+    // are independent of its softmax arithmetic, so the two interleave.
+    // Every step issues the same number of copies (positions past the stream
+    // load a resident token), so one counted wait at its end retires exactly
+    // the previous step's copies.
     f32x16 sA[2], sB[2];
-    if (wave_on && ntiles > 0) scores(sK[0], sA);
-    if (ntiles > 0) {
-      advance(koff);
-      load_tile(kbase, koff, sK[2]);
-      load_tile(vbase, voff, sV[1]);
-      voff_keep(koff);
-    }
-    __syncthreads();  // sK[0] is refilled by step 0
-
-    // One key tile kt: sc holds S(kt) on entry, sn receives S(kt+1).  The
-    // step reads K(kt+1) and V(kt) and copies K(kt+3) and V(kt+2) into the
-    // ring slots last read one step earlier.  Every step issues the same
-    // number of copies (positions past the stream load a resident token), so
-    // one counted wait retires exactly the previous step's copies.
-    // `ph` is kt % 3 as a compile-time constant (ring slots then become
-    // immediate LDS offsets), or -1 to compute it at run time.
-    auto step = [&](auto ph, int kt, f32x16* sc, f32x16* sn) {
+    u32x4 pA[2][2], pB[2][2];
+    // Prologue: K(0), V(0), K(1) resident, S(0) computed, K(2) and V(1) in
+    // flight; oacc / l_run cleared, m_run = the row maximum of tile 0.
+    auto prologue = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < ND; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
+      l_run = 0.0f;
+      m_run = 0.0f;
+#pragma unroll
+      for (int j = 0; j < G::LPW; ++j) group_init(sel, cur[j]);
+      ld_tile = 0;
+      if (ntiles > 0) {
+        advance(koff);
+        load_tile(kbase, koff, sK[0]);
+        load_tile(vbase, koff, sV[0]);
+        advance(koff);
+        load_tile(kbase, koff, sK[1]);
+        voff_keep(koff);
+      }
+      wait_copies();
+      __syncthreads();
+      if (wave_on && ntiles > 0) {
+        scores(sK[0], sA);
+        mask_tail(0, sA);
+        m_run = row_max(sA) * a.scale_log2;
+      }
+      if (ntiles > 0) {
+        advance(koff);
+        load_tile(kbase, koff, sK[2]);
+        load_tile(vbase, voff, sV[1]);
+        voff_keep(koff);
+      }
+    };
+    // `ph` is kt % 4 as a compile-time constant (ring slots then become
+    // immediate LDS offsets), or -1 to compute it at run time.  `first`
+    // marks step 0 (no P(-1)).  With `safe` false the reference m_run stays
+    // at tile 0's row maximum (p may exceed 1; the caller checks the row sums
+    // afterwards); with `safe` true it follows the online maximum with lazy
+    // rescaling.
+    auto step = [&](auto ph, auto safe, auto first, int kt, f32x16* sc, f32x16* sn,
+                    const u32x4 (*pp)[2], u32x4 (*pc)[2]) __attribute__((always_inline)) {
       constexpr int PH = decltype(ph)::value;
-      const int s0 = PH >= 0 ? PH : kt % 3;
-      const int s1 = PH >= 0 ? (PH + 1) % 3 : (kt + 1) % 3;
-      const int s2 = PH >= 0 ? (PH + 2) % 3 : (kt + 2) % 3;
+      constexpr bool SAFE = decltype(safe)::value != 0;
+      constexpr bool FIRST = decltype(first)::value != 0;
+      const int k_rd = PH >= 0 ? (PH + 1) & 3 : (kt + 1) & 3;  // K(kt+1)
+      const int k_wr = PH >= 0 ? (PH + 3) & 3 : (kt + 3) & 3;  // K(kt+3), = V(kt-1)
+      const int v_wr = PH >= 0 ? (PH + 2) & 3 : (kt + 2) & 3;  // V(kt+2)
       advance(koff);
-      load_tile(kbase, koff, sK[s0]);
-      load_tile(vbase, voff, sV[s2]);
+      load_tile(kbase, koff, sK[k_wr]);
+      load_tile(vbase, voff, sV[v_wr]);
       voff_keep(koff);
 
       if (wave_on) {
-        const int kb0 = kt * KT;
-        if (kb0 + KT > nkeys) {
+        mask_tail(kt, sc);
+        if constexpr (SAFE) {
+          if constexpr (!FIRST) pv(sV[k_wr], pp);  // before any rescale of O
+          const float m_tile = row_max(sc) * a.scale_log2;
+          if (__builtin_amdgcn_ballot_w64(m_tile > m_run + RESCALE_LOG2) != 0) {
+            const float m_new = __builtin_elementwise_maximum(m_run, m_tile);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
 #pragma unroll
-          for (int blk = 0; blk < 2; ++blk)
+            for (int db = 0; db < ND; ++db)
 #pragma unroll
-            for (int v = 0; v < 16; ++v)
-              if (kb0 + blk * 32 + acc_row(v, hb) >= nkeys)
-                sc[blk][v] = -__builtin_inf();
-        }
-        const float mx = row_max(sc);
-        const float m_tile = mx * a.scale_log2;
-        const bool first = kt == 0;
-        if (first || __builtin_amdgcn_ballot_w64(m_tile > m_run + RESCALE_LOG2) != 0) {
-          const float m_new = first ? m_tile : __builtin_elementwise_maximum(m_run, m_tile);
-          const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-          m_run = m_new;
-          l_run *= alpha;
-#pragma unroll
-          for (int db = 0; db < ND; ++db)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) oacc[db][v] *= alpha;
+              for (int v = 0; v < 16; ++v) oacc[db][v] *= alpha;
+          }
         }
         // S(kt+1); on the last tile this scores stale keys and is discarded,
         // which keeps the score registers free of a select per element.
-        scores(sK[s1], sn);
-
-        u32x4 pb[2][2];
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-          float p[16];
-#pragma unroll
-          for (int v = 0; v < 16; ++v)
-            p[v] = __builtin_amdgcn_exp2f(
-                __builtin_fmaf(sc[blk][v], a.scale_log2, -m_run));
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            pb[blk][c] = u32x4{pack2<DT>(p[c * 8 + 0], p[c * 8 + 1]),
-                               pack2<DT>(p[c * 8 + 2], p[c * 8 + 3]),
-                               pack2<DT>(p[c * 8 + 4], p[c * 8 + 5]),
-                               pack2<DT>(p[c * 8 + 6], p[c * 8 + 7])};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) l_run = sum2<DT>(pb[blk][c][e], l_run);
-          }
-        }
-        // O^T += V^T P^T.  Slot e of lane (hb, row d) holds key
-        // blk*32 + c*16 + (e/4)*8 + hb*4 + e%4 (the score layout); the two
-        // transposed reads return those keys' column d.
-        const char* vs = sV[s0];
-        const int gi = lane & 15, dh = (lane >> 4) & 1;
-#pragma unroll
-        for (int db = 0; db < ND; ++db) {
-          const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;  // 4 d values
-#pragma unroll
-          for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-              const int k0 = blk * 32 + c * 16 + hb * 4 + (gi >> 2);
-              const int cb = dcol >> 3, half = (dcol & 4) * 2;
-              const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                  (lds_s16x4*)(vs + G::off(k0, cb) + half));
-              const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                  (lds_s16x4*)(vs + G::off(k0 + 8, cb) + half));
-              const u32x2 lw = __builtin_bit_cast(u32x2, lo);
-              const u32x2 hw = __builtin_bit_cast(u32x2, hi);
-              oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]},
-                                    pb[blk][c], oacc[db]);
-            }
-        }
+        scores(sK[k_rd], sn);
+        if constexpr (!SAFE && !FIRST) pv(sV[k_wr], pp);
+        softmax(sc, pc);
       }
       wait_prev_copies<2 * G::LPW>();  // the previous step's copies landed
       __syncthreads();
     };
-    int kt = 0;
-    for (; kt + 6 <= ntiles; kt += 6) {
-      step(Phase<0>{}, kt, sA, sB);
-      step(Phase<1>{}, kt + 1, sB, sA);
-      step(Phase<2>{}, kt + 2, sA, sB);
-      step(Phase<0>{}, kt + 3, sB, sA);
-      step(Phase<1>{}, kt + 4, sA, sB);
-      step(Phase<2>{}, kt + 5, sB, sA);
+    // All steps of one pass, then O += P(last) V(last).
+    auto run = [&](auto safe) __attribute__((always_inline)) {
+      if (ntiles == 0) return;
+      step(Phase<0>{}, safe, Phase<1>{}, 0, sA, sB, pB, pA);
+      int kt = 1;
+      for (; kt + 4 <= ntiles; kt += 4) {
+        step(Phase<1>{}, safe, Phase<0>{}, kt, sB, sA, pA, pB);
+        step(Phase<2>{}, safe, Phase<0>{}, kt + 1, sA, sB, pB, pA);
+        step(Phase<3>{}, safe, Phase<0>{}, kt + 2, sB, sA, pA, pB);
+        step(Phase<0>{}, safe, Phase<0>{}, kt + 3, sA, sB, pB, pA);
+      }
+      // kt % 4 == 1 here
+      if (kt < ntiles) step(Phase<1>{}, safe, Phase<0>{}, kt, sB, sA, pA, pB);
+      if (kt + 1 < ntiles) step(Phase<2>{}, safe, Phase<0>{}, kt + 1, sA, sB, pB, pA);
+      if (kt + 2 < ntiles) step(Phase<3>{}, safe, Phase<0>{}, kt + 2, sB, sA, pA, pB);
+      if (wave_on) {
+        const char* vs = sV[(ntiles - 1) & 3];
+        if ((ntiles - 1) & 1)
+          pv(vs, pB);
+        else
+          pv(vs, pA);
+      }
+    };
+
+    // Fast pass: reference fixed at tile 0's row maximum.  p = 2^(x - m_run)
+    // only exceeds 1 by the amount later tiles beat tile 0, which leaves the
+    // result unchanged up to rounding unless P overflows its 16-bit type or
+    // the sums grow out of range; a row sum that is not below 2^32 (inf and
+    // NaN included) sends the whole tile through the exact online pass.
+    prologue();
+    run(Phase<0>{});
+    const float l_fast = l_run + __shfl_xor(l_run, 32);
+    if (uniform(__syncthreads_or(!(l_fast < 4294967296.0f)))) {
+      wait_copies();  // the fast pass's trailing copies land before reuse
+      __syncthreads();
+      prologue();
+      run(Phase<1>{});
     }
-    for (; kt + 1 < ntiles; kt += 2) {
-      step(Phase<-1>{}, kt, sA, sB);
-      step(Phase<-1>{}, kt + 1, sB, sA);
-    }
-    if (kt < ntiles) step(Phase<-1>{}, kt, sA, sB);
 
     // Epilogue: normalise, store O rows and LSE.
     const float l_tot = l_run + __shfl_xor(l_run, 32);

@@ -195,3 +195,26 @@ def test_fwd_bwd_extreme_scores(mode):
     else:
         _run_case(q, k, v, topk, w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens, w.scale,
                   do=do)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fwd_later_blocks_dominate(dtype):
+    # Every query lists a weak block first (K scaled down) and strong blocks
+    # after it, so the row maxima of later key tiles exceed the first tile's
+    # by ~17 log2 units: unnormalised probabilities reach 2^17, which bf16
+    # holds and fp16 overflows (the kernel must then take its exact online
+    # pass).  Outputs must match the oracle either way.
+    n, bl, hkv, d, topk_n = 2048, 128, 2, 64, 4
+    nb = n // bl
+    gen = torch.Generator().manual_seed(31)
+    cu_blk = torch.arange(0, n + 1, bl, dtype=torch.int32)
+    cu_sb = torch.tensor([0, nb], dtype=torch.int32)
+    cu_q = torch.tensor([0, n], dtype=torch.int32)
+    q = 2.0 * torch.randn(n, hkv, d, generator=gen)
+    k = 2.0 * torch.randn(n, hkv, d, generator=gen)
+    k[:bl] *= 0.02
+    v = torch.randn(n, hkv, d, generator=gen)
+    topk = torch.randint(1, nb, (hkv, n, topk_n), generator=gen).to(torch.int32)
+    topk[:, :, 0] = 0
+    q, k, v = (t.to(dtype) for t in (q, k, v))
+    _run_case(q, k, v, topk, cu_sb, cu_blk, cu_q, 1.0 / math.sqrt(d))
