@@ -248,16 +248,21 @@ struct KvTile {
   static constexpr int KPL = 64 / CH;       // rows per 1 KB load
   static constexpr int LPW = (NR / KPL) / 4;  // loads per wave per tile (4 waves)
   static constexpr int BYTES = NR * D * 2;
-  // Physical chunk = logical chunk ^ swz(row).  Rows that fall on the same
-  // LDS banks (256-byte period) get distinct chunk positions both for the
-  // 16-lane row-strided K reads and the 4-row transposed V reads.
+  // Physical chunk = logical chunk ^ swz(row), a linear map of the row's low
+  // four bits.  LDS has 64 four-byte banks; a ds_read_b128 is served 16
+  // lanes at a time and a ds_read_b64_tr_b16 32 lanes at a time.  The maps
+  // give distinct banks to every lane of a service group both for the
+  // row-strided reads (16 consecutive rows, one chunk each) and for the
+  // transposed reads (rows r0..r0+3 and r0+4..r0+7, two to four chunks
+  // each): rows whose 16-byte chunks would share banks differ in the
+  // swizzle bit that moves a chunk to the other half of the bank range.
   __device__ static constexpr int swz(int r) {
     if constexpr (D == 32)
       return (r >> 2) & 3;
     else if constexpr (D == 64)
-      return (r & 7) ^ ((r >> 3) & 1);
+      return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
     else
-      return ((r & 7) << 1) | ((r >> 3) & 1);
+      return ((r & 3) << 2) | ((r >> 2) & 3);
   }
   // Byte offset of (row, logical chunk) inside a tile.
   __device__ static constexpr int off(int r, int c) {

@@ -22,9 +22,10 @@
 //     transposed in memory;
 //   * the loop is a three-stage software pipeline: step t issues the score
 //     MFMAs of tile t+1 and the P.V MFMAs of tile t-1 next to the softmax
-//     arithmetic of tile t, so matrix and vector work interleave inside one
-//     wave; K and V live in four-slot LDS rings whose copies are issued two
-//     or three steps before they are read, one barrier per tile;
+//     arithmetic of tile t, in a fixed order of slots (one MFMA, then two
+//     scores' worth of softmax) so that matrix and vector work co-issue
+//     inside one wave; K and V live in four-slot LDS rings whose copies are
+//     issued two or three steps before they are read, one barrier per tile;
 //   * the softmax reference is the row maximum of the first key tile and is
 //     not updated afterwards (no per-tile maximum, no rescaling); a tile
 //     whose row sums leave the safe range is recomputed with the exact
@@ -226,13 +227,85 @@ sel_attn_fwd_kernel(AttnArgs a) {
       }
     };
 
+    // K operands of one score tile (S^T = K Q^T), read ahead of the MFMAs.
+    auto read_k = [&](const char* ks, u32x4 (*ka)[NS]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          ka[blk][s] = *reinterpret_cast<const u32x4*>(ks + G::off(blk * 32 + l32, 2 * s + hb));
+    };
+    // One softmax pair (scores 2j, 2j+1 of a lane's 32) against m_run: two
+    // exponentials packed to the 16-bit type and added to the row sum.
+    auto softmax_pair = [&](const f32x16* sc, u32x4 (*pb)[2], int j) __attribute__((always_inline)) {
+      const int blk = j >> 3, c = (j >> 2) & 1, e = j & 3, v0 = c * 8 + 2 * e;
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0], a.scale_log2, -m_run));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0 + 1], a.scale_log2, -m_run));
+      pb[blk][c][e] = pack2<DT>(p0, p1);
+      l_run = sum2<DT>(pb[blk][c][e], l_run);
+    };
+    // The fast step's matrix and vector work in a fixed issue order: slot i
+    // issues one MFMA (the score MFMAs of tile kt+1, alternating between the
+    // two independent 32-key accumulators, then the P.V MFMAs of tile kt-1,
+    // alternating between output blocks) followed by its share of the
+    // softmax of tile kt, so that the vector ALU works while the matrix core
+    // runs.  All K operands are read at the start; the V operands of P.V
+    // MFMA i are read during score slot i.  Scheduling barriers keep the
+    // compiler from regrouping the slots.
+    auto fast_body = [&](auto first, const char* ks, const char* vs, const f32x16* sc,
+                         f32x16* sn, const u32x4 (*pp)[2], u32x4 (*pc)[2]) __attribute__((always_inline)) {
+      constexpr bool FIRST = decltype(first)::value != 0;
+      constexpr int NSM = 2 * NS;              // score MFMAs
+      constexpr int NPV = FIRST ? 0 : 4 * ND;  // P.V MFMAs
+      constexpr int NSLOT = NSM + NPV;
+      constexpr int NPAIR = 16;
+      u32x4 ka[2][NS], va[ND][2][2];
+      read_k(ks, ka);
+      const int gi = lane & 15, dh = (lane >> 4) & 1;
+      auto read_v1 = [&](int i) __attribute__((always_inline)) {  // operands of P.V MFMA i
+        const int db = i % ND, bc = i / ND, blk = bc >> 1, c = bc & 1;
+        const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+        const int k0 = blk * 32 + c * 16 + hb * 4 + (gi >> 2);
+        const int cb = dcol >> 3, half = (dcol & 4) * 2;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(vs + G::off(k0, cb) + half));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(vs + G::off(k0 + 8, cb) + half));
+        const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+        const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+        va[db][blk][c] = u32x4{lw[0], lw[1], hw[0], hw[1]};
+      };
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NSLOT; ++i) {
+        if (i < NSM) {
+          const int blk = i & 1, s = i >> 1;
+          if (s == 0) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sn[blk][v] = 0.0f;
+          }
+          sn[blk] = mfma32<DT>(ka[blk][s], qb[s], sn[blk]);
+          if constexpr (!FIRST) {
+#pragma unroll
+            for (int r = (i * NPV) / NSM; r < ((i + 1) * NPV) / NSM; ++r) read_v1(r);
+          }
+        } else {
+          const int j = i - NSM, db = j % ND, bc = j / ND, blk = bc >> 1, c = bc & 1;
+          oacc[db] = mfma32<DT>(va[db][blk][c], pp[blk][c], oacc[db]);
+        }
+#pragma unroll
+        for (int j = (i * NPAIR) / NSLOT; j < ((i + 1) * NPAIR) / NSLOT; ++j) softmax_pair(sc, pc, j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+
     // Pipeline over key tiles (K and V in four-slot LDS rings).  Step kt
     // copies K(kt+3) and V(kt+2), computes S(kt+1) = K(kt+1) Q^T, adds
     // P(kt-1) V(kt-1) into O and turns S(kt) into P(kt): the step's 16 MFMAs
     // are independent of its softmax arithmetic, so the two interleave.
     // Every step issues the same number of copies (positions past the stream
     // load a resident token), so one counted wait at its end retires exactly
-    // the previous step's copies.
+    // the copies the next step reads.
     f32x16 sA[2], sB[2];
     u32x4 pA[2][2], pB[2][2];
     // Prologue: K(0), V(0), K(1) resident, S(0) computed, K(2) and V(1) in
@@ -306,11 +379,17 @@ sel_attn_fwd_kernel(AttnArgs a) {
         }
         // S(kt+1); on the last tile this scores stale keys and is discarded,
         // which keeps the score registers free of a select per element.
-        scores(sK[k_rd], sn);
-        if constexpr (!SAFE && !FIRST) pv(sV[k_wr], pp);
-        softmax(sc, pc);
+        if constexpr (SAFE) {
+          scores(sK[k_rd], sn);
+          softmax(sc, pc);
+        } else {
+          fast_body(first, sK[k_rd], sV[k_wr], sc, sn, pp, pc);
+        }
       }
-      wait_prev_copies<2 * G::LPW>();  // the previous step's copies landed
+      // Copies complete in issue order (per step: K, then V).  The next step
+      // reads K(kt+2), issued one step ago, and V(kt), issued three steps
+      // ago; V(kt+1) and this step's copies may stay in flight.
+      wait_prev_copies<3 * G::LPW>();
       __syncthreads();
     };
     // All steps of one pass, then O += P(last) V(last).
