@@ -159,6 +159,120 @@ __global__ __launch_bounds__(256) void pool_pieces(
   if (have && b >= 0 && b < nb) flush();
 }
 
+// 16-bit rows, channel count a multiple of 512: one wave per (64-row chunk,
+// 512-channel slab), 8 channels per lane.  The first eight rows are loaded
+// before the block lookup (so every wave has loads in flight from its first
+// instruction) and rows are then streamed in double-buffered groups of
+// eight.  With IF, the block owning the chunk's first row is found in the
+// kernel (nb + 1 <= 512 offsets: lane l compares entries 8l..8l+7 with the
+// row and the wave counts the hits), otherwise it comes from the
+// pool_chunk_first table.  The sums are the same sequential fp32 sums as in
+// pool_pieces.
+constexpr int POOL_G = 8;  // rows per load group
+
+template <int DT, bool IF>
+__global__ __launch_bounds__(256) void pool_pieces_slab(
+    const uint16_t* __restrict__ x, int64_t n, int64_t ch,
+    const int32_t* __restrict__ cu, int64_t nb,
+    const int32_t* __restrict__ first, float* __restrict__ partial) {
+  const int64_t n_vec = ch / 8;
+  const int64_t n_chunks = (n + POOL_CHUNK - 1) / POOL_CHUNK;
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= n_chunks * n_vec) return;  // whole waves (n_vec % 64 == 0)
+  const int64_t j = __builtin_amdgcn_readfirstlane((int)(item / n_vec));
+  const int64_t c0 = (item - j * n_vec) * 8;
+  const int64_t r0 = j * POOL_CHUNK;
+  const int64_t r1 = r0 + POOL_CHUNK < n ? r0 + POOL_CHUNK : n;
+  const uint16_t* xp = x + c0;
+
+  u32x4 buf[2][POOL_G];
+  auto load_group = [&](u32x4* dst, int64_t r) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < POOL_G; ++u) {
+      const int64_t rr = r + u < r1 ? r + u : r1 - 1;
+      dst[u] = *reinterpret_cast<const u32x4*>(xp + rr * ch);
+    }
+  };
+  load_group(buf[0], r0);
+
+  // b = last block whose start is <= r0 (-1: before the first block,
+  // nb: past the last).  bs/be bound the rows block b owns.
+  int64_t b;
+  if constexpr (IF) {
+    const int lane = threadIdx.x & 63;
+    int32_t cv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t idx = 8 * lane + i;
+      cv[i] = idx <= nb ? cu[idx] : 0x7fffffff;
+    }
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      cnt += __popcll(__ballot((int64_t)cv[i] <= r0 && 8 * lane + i <= nb));
+    b = __builtin_amdgcn_readfirstlane(cnt) - 1;
+  } else {
+    b = first[j];
+  }
+  int64_t be = b < 0 ? (int64_t)cu[0] : (b < nb ? (int64_t)cu[b + 1] : INT64_MAX);
+  int64_t bs = (b >= 0 && b < nb) ? (int64_t)cu[b] : INT64_MAX;
+
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  auto add_row = [&](const u32x4& w) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] = acc[2 * i] + to_f32<DT>((uint16_t)(w[i] & 0xffffu));
+      acc[2 * i + 1] = acc[2 * i + 1] + to_f32<DT>((uint16_t)(w[i] >> 16));
+    }
+  };
+  auto flush = [&]() __attribute__((always_inline)) {
+    float4* dst = reinterpret_cast<float4*>(partial + (b + j) * ch + c0);
+    dst[0] = float4{acc[0], acc[1], acc[2], acc[3]};
+    dst[1] = float4{acc[4], acc[5], acc[6], acc[7]};
+  };
+  constexpr int NG = POOL_CHUNK / POOL_G;
+
+  if (b >= 0 && b < nb && bs <= r0 && be >= r1) {
+    // The chunk lies inside block b: no boundary checks.
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g + 1 < NG) load_group(buf[(g + 1) & 1], r0 + (g + 1) * POOL_G);
+#pragma unroll
+      for (int u = 0; u < POOL_G; ++u)
+        if (r0 + g * POOL_G + u < r1) add_row(buf[g & 1][u]);
+    }
+    flush();
+    return;
+  }
+  bool have = false;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (g + 1 < NG) load_group(buf[(g + 1) & 1], r0 + (g + 1) * POOL_G);
+#pragma unroll
+    for (int u = 0; u < POOL_G; ++u) {
+      const int64_t row = r0 + g * POOL_G + u;
+      if (row < r1) {
+        while (b < nb && row >= be) {
+          if (have) flush();
+          have = false;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+          ++b;
+          bs = b < nb ? (int64_t)cu[b] : INT64_MAX;
+          be = b < nb ? (int64_t)cu[b + 1] : INT64_MAX;
+        }
+        if (b >= 0 && b < nb && row >= bs) {
+          add_row(buf[g & 1][u]);
+          have = true;
+        }
+      }
+    }
+  }
+  if (have && b >= 0 && b < nb) flush();
+}
+
 template <int ODT>
 __device__ inline void store_out(void* out, int64_t off, float v) {
   if constexpr (ODT == LSRM_F32)
@@ -184,10 +298,30 @@ __global__ __launch_bounds__(256) void pool_combine(
   for (int i = 0; i < VEC; ++i) acc[i] = 0.0f;
   if (e > s) {
     const int64_t j0 = s / POOL_CHUNK, j1 = (e - 1) / POOL_CHUNK;
-    for (int64_t j = j0; j <= j1; ++j) {
-      const float* src = partial + (b + j) * ch + c0;
+    // Up to PB pieces are loaded before any is added (one memory round trip
+    // per PB pieces); the adds stay in chunk order.
+    constexpr int PB = VEC == 8 ? 8 : 16;
+    for (int64_t jb = j0; jb <= j1; jb += PB) {
+      float v[PB][VEC];
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) acc[i] = acc[i] + src[i];
+      for (int u = 0; u < PB; ++u) {
+        const int64_t j = jb + u <= j1 ? jb + u : j1;
+        const float* src = partial + (b + j) * ch + c0;
+        if constexpr (VEC == 8) {
+          const float4 lo = reinterpret_cast<const float4*>(src)[0];
+          const float4 hi = reinterpret_cast<const float4*>(src)[1];
+          v[u][0] = lo.x; v[u][1] = lo.y; v[u][2] = lo.z; v[u][3] = lo.w;
+          v[u][4] = hi.x; v[u][5] = hi.y; v[u][6] = hi.z; v[u][7] = hi.w;
+        } else {
+          v[u][0] = src[0];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < PB; ++u)
+        if (jb + u <= j1) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[i] = acc[i] + v[u][i];
+        }
     }
   }
   // IEEE quotient; a block with no rows gives 0/0 = NaN.
@@ -214,7 +348,32 @@ int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
                    ((uintptr_t)partial % 16) == 0;
   const int64_t n_vec = vec ? ch / POOL_VEC : ch;
   const int64_t n_chunks = (n + POOL_CHUNK - 1) / POOL_CHUNK;
-  if (n > 0) {
+  const bool slab = vec && x_dtype != LSRM_F32 && n_vec % 64 == 0;
+  const bool inline_first = slab && nb + 1 <= 512;
+  if (n > 0 && slab) {
+    if (!inline_first)
+      hipLaunchKernelGGL(pool_chunk_first, dim3((unsigned)((n_chunks + 255) / 256)),
+                         dim3(256), 0, st, cu, nb, n_chunks, first);
+    const int64_t items = n_chunks * n_vec;
+    dim3 grid((unsigned)((items + 255) / 256));
+    const uint16_t* xs = reinterpret_cast<const uint16_t*>(x);
+    if (x_dtype == LSRM_F16) {
+      if (inline_first)
+        hipLaunchKernelGGL((pool_pieces_slab<LSRM_F16, true>), grid, dim3(256), 0, st,
+                           xs, n, ch, cu, nb, first, partial);
+      else
+        hipLaunchKernelGGL((pool_pieces_slab<LSRM_F16, false>), grid, dim3(256), 0, st,
+                           xs, n, ch, cu, nb, first, partial);
+    } else {
+      if (inline_first)
+        hipLaunchKernelGGL((pool_pieces_slab<LSRM_BF16, true>), grid, dim3(256), 0, st,
+                           xs, n, ch, cu, nb, first, partial);
+      else
+        hipLaunchKernelGGL((pool_pieces_slab<LSRM_BF16, false>), grid, dim3(256), 0, st,
+                           xs, n, ch, cu, nb, first, partial);
+    }
+    LSRM_CHECK_LAUNCH();
+  } else if (n > 0) {
     hipLaunchKernelGGL(pool_chunk_first, dim3((unsigned)((n_chunks + 255) / 256)),
                        dim3(256), 0, st, cu, nb, n_chunks, first);
     const int64_t items = n_chunks * n_vec;

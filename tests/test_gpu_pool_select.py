@@ -64,6 +64,34 @@ def test_pool_matches_segment_reduce_and_empty_block():
     torch.testing.assert_close(out[keep], ref[keep], rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("c", [512, 1024])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("out_dtype", [None, torch.float32])
+@pytest.mark.parametrize("n_blocks", [300, 800])
+def test_pool_slab_path_small_and_empty_blocks(c, dtype, out_dtype, n_blocks):
+    # Channel counts that are multiples of 512 take the slab kernel (with the
+    # in-kernel block lookup below 512 blocks, the lookup table above).
+    # Blocks of length 0..40 put several block boundaries (and empty blocks,
+    # whose mean is NaN) inside one 64-row piece; rows before the first and
+    # after the last block are ignored.
+    rng = np.random.default_rng(11)
+    sizes = rng.integers(0, 41, size=n_blocks)
+    sizes[[3, 4, 50, 299]] = 0
+    sizes[[10, 11]] = 1
+    cu_np = np.concatenate([[37], 37 + np.cumsum(sizes)]).astype(np.int32)
+    n = int(cu_np[-1]) + 29
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(n, c, generator=g).to(dtype)
+    cu = torch.from_numpy(cu_np)
+    ref = torch.from_numpy(block_mean_pool_ref(_f32(x), cu_np)).to(out_dtype or dtype)
+    for _ in range(2):
+        out = H.block_mean_pool(x.to(DEV), cu.to(DEV), out_dtype).cpu()
+        nan = torch.isnan(ref)
+        assert torch.equal(torch.isnan(out), nan)
+        ints = torch.int16 if out.element_size() == 2 else torch.int32
+        assert torch.equal(out[~nan.all(1)].view(ints), ref[~nan.all(1)].view(ints))
+
+
 def _select_case(w, forced=None, hq=None, hkv=None, dtype=None):
     dtype = dtype or w.dtype
     g = torch.Generator().manual_seed(w.seed)
