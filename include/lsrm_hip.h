@@ -26,6 +26,8 @@
  *                             selected-attention kernels into
  *                             sparse/ops/block_window_attention.py:14-31
  *                             (sparse_window_attention)
+ *   lsrm_block_score          sparse/ops/block_score.py:16-98 (get_block_score,
+ *                             the learned per-token block selection)
  */
 #ifndef LSRM_HIP_H
 #define LSRM_HIP_H
@@ -250,6 +252,29 @@ int lsrm_reverse_query_map(const int32_t* topk_idx, int64_t hkv, int64_t n_q,
 int lsrm_block_ids(const int32_t* cu_seqblocks, int64_t batch,
                    const int32_t* cu_block_tokens, int64_t n_blocks,
                    int64_t n_tokens, int64_t hkv, int32_t* ids, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Learned per-token block selection (get_block_score).
+ *   q [n_q, hq, head_dim], compressed_k [n_compressed, hkv, head_dim] of
+ *   dtype (F16 or BF16); lse [hq, n_q] fp32 in natural-log units (the
+ *   softmax LSE of the queries against the compressed keys, as flash-attn
+ *   returns it); cu_seqlens_q / compressed_cu_seqlens [batch + 1].
+ * For token i of batch element b and kv head h, the score of compressed key
+ * c of b is the sum over the hq/hkv query heads g of h of
+ *   exp2(q[i, g] . ck[c, h] * sm_scale * 1.44269504 - lse[g, i] * 1.44269504)
+ * (fp32); the min(topk, keys of b) best keys (score descending, lower id
+ * first among equal scores, NaN never chosen) are written to
+ *   block_topk [hkv, n_q, topk] int32 as batch-local ids ascending, the row
+ *   padded with -1 (all -1 for a batch element without compressed keys).
+ * topk <= 64; head_dim in {32, 64, 128}.  No workspace.
+ * Replaces sparse/ops/block_score.py:16-98.
+ * ---------------------------------------------------------------------- */
+int lsrm_block_score(const void* q, const void* compressed_k, int dtype,
+                     const float* lse, int64_t n_q, int64_t hq, int64_t hkv,
+                     int64_t head_dim, const int32_t* cu_seqlens_q,
+                     const int32_t* compressed_cu_seqlens, int64_t batch,
+                     int64_t topk, float sm_scale, int32_t* block_topk,
+                     void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,251 @@
+// Learned block selection (get_block_score,
+// sparse/ops/block_score.py:16-98) on gfx950.
+//
+// For query token i of batch element b, kv head h and compressed key c of b:
+//   score(i, c) = sum over the G query heads g of h of
+//                 exp2(q[i, hG+g] . ck[c, h] * qk_scale - lse[hG+g, i] * 1.44269504)
+// (qk_scale = sm_scale * 1.44269504, the reference's constants, lines 53-56);
+// the min(topk, n_compressed) best compressed keys (score descending, id
+// ascending among equal scores; NaN scores are never chosen) are written
+// ascending, the row padded with -1 (lines 61-63, 94-96).
+//
+// One wave per (kv head, 32-token tile).  S^T = Ck Q^T on 32x32x16 MFMA:
+// the compressed keys (A operand, 16 contiguous bytes per lane) come
+// straight from global memory, one 32-key block ahead of their use; a lane
+// owns one query row and 16 of every 32 keys.  Each lane keeps a running
+// top-K list (K >= topk, a power of two) of its candidates in registers,
+// sorted by (score desc, id asc); at the end the two lanes of a row merge
+// their lists with a bitonic network and the chosen ids are sorted
+// ascending.  Tiles that straddle a batch boundary are processed once per
+// batch element they touch.
+#include "common.h"
+
+namespace lsrm {
+
+constexpr float LOG2E_REF = 1.44269504f;  // sparse/ops/block_score.py:53-56
+
+struct BlockScoreArgs {
+  const uint16_t* q;
+  const uint16_t* ck;
+  const float* lse;
+  const int32_t* cu_q;
+  const int32_t* cu_c;
+  int32_t* out;
+  int64_t nq, batch;
+  int hq, hkv, g, topk;
+  float qk_scale;
+};
+
+// (v, i) ranks before (w, j): larger score, equal scores by lower id.
+__device__ inline bool ranks_before(float v, int i, float w, int j) {
+  return v > w || (v == w && i < j);
+}
+
+template <int DT, int D, int K>
+__global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
+  constexpr int NS = D / 16;
+  const int lane = threadIdx.x & 63, hb = lane >> 5, l32 = lane & 31;
+  const int64_t tiles = (a.nq + 31) / 32;
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (wave >= tiles * a.hkv) return;
+  const int h = __builtin_amdgcn_readfirstlane((int)(wave / tiles));
+  const int64_t t0 = (wave - (int64_t)h * tiles) * 32;
+  const int64_t t_last = t0 + 31 < a.nq ? t0 + 31 : a.nq - 1;
+  const int b0 = (int)upper_index(a.cu_q, 0, a.batch + 1, t0);
+  const int b1 = (int)upper_index(a.cu_q, 0, a.batch + 1, t_last);
+  const int64_t row = t0 + l32;
+  const int64_t ck_stride = (int64_t)a.hkv * D;
+
+  for (int b = b0 < 0 ? 0 : b0; b <= b1 && b < a.batch; ++b) {
+    const int64_t qs = a.cu_q[b], qe = a.cu_q[b + 1];
+    if (qe <= t0 || qs > t_last) continue;
+    const bool row_ok = row >= qs && row < qe && row < a.nq;
+    const int64_t ks = a.cu_c[b];
+    const int64_t nc = (int64_t)a.cu_c[b + 1] - ks;
+    const int kk = nc <= 0 ? 0 : (nc < a.topk ? (int)nc : a.topk);
+
+    float tv[K];
+    int ti[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      tv[i] = -1.0f;  // below every score (scores are >= 0)
+      ti[i] = -1;
+    }
+    // Inserts (v, id) into the descending list; ids arrive ascending, so an
+    // equal score already listed keeps its place.
+    auto insert = [&](float v, int id) __attribute__((always_inline)) {
+      if (v > tv[K - 1]) {
+#pragma unroll
+        for (int i = K - 1; i >= 0; --i) {
+          const bool prev_less = i > 0 ? (tv[i > 0 ? i - 1 : 0] < v) : false;
+          if (tv[i] < v) {
+            tv[i] = prev_less ? tv[i > 0 ? i - 1 : 0] : v;
+            ti[i] = prev_less ? ti[i > 0 ? i - 1 : 0] : id;
+          }
+        }
+      }
+    };
+
+    const uint16_t* ckh = a.ck + ks * ck_stride + (int64_t)h * D + hb * 8;
+    auto load_k = [&](int64_t c0, u32x4* ka) __attribute__((always_inline)) {
+      const int64_t key = c0 + l32;
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        ka[s] = key < nc ? *reinterpret_cast<const u32x4*>(ckh + key * ck_stride + s * 16)
+                         : u32x4{0u, 0u, 0u, 0u};
+    };
+    u32x4 kbuf[2][NS];
+    if (nc > 0) load_k(0, kbuf[0]);
+    int cur = 0;
+    for (int64_t c0 = 0; c0 < nc; c0 += 32) {
+      if (c0 + 32 < nc) load_k(c0 + 32, kbuf[cur ^ 1]);
+      const u32x4* ka = kbuf[cur];
+      float p[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) p[v] = 0.0f;
+      for (int g = 0; g < a.g; ++g) {
+        const int hh = h * a.g + g;
+        u32x4 qb[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          qb[s] = row_ok ? *reinterpret_cast<const u32x4*>(
+                               a.q + (row * a.hq + hh) * D + s * 16 + hb * 8)
+                         : u32x4{0u, 0u, 0u, 0u};
+        const float l2 = row_ok ? a.lse[(int64_t)hh * a.nq + row] * LOG2E_REF : 0.0f;
+        f32x16 sacc;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) sacc = mfma32<DT>(ka[s], qb[s], sacc);
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          p[v] += __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], a.qk_scale, -l2));
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t key = c0 + acc_row(v, hb);
+        if (key < nc) insert(p[v], (int)key);
+      }
+      cur ^= 1;
+    }
+
+    // Merge with the partner lane's list (same row, the other 16 keys of
+    // every block): the better of (own[i], partner[K-1-i]) is a bitonic
+    // sequence holding the row's best K, sorted by a bitonic merge.
+    float mv[K];
+    int mi[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const float pv = __shfl_xor(tv[K - 1 - i], 32);
+      const int pi = __shfl_xor(ti[K - 1 - i], 32);
+      const bool own = ti[i] >= 0 && (pi < 0 || ranks_before(tv[i], ti[i], pv, pi));
+      mv[i] = own ? tv[i] : pv;
+      mi[i] = own ? ti[i] : pi;
+    }
+#pragma unroll
+    for (int j = K / 2; j > 0; j >>= 1) {
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+        if ((i & j) == 0) {
+          const int o = i | j;
+          const bool keep = mi[i] >= 0 && (mi[o] < 0 || ranks_before(mv[i], mi[i], mv[o], mi[o]));
+          const float v0 = keep ? mv[i] : mv[o], v1 = keep ? mv[o] : mv[i];
+          const int i0 = keep ? mi[i] : mi[o], i1 = keep ? mi[o] : mi[i];
+          mv[i] = v0; mv[o] = v1; mi[i] = i0; mi[o] = i1;
+        }
+      }
+    }
+    // The best kk ids, sorted ascending (bitonic sort; unused slots last).
+    int ids[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) ids[i] = (i < kk && mi[i] >= 0) ? mi[i] : 0x7fffffff;
+#pragma unroll
+    for (int size = 2; size <= K; size <<= 1) {
+#pragma unroll
+      for (int j = size / 2; j > 0; j >>= 1) {
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+          const int o = i ^ j;
+          if (o > i) {
+            const bool up = (i & size) == 0;
+            const int lo = ids[i] < ids[o] ? ids[i] : ids[o];
+            const int hi = ids[i] < ids[o] ? ids[o] : ids[i];
+            ids[i] = up ? lo : hi;
+            ids[o] = up ? hi : lo;
+          }
+        }
+      }
+    }
+    if (row_ok && hb == 0) {
+      int32_t* dst = a.out + ((int64_t)h * a.nq + row) * a.topk;
+#pragma unroll
+      for (int i = 0; i < K; ++i)
+        if (i < a.topk) dst[i] = (i < kk && ids[i] != 0x7fffffff) ? ids[i] : -1;
+    }
+  }
+}
+
+template <int DT, int D>
+int launch_block_score_d(const BlockScoreArgs& a, hipStream_t st) {
+  const int64_t waves = (a.nq + 31) / 32 * a.hkv;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+#define LSRM_BS_K(KV)                                                            \
+  hipLaunchKernelGGL((block_score_kernel<DT, D, KV>), grid, dim3(256), 0, st, a); \
+  break;
+  switch (a.topk <= 8 ? 8 : a.topk <= 16 ? 16 : a.topk <= 32 ? 32 : 64) {
+    case 8: LSRM_BS_K(8)
+    case 16: LSRM_BS_K(16)
+    case 32: LSRM_BS_K(32)
+    default: LSRM_BS_K(64)
+  }
+#undef LSRM_BS_K
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
+}
+
+}  // namespace lsrm
+
+using namespace lsrm;
+
+extern "C" int lsrm_block_score(const void* q, const void* compressed_k, int dtype,
+                                const float* lse, int64_t n_q, int64_t hq, int64_t hkv,
+                                int64_t head_dim, const int32_t* cu_seqlens_q,
+                                const int32_t* compressed_cu_seqlens, int64_t batch,
+                                int64_t topk, float sm_scale, int32_t* block_topk,
+                                void* stream) {
+  if (n_q < 0 || hq <= 0 || hkv <= 0 || batch <= 0 || topk <= 0 || hq % hkv != 0 ||
+      !cu_seqlens_q || !compressed_cu_seqlens ||
+      (n_q > 0 && (!q || !compressed_k || !lse || !block_topk)))
+    return LSRM_ERR_INVALID_ARG;
+  if (dtype != LSRM_F16 && dtype != LSRM_BF16) return LSRM_ERR_UNSUPPORTED;
+  if (topk > 64 || (head_dim != 32 && head_dim != 64 && head_dim != 128))
+    return LSRM_ERR_UNSUPPORTED;
+  if (n_q == 0) return LSRM_OK;
+  BlockScoreArgs a;
+  a.q = reinterpret_cast<const uint16_t*>(q);
+  a.ck = reinterpret_cast<const uint16_t*>(compressed_k);
+  a.lse = lse;
+  a.cu_q = cu_seqlens_q;
+  a.cu_c = compressed_cu_seqlens;
+  a.out = block_topk;
+  a.nq = n_q;
+  a.batch = batch;
+  a.hq = (int)hq;
+  a.hkv = (int)hkv;
+  a.g = (int)(hq / hkv);
+  a.topk = (int)topk;
+  a.qk_scale = sm_scale * LOG2E_REF;
+  hipStream_t st = (hipStream_t)stream;
+#define LSRM_BS_D(DT)                                               \
+  switch (head_dim) {                                               \
+    case 32: return launch_block_score_d<DT, 32>(a, st);            \
+    case 64: return launch_block_score_d<DT, 64>(a, st);            \
+    default: return launch_block_score_d<DT, 128>(a, st);           \
+  }
+  if (dtype == LSRM_BF16) {
+    LSRM_BS_D(LSRM_BF16)
+  } else {
+    LSRM_BS_D(LSRM_F16)
+  }
+#undef LSRM_BS_D
+}

@@ -79,6 +79,8 @@ _SIGNATURES = {
     "lsrm_reverse_query_map": (
         _I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _SZ, _P]),
     "lsrm_block_ids": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P]),
+    "lsrm_block_score": (
+        _I, [_P, _P, _I, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _F, _P, _P]),
 }
 
 
@@ -401,3 +403,40 @@ def block_ids(cu_seqblocks: torch.Tensor, cu_block_tokens: torch.Tensor, n_token
 
 def default_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
+
+
+# ------------------------------------------------------ learned selection --
+
+def block_score(q: torch.Tensor, compressed_k: torch.Tensor, lse: torch.Tensor, topk: int,
+                cu_seqlens_q: torch.Tensor, compressed_cu_seqlens: torch.Tensor,
+                sm_scale: float) -> torch.Tensor:
+    """get_block_score on the GPU -> block_topk [Hkv, Nq, topk] int32
+    (batch-local compressed-key ids ascending, -1 padded)."""
+    if q.dim() != 3 or compressed_k.dim() != 3 or q.shape[2] != compressed_k.shape[2]:
+        raise ValueError("q [Nq, Hq, D] and compressed_k [Nc, Hkv, D] must share D")
+    if q.dtype != compressed_k.dtype or q.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("q and compressed_k must share dtype float16 or bfloat16")
+    if q.shape[1] % compressed_k.shape[1] != 0:
+        raise ValueError("Hq must be a multiple of Hkv")
+    if topk <= 0:
+        raise ValueError("topk must be positive")
+    dev = _dev_check(q, compressed_k, lse, cu_seqlens_q, compressed_cu_seqlens)
+    nq, hq, d = q.shape
+    hkv = compressed_k.shape[1]
+    if tuple(lse.shape) != (hq, nq):
+        raise ValueError(f"lse must be [Hq, Nq] = [{hq}, {nq}]; got {tuple(lse.shape)}")
+    q = q.contiguous()
+    ck = compressed_k.contiguous()
+    lse = lse.contiguous().float()
+    cu_q = _i32(cu_seqlens_q)
+    cu_c = _i32(compressed_cu_seqlens)
+    batch = cu_q.numel() - 1
+    out = torch.full((hkv, nq, topk), -1, dtype=torch.int32, device=dev)
+    if nq == 0 or batch <= 0:
+        return out
+    with torch.cuda.device(dev):
+        _check(lib().lsrm_block_score(
+            _ptr(q), _ptr(ck), _DTYPE_CODE[q.dtype], _ptr(lse), nq, hq, hkv, d, _ptr(cu_q),
+            _ptr(cu_c), batch, topk, float(sm_scale), _ptr(out), _stream(dev)),
+            "lsrm_block_score")
+    return out

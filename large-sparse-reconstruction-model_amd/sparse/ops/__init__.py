@@ -1,8 +1,11 @@
 """gfx950 HIP replacement of LSRM's sparse/ops (same public names and
-signatures as sparse/ops/__init__.py:7-9, plus the compression and
-selection operators)."""
+signatures as sparse/ops/__init__.py:7-9, plus the compression, selection,
+learned-selection (get_block_score, sparse/ops/block_score.py:16-98) and
+compressed-attention operators)."""
 
+from .block_score import get_block_score
 from .block_window_attention import sparse_window_attention
+from .compressed_attention import compressed_attention
 from .compression import block_mean_pool, sparse3d_compression
 from .native_sparse_attention import (
     NSA,
@@ -16,6 +19,8 @@ from .selection import select_blocks
 __all__ = [
     "NSA",
     "block_mean_pool",
+    "compressed_attention",
+    "get_block_score",
     "native_sparse_attend",
     "select_blocks",
     "set_validation",
