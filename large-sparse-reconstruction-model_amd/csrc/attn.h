@@ -119,6 +119,194 @@ __device__ inline void load_selection(const AttnArgs& a, int h, int64_t q,
   __syncthreads();
 }
 
+// ------------------------------------------------ grouped (union) tiles --
+// A TILE_GROUPED tile holds consecutive queries whose selection rows differ.
+// build_union() collects the union of their selected blocks (ascending block
+// id, each block once) as the tile's key stream in SelLds, and for every
+// union segment the set of the tile's queries that selected it.  The tile is
+// then either run once over the union, each query masked to its own blocks
+// (UnionLds::ok), or once per run of identical rows.
+constexpr int UMAXW = 256;  // bitmap words: batch elements of <= 8192 blocks
+
+struct UnionLds {
+  uint32_t bits[UMAXW];         // selected batch-local block ids
+  int word_off[UMAXW];          // exclusive prefix of popcount(bits)
+  uint32_t seg_q[MAXSEL][4];    // segment s: bit q = tile query q selected it
+  int run_start[ROWS + 1];      // tile-local query offsets where runs begin
+  int n_runs, n_union, dup, run_keys, feasible, ok;
+};
+
+// Length and first token of batch-local block v of batch element (bs, nbb),
+// clamped as load_selection does; len 0 for an invalid or empty block.
+__device__ inline void block_span(const AttnArgs& a, int bs, int nbb, int v, int& t0,
+                                  int& len) {
+  t0 = 0;
+  len = 0;
+  if (v >= 0 && v < nbb && (int64_t)bs + v < a.nb) {
+    int64_t s0 = a.cu_blk[bs + v], s1 = a.cu_blk[bs + v + 1];
+    s0 = s0 < 0 ? 0 : (s0 > a.nk ? a.nk : s0);
+    s1 = s1 < s0 ? s0 : (s1 > a.nk ? a.nk : s1);
+    t0 = (int)s0;
+    len = (int)(s1 - s0);
+  }
+}
+
+// All 256 threads.  Queries q0 .. q0+qn-1 of kv head h (one batch element,
+// qn <= ROWS).  Fills s (the union stream) and u; u.ok says whether one
+// masked pass over the union is valid and no more keys than the runs' own
+// streams together (valid: the union has at most MAXSEL blocks, the batch
+// element at most UMAXW * 32 blocks, and no row lists a block twice --
+// repeated ids count twice and need the run-by-run passes).
+__device__ inline void build_union(const AttnArgs& a, int h, int64_t q0, int qn,
+                                   SelLds& s, UnionLds& u) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  int b, bs, nbb;
+  bool st;
+  query_batch(a.cu_q, a.batch, a.cu_sb, q0, &b, &bs, &nbb, &st);
+  const int nw = (nbb + 31) / 32;
+  const bool feasible = nw <= UMAXW;
+  for (int i = tid; i < UMAXW; i += blockDim.x) u.bits[i] = 0u;
+  if (tid == 0) {
+    u.dup = 0;
+    u.run_keys = 0;
+    u.feasible = feasible ? 1 : 0;
+  }
+  __syncthreads();
+  const int32_t* rows = a.topk + ((int64_t)h * a.nq + q0) * a.topk_n;
+  // Selected blocks (bitmap) and the run structure with each run's keys.
+  for (int e = tid; e < qn * a.topk_n; e += blockDim.x) {
+    int t0, len;
+    const int v = rows[e];
+    block_span(a, bs, nbb, v, t0, len);
+    if (len > 0 && feasible) atomicOr(&u.bits[v >> 5], 1u << (v & 31));
+  }
+  for (int q = tid; q < qn; q += blockDim.x) {
+    const int32_t* r1 = rows + (int64_t)q * a.topk_n;
+    bool start = q == 0;
+    if (!start) {
+      const int32_t* r0 = r1 - a.topk_n;
+      for (int j = 0; j < a.topk_n; ++j) {
+        const int x = (r1[j] >= 0 && r1[j] < nbb) ? r1[j] : -1;
+        const int y = (r0[j] >= 0 && r0[j] < nbb) ? r0[j] : -1;
+        if (x != y) {
+          start = true;
+          break;
+        }
+      }
+    }
+    u.word_off[q] = start ? 1 : 0;  // run-start flags, compacted below
+    if (start) {
+      int keys = 0;
+      for (int j = 0; j < a.topk_n; ++j) {
+        int t0, len;
+        block_span(a, bs, nbb, r1[j], t0, len);
+        keys += len;
+      }
+      atomicAdd(&u.run_keys, keys);
+    }
+  }
+  __syncthreads();
+  // Run starts in query order (one wave; qn <= ROWS).
+  if (tid < 64) {
+    int cnt = 0;
+    for (int base = 0; base < qn; base += 64) {
+      const int q = base + lane;
+      const bool f = q < qn && u.word_off[q] != 0;
+      const unsigned long long m = __ballot(f);
+      if (f) u.run_start[cnt + __popcll(m & ((1ull << lane) - 1ull))] = q;
+      cnt += __popcll(m);
+    }
+    if (lane == 0) {
+      u.run_start[cnt] = qn;
+      u.n_runs = cnt;
+    }
+  }
+  __syncthreads();
+  // Ranks of the selected blocks: exclusive prefix of the word popcounts.
+  if (tid < 64) {
+    int carry = 0;
+    for (int base = 0; base < UMAXW; base += 64) {
+      const int i = base + lane;
+      const int c = i < nw ? __popc(u.bits[i]) : 0;
+      int x = c;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+      }
+      u.word_off[i] = carry + x - c;
+      carry += __shfl(x, 63);
+    }
+    if (lane == 0) u.n_union = carry;
+  }
+  __syncthreads();
+  const int nu = u.n_union;
+  const bool fits = feasible && nu <= MAXSEL;
+  if (fits) {
+    for (int i = tid; i < nu * 4; i += blockDim.x) u.seg_q[i >> 2][i & 3] = 0u;
+    for (int i = tid; i < nw; i += blockDim.x) {
+      uint32_t m = u.bits[i];
+      int rank = u.word_off[i];
+      while (m) {
+        const int bit = __ffs(m) - 1;
+        m &= m - 1u;
+        int t0, len;
+        block_span(a, bs, nbb, i * 32 + bit, t0, len);
+        s.tok_tmp[rank] = t0;
+        s.len_tmp[rank] = len;
+        ++rank;
+      }
+    }
+  }
+  __syncthreads();
+  if (fits) {
+    // Membership; a block listed twice by one query needs the run passes.
+    for (int e = tid; e < qn * a.topk_n; e += blockDim.x) {
+      const int q = e / a.topk_n;
+      int t0, len;
+      const int v = rows[e];
+      block_span(a, bs, nbb, v, t0, len);
+      if (len > 0) {
+        const uint32_t w = u.bits[v >> 5];
+        const int rank = u.word_off[v >> 5] + __popc(w & ((1u << (v & 31)) - 1u));
+        const uint32_t bit = 1u << (q & 31);
+        if (atomicOr(&u.seg_q[rank][q >> 5], bit) & bit) u.dup = 1;
+      }
+    }
+  }
+  // The union stream: tok / cum / tb as load_selection builds them.
+  if (tid < 64 && fits) {
+    int cc = 0;
+    for (int base = 0; base < nu; base += 64) {
+      const int j = base + lane;
+      const int len = j < nu ? s.len_tmp[j] : 0;
+      const int t0 = j < nu ? s.tok_tmp[j] : 0;
+      int x = len;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+      }
+      if (j < nu) {
+        s.tok[j] = t0;
+        s.cum[j + 1] = cc + x;
+        s.tb[j] = t0 - (cc + x - len);
+      }
+      cc += __shfl(x, 63);
+    }
+    if (lane == 0) {
+      s.cum[0] = 0;
+      s.cum[nu + 1] = 0x7fffffff;
+      s.tb[nu] = 0;
+      s.n = nu;
+    }
+  }
+  __syncthreads();
+  if (tid == 0)
+    u.ok = (fits && !u.dup && s.cum[nu] <= u.run_keys) ? 1 : 0;
+  __syncthreads();
+}
+
 // Token of stream position p (< total keys); `cur` is a monotone cursor.
 __device__ inline int stream_token(const SelLds& s, int p, int& cur) {
   while (cur + 1 < s.n && s.cum[cur + 1] <= p) ++cur;

@@ -30,6 +30,8 @@
 //     not updated afterwards (no per-tile maximum, no rescaling); a tile
 //     whose row sums leave the safe range is recomputed with the exact
 //     online maximum.
+#include <type_traits>
+
 #include "attn.h"
 
 namespace lsrm {
@@ -63,7 +65,11 @@ __device__ inline float row_max(const f32x16* sc) {
                                        __builtin_bit_cast(float, (unsigned)sw[1]));
 }
 
-template <int DT, int D>
+// UNION false: the run tiles of the plan (every row of a tile shares one
+// key stream).  UNION true: the grouped tiles (see build_union), run with the
+// exact online-maximum pass and per-row key masks; a separate instantiation
+// so that the run-tile kernel carries none of that code or state.
+template <int DT, int D, bool UNION>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 sel_attn_fwd_kernel(AttnArgs a) {
   using G = KvTile<D>;
@@ -72,11 +78,15 @@ sel_attn_fwd_kernel(AttnArgs a) {
   __shared__ __align__(1024) char sK[4][G::BYTES];
   __shared__ __align__(1024) char sV[4][G::BYTES];
   __shared__ SelLds sel;
+  __shared__ typename std::conditional<UNION, UnionLds, int>::type ul;
   __shared__ int s_slot;
 
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
-  const int total = a.plan.head_off[a.hkv];
+  const int32_t* head_off = UNION ? a.plan.ghead_off : a.plan.head_off;
+  const int2* tiles = UNION ? a.plan.gtiles : a.plan.tiles;
+  int32_t* queue = a.plan.counter + (UNION ? 4 : 0);
+  const int total = head_off[a.hkv];
 
   // Loader geometry: load j of this wave covers keys (wv*LPW + j)*KPL + ...
   int ld_key[G::LPW], ld_byte[G::LPW];
@@ -94,12 +104,33 @@ sel_attn_fwd_kernel(AttnArgs a) {
   for (int j = 0; j < G::LPW; ++j) ld_lane_off[j] = (uint32_t)ld_row * row_bytes + ld_byte[j];
 
   for (;;) {
-    const int w = uniform(fetch_work(a.plan.counter, &s_slot));
+    const int w = uniform(fetch_work(queue, &s_slot));
     if (w >= total) break;
-    const int h = head_of(a.plan.head_off, a.hkv, w);
-    const int2 tile = a.plan.tiles[(int64_t)h * a.nq + (w - a.plan.head_off[h])];
-    const int q0 = tile.x, rows = tile.y * a.g;
-    load_selection(a, h, q0, sel);
+    const int h = head_of(head_off, a.hkv, w);
+    const int2 tile = tiles[(int64_t)h * a.nq + (w - head_off[h])];
+    const int q0 = tile.x, qn = tile.y, rows = qn * a.g;
+    // Passes over the tile: umode 0 -- one key stream shared by every row
+    // (a run tile); umode 1 -- a grouped tile run once over the union of
+    // its rows' blocks, each row masked to the blocks it selected; umode 2
+    // -- a grouped tile run once per run of identical rows, the other rows
+    // masked off.  Modes 1 and 2 use the exact online-maximum pass.
+    int umode = 0, n_pass = 1;
+    if constexpr (UNION) {
+      build_union(a, h, q0, qn, sel, ul);
+      umode = ul.ok ? 1 : 2;
+      n_pass = ul.ok ? 1 : ul.n_runs;
+    } else {
+      load_selection(a, h, q0, sel);
+    }
+    for (int pass = 0; pass < n_pass; ++pass) {
+    int q_lo = 0, q_hi = qn;  // the pass writes the rows of queries [q_lo, q_hi)
+    if constexpr (UNION) {
+      if (umode == 2) {
+        q_lo = ul.run_start[pass];
+        q_hi = ul.run_start[pass + 1];
+        load_selection(a, h, q0 + q_lo, sel);
+      }
+    }
     const int nkeys = uniform(sel.cum[sel.n]);
     const int ntiles = (nkeys + KT - 1) / KT;
     const int t_safe = uniform(sel.n > 0 ? sel.tok[0] : 0);  // in-bounds filler token
@@ -107,7 +138,9 @@ sel_attn_fwd_kernel(AttnArgs a) {
     // This wave's row and its Q operand (B of S^T = K Q^T).
     const int r = wv * 32 + l32;
     const bool row_ok = r < rows;
-    const bool wave_on = wv * 32 < rows;
+    const int qr = row_ok ? r / a.g : 0;  // the row's query within the tile
+    const bool row_in_pass = row_ok && qr >= q_lo && qr < q_hi;
+    const bool wave_on = wv * 32 < q_hi * a.g && wv * 32 + 32 > q_lo * a.g;
     const int64_t qi = q0 + (row_ok ? r / a.g : 0);
     const int hh = h * a.g + (row_ok ? r % a.g : 0);
     u32x4 qb[NS];
@@ -180,6 +213,41 @@ sel_attn_fwd_kernel(AttnArgs a) {
           for (int v = 0; v < 16; ++v)
             if (kb0 + blk * 32 + acc_row(v, hb) >= nkeys) sc[blk][v] = -__builtin_inf();
       }
+    };
+    // Grouped passes: keys a row does not attend score -inf.  umode 1: the
+    // 64-bit mask of tile kt's positions covered by union segments the row's
+    // query selected (segments are walked with a cursor, `useg`); umode 2:
+    // all or nothing by run membership.
+    int useg = 0;
+    auto mask_keys = [&](int kt, f32x16* sc) __attribute__((always_inline)) {
+      uint64_t m = 0ull;
+      if constexpr (!UNION) {
+        return;
+      } else if (umode == 1) {
+        const int p0 = kt * KT;
+        int sg = useg;
+        while (sel.cum[sg + 1] <= p0) ++sg;  // stops at the sentinel
+        useg = sg;
+        for (; sg < sel.n && sel.cum[sg] < p0 + KT; ++sg) {
+          const int lo = sel.cum[sg] > p0 ? sel.cum[sg] - p0 : 0;
+          const int hi = sel.cum[sg + 1] - p0 < KT ? sel.cum[sg + 1] - p0 : KT;
+          const uint64_t upto = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+          const uint64_t range = upto & ~((1ull << lo) - 1ull);
+          if ((ul.seg_q[sg][qr >> 5] >> (qr & 31)) & 1u) m |= range;
+        }
+      } else {
+        m = row_in_pass ? ~0ull : 0ull;
+        if (kt * KT + KT > nkeys) {
+          const int hi = nkeys - kt * KT;
+          m &= hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+        }
+      }
+      const uint64_t mh = m >> (hb * 4);  // position of slot v: (v/4)*8 + hb*4 + v%4
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (!((mh >> (blk * 32 + (v / 4) * 8 + (v % 4))) & 1ull)) sc[blk][v] = -__builtin_inf();
     };
 
     // Softmax of one score tile against m_run: P packed to the 16-bit type
@@ -332,8 +400,16 @@ sel_attn_fwd_kernel(AttnArgs a) {
       __syncthreads();
       if (wave_on && ntiles > 0) {
         scores(sK[0], sA);
-        mask_tail(0, sA);
-        m_run = row_max(sA) * a.scale_log2;
+        if (umode == 0) {
+          mask_tail(0, sA);
+          m_run = row_max(sA) * a.scale_log2;
+        } else {
+          // A row may attend nothing in tile 0: keep the reference finite so
+          // that masked scores give exp2(-inf) = 0, never inf - inf.
+          useg = 0;
+          mask_keys(0, sA);
+          m_run = __builtin_elementwise_maximum(row_max(sA) * a.scale_log2, -1.0e30f);
+        }
       }
       if (ntiles > 0) {
         advance(koff);
@@ -362,7 +438,14 @@ sel_attn_fwd_kernel(AttnArgs a) {
       voff_keep(koff);
 
       if (wave_on) {
-        mask_tail(kt, sc);
+        if constexpr (SAFE) {
+          if (umode == 0)
+            mask_tail(kt, sc);
+          else
+            mask_keys(kt, sc);
+        } else {
+          mask_tail(kt, sc);
+        }
         if constexpr (SAFE) {
           if constexpr (!FIRST) pv(sV[k_wr], pp);  // before any rescale of O
           const float m_tile = row_max(sc) * a.scale_log2;
@@ -422,18 +505,22 @@ sel_attn_fwd_kernel(AttnArgs a) {
     // the sums grow out of range; a row sum that is not below 2^32 (inf and
     // NaN included) sends the whole tile through the exact online pass.
     prologue();
-    run(Phase<0>{});
-    const float l_fast = l_run + __shfl_xor(l_run, 32);
-    if (uniform(__syncthreads_or(!(l_fast < 4294967296.0f)))) {
-      wait_copies();  // the fast pass's trailing copies land before reuse
-      __syncthreads();
-      prologue();
+    if (umode == 0) {
+      run(Phase<0>{});
+      const float l_fast = l_run + __shfl_xor(l_run, 32);
+      if (uniform(__syncthreads_or(!(l_fast < 4294967296.0f)))) {
+        wait_copies();  // the fast pass's trailing copies land before reuse
+        __syncthreads();
+        prologue();
+        run(Phase<1>{});
+      }
+    } else {
       run(Phase<1>{});
     }
 
     // Epilogue: normalise, store O rows and LSE.
     const float l_tot = l_run + __shfl_xor(l_run, 32);
-    if (row_ok) {
+    if (row_in_pass) {
       const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
       uint16_t* orow = a.out + (qi * a.hq + hh) * D;
 #pragma unroll
@@ -449,19 +536,31 @@ sel_attn_fwd_kernel(AttnArgs a) {
         a.lse[(int64_t)hh * a.nq + qi] =
             l_tot > 0.0f ? m_run + log2f(l_tot) : -__builtin_inf();
     }
+    if (n_pass > 1) {
+      wait_copies();  // this pass's trailing copies land before the next pass
+      __syncthreads();
+    }
+    }  // passes
   }
   wait_copies();  // no copy into LDS outlives the workgroup
-  leave_queue(a.plan.counter, a.plan.counter + 2);
+  leave_queue(queue, queue + 2);
 }
 
 template <int DT, int D>
 int launch_fwd_t(const AttnArgs& a, hipStream_t st) {
-  const void* fn = reinterpret_cast<const void*>(&sel_attn_fwd_kernel<DT, D>);
+  const void* fn = reinterpret_cast<const void*>(&sel_attn_fwd_kernel<DT, D, false>);
   const int grid = persistent_grid(fn, 256, 0);
   if (grid <= 0) return LSRM_ERR_LAUNCH;
-  hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D>), dim3(grid), dim3(256), 0, st,
+  hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, false>), dim3(grid), dim3(256), 0, st,
                      a);
   LSRM_CHECK_LAUNCH();
+  if (a.plan.gtiles) {  // forward plans: the grouped tiles (often none)
+    const void* fu = reinterpret_cast<const void*>(&sel_attn_fwd_kernel<DT, D, true>);
+    const int gu = persistent_grid(fu, 256, 0);
+    if (gu <= 0) return LSRM_ERR_LAUNCH;
+    hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, true>), dim3(gu), dim3(256), 0, st, a);
+    LSRM_CHECK_LAUNCH();
+  }
   return LSRM_OK;
 }
 

@@ -65,7 +65,7 @@ int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
               int64_t batch, int g, bool backward, AttnWs& w, hipStream_t st) {
   const int tq = ROWS / g;
   int rc = build_tile_plan(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, tq, ws,
-                           w.plan, st);
+                           w.plan, st, !backward);
   if (rc) return rc;
   if (backward) {
     w.rev = RevMap{};

@@ -7,12 +7,20 @@
 
 namespace lsrm {
 
-// Queries of one kv head that share a selection row: [q0, q0 + qn).
+// Queries of one kv head that share a selection row: [q0, q0 + qn) as
+// int2 {q0, qn}.  A forward plan also lists grouped tiles: consecutive short
+// runs of one batch element whose rows differ, run over the union of their
+// blocks (a second work queue).
 struct TilePlan {
-  int2* tiles;          // [hkv, n_q]; tile t of head h at tiles[h * n_q + t]
-  int32_t* tile_count;  // [hkv]
-  int32_t* head_off;    // [hkv + 1] exclusive prefix of tile_count
-  int32_t* counter;     // persistent-kernel work counter, zeroed by the plan
+  int2* tiles;           // [hkv, n_q]; tile t of head h at tiles[h * n_q + t]
+  int32_t* tile_count;   // [hkv]
+  int32_t* head_off;     // [hkv + 1] exclusive prefix of tile_count
+  int32_t* counter;      // work counters, zeroed by the plan: [0], [2] run
+                         // tiles (fwd / dq), [1], [3] key chunks (dK/dV),
+                         // [4], [6] grouped tiles
+  int2* gtiles;          // [hkv, n_q] grouped tiles (forward plans)
+  int32_t* gtile_count;  // [hkv]
+  int32_t* ghead_off;    // [hkv + 1]
 };
 
 // CSR map block -> rows (tiles or queries) that selected it, per kv head.
@@ -24,10 +32,12 @@ struct RevMap {
 };
 
 // Workspace carving: pass a Carver with base == nullptr to size.
+// group_short: move consecutive short run tiles into grouped tiles (forward
+// plans only; the backward kernels need run tiles).
 int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
                     int64_t topk_n, const int32_t* cu_q, int64_t batch,
                     const int32_t* cu_sb, int tq, Carver& ws, TilePlan& plan,
-                    hipStream_t st);
+                    hipStream_t st, bool group_short = false);
 
 // rows_are_tiles: rows are the tiles of `plan` (row r of head h reads the
 // selection of query tiles[h*nq + r].x); otherwise rows are queries.

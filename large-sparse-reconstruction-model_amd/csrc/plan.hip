@@ -259,26 +259,94 @@ struct EmitTilesW {
   }
 };
 
-__global__ void head_offsets_kernel(const int32_t* counts, int hkv,
-                                    int32_t* head_off, int32_t* counter) {
+
+// --------------------------------------------------------- union tiles --
+// Consecutive short run tiles (fewer than tq / 4 queries) of one batch
+// element whose first queries fall in the same window of 3 tq / 4 queries
+// form a group of at most tq - 1 queries.  Groups of two or more run tiles
+// become grouped tiles (TilePlan::gtiles): the forward runs them over the
+// union of their queries' selections with a per-query mask, or run by run
+// when that is cheaper.  Every other run tile is kept as it is.
+struct GroupF {
+  const int2* tiles;
+  const int32_t* count;
+  const int32_t* cu_q;
+  int64_t batch, nq;
+  int short_q, window_q;
+  __device__ int64_t limit(int h, int64_t) const { return count[h]; }
+  __device__ int operator()(int h, int64_t t) const {
+    if (t == 0) return 1;
+    const int2 a = tiles[(int64_t)h * nq + t - 1], b = tiles[(int64_t)h * nq + t];
+    if (a.y >= short_q || b.y >= short_q) return 1;
+    if (a.x / window_q != b.x / window_q) return 1;
+    return batch_of(cu_q, batch, a.x) != batch_of(cu_q, batch, b.x) ? 1 : 0;
+  }
+};
+struct GroupW {
+  int32_t* gstart;  // [hkv, nq + 1]
+  int64_t nq;
+  __device__ void operator()(int h, int64_t t, int ex, int v, int64_t lim) const {
+    int32_t* gs = gstart + (int64_t)h * (nq + 1);
+    if (v) gs[ex] = (int32_t)t;
+    if (t == lim - 1) gs[ex + v] = (int32_t)lim;
+  }
+};
+// Second pass over the groups: grouped (>= 2 run tiles) or kept.
+struct SplitF {
+  const int32_t* gstart;
+  const int32_t* n_groups;
+  int64_t nq;
+  __device__ int64_t limit(int h, int64_t) const { return n_groups[h]; }
+  __device__ int operator()(int h, int64_t s) const {
+    const int32_t* gs = gstart + (int64_t)h * (nq + 1);
+    return gs[s + 1] - gs[s] > 1 ? 1 : 0;
+  }
+};
+struct SplitW {
+  const int2* run_tiles;
+  const int32_t* gstart;
+  int64_t nq;
+  int2* tiles;
+  int2* gtiles;
+  __device__ void operator()(int h, int64_t s, int ex, int v, int64_t) const {
+    const int32_t* gs = gstart + (int64_t)h * (nq + 1);
+    const int t0 = gs[s], t1 = gs[s + 1];
+    const int2 first = run_tiles[(int64_t)h * nq + t0];
+    const int2 last = run_tiles[(int64_t)h * nq + t1 - 1];
+    const int2 out = make_int2(first.x, last.x + last.y - first.x);
+    if (v)
+      gtiles[(int64_t)h * nq + ex] = out;
+    else
+      tiles[(int64_t)h * nq + (s - ex)] = out;
+  }
+};
+
+// tile_count = groups - grouped tiles (grouping) or the run count.
+__global__ void plan_offsets_kernel(const int32_t* n_groups, int32_t* tile_count,
+                                    const int32_t* gtile_count, int hkv,
+                                    int32_t* head_off, int32_t* ghead_off,
+                                    int32_t* counter) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
-    int acc = 0;
+    int acc = 0, gacc = 0;
     head_off[0] = 0;
+    ghead_off[0] = 0;
     for (int h = 0; h < hkv; ++h) {
-      acc += counts[h];
+      const int g = gtile_count[h];
+      const int c = n_groups ? n_groups[h] - g : tile_count[h];
+      tile_count[h] = c;
+      acc += c;
+      gacc += g;
       head_off[h + 1] = acc;
+      ghead_off[h + 1] = gacc;
     }
-    counter[0] = 0;
-    counter[1] = 0;
-    counter[2] = 0;
-    counter[3] = 0;
+    for (int i = 0; i < 8; ++i) counter[i] = 0;
   }
 }
 
 int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
                     int64_t topk_n, const int32_t* cu_q, int64_t batch,
                     const int32_t* cu_sb, int tq, Carver& ws, TilePlan& plan,
-                    hipStream_t st) {
+                    hipStream_t st, bool group_short) {
   uint8_t* brk = ws.take<uint8_t>((size_t)(hkv * nq));
   int32_t* run_start = ws.take<int32_t>((size_t)(hkv * (nq + 1)));
   int32_t* n_runs = ws.take<int32_t>((size_t)hkv);
@@ -287,8 +355,24 @@ int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
   plan.tile_count = ws.take<int32_t>((size_t)hkv);
   plan.head_off = ws.take<int32_t>((size_t)(hkv + 1));
   plan.counter = ws.take<int32_t>(64);
+  plan.gtile_count = ws.take<int32_t>((size_t)hkv);
+  plan.ghead_off = ws.take<int32_t>((size_t)(hkv + 1));
+  plan.gtiles = nullptr;
+  int2* run_tiles = plan.tiles;
+  int32_t* run_count = plan.tile_count;
+  int32_t* gstart = nullptr;
+  int32_t* n_groups = nullptr;
+  if (group_short) {
+    plan.gtiles = ws.take<int2>((size_t)(hkv * (nq > 0 ? nq : 1)));
+    run_tiles = ws.take<int2>((size_t)(hkv * (nq > 0 ? nq : 1)));
+    run_count = ws.take<int32_t>((size_t)hkv);
+    gstart = ws.take<int32_t>((size_t)(hkv * (nq + 1)));
+    n_groups = ws.take<int32_t>((size_t)hkv);
+  }
   if (!ws.base || ws.dry) return LSRM_OK;
   if (!ws.ok()) return LSRM_ERR_WORKSPACE;
+  int rc0 = launch_zero_i32(plan.gtile_count, hkv, st);
+  if (rc0) return rc0;
 
   if (nq > 0) {
     dim3 grid(ceil_div(nq, 256), (unsigned)hkv);
@@ -303,15 +387,28 @@ int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
                       sums, n_runs, st);
     if (rc) return rc;
     rc = run_scan(RunTilesF{run_start, n_runs, nq, tq},
-                  EmitTilesW{run_start, plan.tiles, nq, tq}, nq, (int)hkv, sums,
-                  plan.tile_count, st);
+                  EmitTilesW{run_start, run_tiles, nq, tq}, nq, (int)hkv, sums,
+                  run_count, st);
     if (rc) return rc;
+    if (group_short) {
+      const int short_q = tq / 4 > 1 ? tq / 4 : 1;
+      const int window_q = (3 * tq) / 4 > 1 ? (3 * tq) / 4 : 1;
+      rc = run_scan(GroupF{run_tiles, run_count, cu_q, batch, nq, short_q, window_q},
+                    GroupW{gstart, nq}, nq, (int)hkv, sums, n_groups, st);
+      if (rc) return rc;
+      rc = run_scan(SplitF{gstart, n_groups, nq},
+                    SplitW{run_tiles, gstart, nq, plan.tiles, plan.gtiles}, nq, (int)hkv,
+                    sums, plan.gtile_count, st);
+      if (rc) return rc;
+    }
   } else {
     int rc = launch_zero_i32(plan.tile_count, hkv, st);
     if (rc) return rc;
+    n_groups = nullptr;
   }
-  hipLaunchKernelGGL(head_offsets_kernel, dim3(1), dim3(64), 0, st,
-                     plan.tile_count, (int)hkv, plan.head_off, plan.counter);
+  hipLaunchKernelGGL(plan_offsets_kernel, dim3(1), dim3(64), 0, st,
+                     nq > 0 ? n_groups : nullptr, plan.tile_count, plan.gtile_count, (int)hkv,
+                     plan.head_off, plan.ghead_off, plan.counter);
   LSRM_CHECK_LAUNCH();
   return LSRM_OK;
 }

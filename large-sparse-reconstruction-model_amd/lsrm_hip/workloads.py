@@ -43,6 +43,9 @@ class Workload:
     seed: int = 0
     qk_scale: float = 0.5              # std of Q/K/V entries
     lowrank: Optional[dict] = None     # config 5 near-tie construction
+    voxel_coords: Optional[np.ndarray] = None  # cfg3: (x, y, z) cells of the voxel tokens
+    n_image_tokens: int = 0            # cfg3: tokens before the voxel tokens
+    n_image_blocks: int = 0
 
     @property
     def n_blocks(self) -> int:
@@ -96,16 +99,20 @@ def morton3(x: np.ndarray, y: np.ndarray, z: np.ndarray, bits: int = 6) -> np.nd
 
 
 def morton_voxel_runs(n_vox: int, grid: int, lo: int, hi: int,
-                      rng: np.random.Generator) -> np.ndarray:
+                      rng: np.random.Generator, return_coords: bool = False):
     """Distinct random occupied cells of a grid^3 volume sorted by Morton code
     and cut into consecutive runs of U[lo, hi] tokens (spatially coherent
-    blocks).  Returns the run lengths."""
+    blocks).  Returns the run lengths (and, with return_coords, the cells'
+    integer (x, y, z) coordinates [n_vox, 3] in token order)."""
     cells = rng.choice(grid ** 3, size=n_vox, replace=False)
     x, y, z = cells // (grid * grid), (cells // grid) % grid, cells % grid
     bits = int(math.log2(grid))
     order = np.argsort(morton3(x, y, z, bits), kind="stable")
     assert order.shape[0] == n_vox
-    return uniform_partition(n_vox, lo, hi, rng)
+    runs = uniform_partition(n_vox, lo, hi, rng)
+    if return_coords:
+        return runs, np.stack([x[order], y[order], z[order]], axis=1).astype(np.int64)
+    return runs
 
 
 def _cu(sizes: np.ndarray) -> torch.Tensor:
@@ -134,12 +141,16 @@ def config(idx: int, n: Optional[int] = None, heads: Optional[int] = None) -> Wo
         if n < 131072:  # shrunken variant: keep 8 image blocks, scale their size
             img_len = max(32, n // 128)
         n_vox = n - n_img_blocks * img_len
-        runs = morton_voxel_runs(n_vox, 64, 32, 512, rng)
+        runs, vox = morton_voxel_runs(n_vox, 64, 32, 512, rng, return_coords=True)
         sizes = np.concatenate([np.full(n_img_blocks, img_len), runs])
-        return Workload("cfg3", n, heads or 24, heads or 24, 64, torch.bfloat16, 16, _cu(sizes),
-                        torch.tensor([0, len(sizes)], dtype=torch.int32),
-                        torch.tensor([0, n], dtype=torch.int32),
-                        forced_blocks=list(range(n_img_blocks)), seed=3)
+        w = Workload("cfg3", n, heads or 24, heads or 24, 64, torch.bfloat16, 16, _cu(sizes),
+                     torch.tensor([0, len(sizes)], dtype=torch.int32),
+                     torch.tensor([0, n], dtype=torch.int32),
+                     forced_blocks=list(range(n_img_blocks)), seed=3)
+        w.voxel_coords = vox
+        w.n_image_tokens = n_img_blocks * img_len
+        w.n_image_blocks = n_img_blocks
+        return w
     if idx == 5:
         n = n or 524288
         sizes = lognormal_partition(n, math.log(64.0), 1.0, 8, 1024, rng)

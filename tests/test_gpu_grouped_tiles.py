@@ -1,0 +1,98 @@
+"""GPU parity of the forward on per-token selection rows: consecutive
+queries whose rows differ are grouped into tiles that run over the union of
+their blocks with a per-query mask, or run by run (duplicated ids, unions too
+large or more expensive than the runs).  Checked against the fp32 oracle at
+the attention tolerance, including the LSE."""
+
+import numpy as np
+import pytest
+import torch
+
+import lsrm_hip as H
+from helpers import assert_attn_close
+from lsrm_hip import workloads as W
+from oracle.attention import sel_attn_ref
+from oracle.select3d import nearest_blocks_ref, volume_points_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _voxel_case(n=16384, hq=2, hkv=2, topk=16, seed=0):
+    """cfg3-style voxel tokens (Morton-ordered cells of a 64^3 grid cut into
+    runs of 32..512) with the 3D-aware per-token rows (nearest centroids)."""
+    w = W.config(3, n=n, heads=hkv)
+    nv = w.voxel_coords.shape[0]
+    cu_blk = w.cu_block_tokens.numpy().astype(np.int64)
+    cu_v = (cu_blk[w.n_image_blocks:] - cu_blk[w.n_image_blocks]).astype(np.int32)
+    coords = np.concatenate([np.zeros((nv, 1), np.int64), w.voxel_coords], axis=1)
+    pts = volume_points_ref(coords, 64, 1.0)
+    sel = nearest_blocks_ref(pts, cu_v, np.array([0, len(cu_v) - 1]), np.array([0, nv]), topk)
+    topk_idx = torch.from_numpy(np.broadcast_to(sel, (hkv, nv, topk)).copy())
+    g = torch.Generator().manual_seed(seed)
+    q = (0.5 * torch.randn(nv, hq, 64, generator=g)).to(torch.bfloat16)
+    k = (0.5 * torch.randn(nv, hkv, 64, generator=g)).to(torch.bfloat16)
+    v = (0.5 * torch.randn(nv, hkv, 64, generator=g)).to(torch.bfloat16)
+    cu_sb = torch.tensor([0, len(cu_v) - 1], dtype=torch.int32)
+    cu_q = torch.tensor([0, nv], dtype=torch.int32)
+    return q, k, v, topk_idx, cu_sb, torch.from_numpy(cu_v), cu_q
+
+
+def _check(q, k, v, topk_idx, cu_sb, cu_blk, cu_q):
+    scale = 1.0 / 8.0
+    o, lse = H.sel_attn_fwd(*(t.to(DEV) for t in (q, k, v, topk_idx, cu_sb, cu_blk, cu_q)),
+                            scale)
+    o_ref, lse_ref = sel_attn_ref(q.float(), k.float(), v.float(), topk_idx, cu_sb, cu_blk,
+                                  cu_q, scale)
+    assert_attn_close(o, o_ref, "out")
+    lse_c = lse.cpu()
+    fin = torch.isfinite(lse_ref)
+    assert torch.equal(torch.isfinite(lse_c), fin)
+    if fin.any():
+        assert float((lse_c[fin] - lse_ref[fin]).abs().max()) <= 2e-2
+
+
+def test_3d_aware_rows_union_tiles():
+    _check(*_voxel_case())
+
+
+def test_3d_aware_rows_gqa():
+    _check(*_voxel_case(n=8192, hq=8, hkv=2, topk=8, seed=1))
+
+
+def test_rows_with_duplicate_ids_run_passes():
+    q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _voxel_case(n=8192, topk=8, seed=2)
+    topk_idx = topk_idx.clone()
+    topk_idx[:, ::3, 7] = topk_idx[:, ::3, 0]   # every third query lists a block twice
+    _check(q, k, v, topk_idx, cu_sb, cu_blk, cu_q)
+
+
+def test_random_per_token_rows_union_or_runs():
+    # Unrelated rows: unions of 128 queries exceed the runs' own keys or the
+    # 256-block limit, so tiles fall back to passes per run.  Includes -1
+    # padding, out-of-range ids and empty rows.
+    w = W.config(2, n=6000, heads=2)
+    q, k, v = W.tensors(w, "cpu")
+    g = torch.Generator().manual_seed(4)
+    nb = w.n_blocks
+    topk_idx = torch.randint(0, nb, (w.hkv, w.n, 12), generator=g, dtype=torch.int32)
+    topk_idx[:, ::5, 9:] = -1
+    topk_idx[:, 1::7, 3] = nb + 5
+    topk_idx[:, 2::11, :] = -1
+    _check(q, k, v, topk_idx, w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens)
+
+
+def test_two_batch_elements_short_runs():
+    # short runs on both sides of a batch boundary are never grouped together
+    q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _voxel_case(n=8192, topk=8, seed=3)
+    nv = q.shape[0]
+    half = nv // 2
+    nbv = cu_blk.numel() - 1
+    # batch element 1 = the same tokens again, with its own copy of the blocks
+    q2 = torch.cat([q, q]); k2 = torch.cat([k, k]); v2 = torch.cat([v, v])
+    cu_blk2 = torch.cat([cu_blk, cu_blk[1:] + nv])
+    cu_sb2 = torch.tensor([0, nbv, 2 * nbv], dtype=torch.int32)
+    cu_q2 = torch.tensor([0, nv, 2 * nv], dtype=torch.int32)
+    rows2 = torch.cat([topk_idx, topk_idx], dim=1)
+    _check(q2, k2, v2, rows2, cu_sb2, cu_blk2, cu_q2)
+    assert half > 0
