@@ -28,6 +28,12 @@
  *                             (sparse_window_attention)
  *   lsrm_block_score          sparse/ops/block_score.py:16-98 (get_block_score,
  *                             the learned per-token block selection)
+ *   lsrm_volume_points        misc/sparse_utils.py:644-650 (from_volcoords_to_points)
+ *   lsrm_nearest_blocks       misc/sparse_utils.py:1219-1273 (the 3D-aware
+ *                             per-token selection of build_volume_to_volume_attn)
+ *   lsrm_block_separation     misc/sparse_utils.py:592-641 (compute_block_separation)
+ *   lsrm_block_sort           misc/sparse_utils.py:95-152 (sort_image_blocks,
+ *                             sort_volume_blocks: the sort permutation)
  */
 #ifndef LSRM_HIP_H
 #define LSRM_HIP_H
@@ -275,6 +281,66 @@ int lsrm_block_score(const void* q, const void* compressed_k, int dtype,
                      const int32_t* compressed_cu_seqlens, int64_t batch,
                      int64_t topk, float sm_scale, int32_t* block_topk,
                      void* stream);
+
+/* ------------------------------------------------------------------------
+ * 3D-aware per-token block selection (volume to volume).
+ * lsrm_volume_points: coords [n_tokens, 4] int32 (batch, c1, c2, c3) ->
+ *   points [n_tokens, 3] fp32 (x, y, z) = (f(c3), f(c2), f(c1)),
+ *   f(c) = 2 * (c / (volume_res - 1) - 0.5) * radius in fp32, radius =
+ *   bbox_radius * 1.05 (misc/sparse_utils.py:644-650).
+ * lsrm_nearest_blocks: points [n_tokens, 3] fp32, centroids [n_blocks, 3]
+ *   fp32 (block means of the points: lsrm_block_mean_pool of the points),
+ *   cu_seqlens / cu_seqblocks [batch + 1]; for every token the
+ *   min(topk, blocks of its batch element) blocks with the nearest centroid
+ *   (squared distance in fp64, ties to the lower id), batch-local ids
+ *   ascending, -1 padded, written identically for each of the hkv heads:
+ *   block_topk [hkv, n_tokens, topk] int32.  topk <= 64.  No workspace.
+ * Replaces misc/sparse_utils.py:1219-1273 (use_3d_aware_attn branch).
+ * ---------------------------------------------------------------------- */
+int lsrm_volume_points(const int32_t* coords, int64_t n_tokens, int64_t volume_res,
+                       float radius, float* points, void* stream);
+int lsrm_nearest_blocks(const float* points, const float* centroids,
+                        const int32_t* cu_seqlens, const int32_t* cu_seqblocks,
+                        int64_t batch, int64_t n_tokens, int64_t topk, int64_t hkv,
+                        int32_t* block_topk, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Block separation (compute_block_separation).
+ *   coords [n_tokens, 1 + dim] int32: batch id (tokens sorted by batch,
+ *   ids 0..batch-1), then dim (1..3) non-negative grid coordinates;
+ *   block_size / resolution: host arrays of dim ints.  A token lies in block
+ *   (c[d] / block_size[d])_d, flattened row-major over
+ *   resolution[d] / block_size[d] blocks per dimension; tokens outside the
+ *   grid are not counted.  Outputs: cu_seqblocks [batch + 1] (non-empty
+ *   blocks per batch element, prefix), cu_block_tokens [batch * bins + 1]
+ *   (prefix of the non-empty blocks' token counts in (batch, block) order;
+ *   the first *n_blocks + 1 entries are valid), n_blocks (device int32).
+ * Replaces misc/sparse_utils.py:592-641.
+ * ---------------------------------------------------------------------- */
+size_t lsrm_block_separation_workspace_size(int64_t batch, int dim,
+                                            const int32_t* block_size,
+                                            const int32_t* resolution);
+int lsrm_block_separation(const int32_t* coords, int64_t n_tokens, int dim,
+                          const int32_t* block_size, const int32_t* resolution,
+                          int64_t batch, int32_t* cu_seqblocks, int32_t* cu_block_tokens,
+                          int32_t* n_blocks, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* ------------------------------------------------------------------------
+ * Block sort permutation (sort_volume_blocks / sort_image_blocks).
+ *   coords [n_tokens, 4] int32, non-negative: layout 0 (volume) =
+ *   (batch, c1, c2, c3) with dims = {volume_res}; layout 1 (image) =
+ *   (batch, image, row, col) with dims = {n_images, patch_res} (host
+ *   int64 arrays).  Sort key: the reference's offsets (batch, then block
+ *   coordinates c / block_size, then in-block coordinates c % block_size);
+ *   perm [n_tokens] int32 receives the token indices in ascending key
+ *   order (stable: equal keys keep token order).
+ * Replaces the torch.argsort of misc/sparse_utils.py:95-152.
+ * ---------------------------------------------------------------------- */
+size_t lsrm_block_sort_workspace_size(int64_t n_tokens);
+int lsrm_block_sort(const int32_t* coords, int64_t n_tokens, int layout, int64_t block_size,
+                    const int64_t* dims, int32_t* perm, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

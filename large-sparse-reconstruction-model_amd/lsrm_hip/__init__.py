@@ -81,6 +81,12 @@ _SIGNATURES = {
     "lsrm_block_ids": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P]),
     "lsrm_block_score": (
         _I, [_P, _P, _I, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _F, _P, _P]),
+    "lsrm_volume_points": (_I, [_P, _I64, _I64, _F, _P, _P]),
+    "lsrm_nearest_blocks": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
+    "lsrm_block_separation_workspace_size": (_SZ, [_I64, _I, _P, _P]),
+    "lsrm_block_separation": (_I, [_P, _I64, _I, _P, _P, _I64, _P, _P, _P, _P, _SZ, _P]),
+    "lsrm_block_sort_workspace_size": (_SZ, [_I64]),
+    "lsrm_block_sort": (_I, [_P, _I64, _I, _I64, _P, _P, _P, _SZ, _P]),
 }
 
 
@@ -440,3 +446,98 @@ def block_score(q: torch.Tensor, compressed_k: torch.Tensor, lse: torch.Tensor, 
             _ptr(cu_c), batch, topk, float(sm_scale), _ptr(out), _stream(dev)),
             "lsrm_block_score")
     return out
+
+
+# ------------------------------------------------------------ 3D-aware --
+
+def volume_points(coords: torch.Tensor, volume_res: int, bbox_radius: float) -> torch.Tensor:
+    """coords [N, 4] ints (batch, c1, c2, c3) -> points [N, 3] fp32 (x, y, z)."""
+    if coords.dim() != 2 or coords.shape[1] != 4:
+        raise ValueError("coords must be [N, 4] (batch, c1, c2, c3)")
+    dev = _dev_check(coords)
+    c = _i32(coords)
+    n = c.shape[0]
+    pts = torch.empty(n, 3, dtype=torch.float32, device=dev)
+    radius = float(torch.tensor(bbox_radius * 1.05, dtype=torch.float32))
+    with torch.cuda.device(dev):
+        _check(lib().lsrm_volume_points(_ptr(c), n, int(volume_res), radius, _ptr(pts),
+                                        _stream(dev)), "lsrm_volume_points")
+    return pts
+
+
+def nearest_blocks(points: torch.Tensor, cu_block_tokens: torch.Tensor,
+                   cu_seqblocks: torch.Tensor, cu_seqlens: torch.Tensor, topk: int,
+                   num_kv_heads: int = 2) -> torch.Tensor:
+    """Per-token nearest block centroids -> block_topk [num_kv_heads, N, topk]
+    int32 (batch-local ids ascending, -1 padded)."""
+    if points.dim() != 2 or points.shape[1] != 3 or points.dtype != torch.float32:
+        raise ValueError("points must be [N, 3] float32")
+    if topk <= 0:
+        raise ValueError("topk must be positive")
+    dev = _dev_check(points, cu_block_tokens, cu_seqblocks, cu_seqlens)
+    points = points.contiguous()
+    n = points.shape[0]
+    cu_q = _i32(cu_seqlens)
+    cu_sb = _i32(cu_seqblocks)
+    centroids = block_mean_pool(points, cu_block_tokens, torch.float32)
+    out = torch.full((num_kv_heads, n, topk), -1, dtype=torch.int32, device=dev)
+    batch = cu_q.numel() - 1
+    if n == 0 or batch <= 0:
+        return out
+    with torch.cuda.device(dev):
+        _check(lib().lsrm_nearest_blocks(_ptr(points), _ptr(centroids), _ptr(cu_q),
+                                         _ptr(cu_sb), batch, n, topk, num_kv_heads,
+                                         _ptr(out), _stream(dev)), "lsrm_nearest_blocks")
+    return out
+
+
+# ------------------------------------------------------- metadata builders --
+
+def block_separation(coords: torch.Tensor, dim: int, block_size, resolution,
+                     batch: int):
+    """compute_block_separation on the GPU -> (cu_seqblocks [batch + 1],
+    cu_block_tokens [n_blocks + 1]) int32 (one host synchronisation, to
+    size the second output)."""
+    if coords.dim() != 2 or coords.shape[1] != 1 + dim:
+        raise ValueError(f"coords must be [N, {1 + dim}] (batch, then {dim} coordinates)")
+    dev = _dev_check(coords)
+    c = _i32(coords)
+    bs = (ctypes.c_int32 * dim)(*[int(x) for x in block_size][:dim])
+    res = (ctypes.c_int32 * dim)(*[int(x) for x in resolution][:dim])
+    bs_p, res_p = ctypes.addressof(bs), ctypes.addressof(res)
+    ws_n = lib().lsrm_block_separation_workspace_size(batch, dim, bs_p, res_p)
+    if ws_n == 0:
+        raise ValueError("unsupported block_size / resolution / batch")
+    nbins = 1
+    for d in range(dim):
+        nbins *= int(resolution[d]) // int(block_size[d])
+    cu_sb = torch.empty(batch + 1, dtype=torch.int32, device=dev)
+    cu_blk = torch.empty(batch * nbins + 1, dtype=torch.int32, device=dev)
+    n_blocks = torch.empty(1, dtype=torch.int32, device=dev)
+    ws = _workspace(ws_n, dev)
+    with torch.cuda.device(dev):
+        _check(lib().lsrm_block_separation(
+            _ptr(c), c.shape[0], dim, bs_p, res_p, batch, _ptr(cu_sb), _ptr(cu_blk),
+            _ptr(n_blocks), _ptr(ws), ws.numel(), _stream(dev)), "lsrm_block_separation")
+    nb = int(n_blocks.item())
+    return cu_sb, cu_blk[:nb + 1]
+
+
+def block_sort_permutation(coords: torch.Tensor, layout: int, block_size: int, dims) -> torch.Tensor:
+    """Sort permutation of sort_volume_blocks (layout 0, dims = (volume_res,))
+    or sort_image_blocks (layout 1, dims = (n_images, patch_res)) -> int64 [N]."""
+    if coords.dim() != 2 or coords.shape[1] != 4:
+        raise ValueError("coords must be [N, 4]")
+    dev = _dev_check(coords)
+    c = _i32(coords)
+    n = c.shape[0]
+    perm = torch.empty(n, dtype=torch.int32, device=dev)
+    if n == 0:
+        return perm.long()
+    dd = (ctypes.c_int64 * len(dims))(*[int(x) for x in dims])
+    ws = _workspace(lib().lsrm_block_sort_workspace_size(n), dev)
+    with torch.cuda.device(dev):
+        _check(lib().lsrm_block_sort(_ptr(c), n, layout, int(block_size), ctypes.addressof(dd),
+                                     _ptr(perm),
+                                     _ptr(ws), ws.numel(), _stream(dev)), "lsrm_block_sort")
+    return perm.long()
