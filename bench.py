@@ -103,6 +103,51 @@ def cpu_baseline(w, q, k, v, topk_idx, flops_per_head_q, budget_s: float):
     }
 
 
+def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
+    """Config-3 paths with per-token selection rows (reported beside the
+    headline, not part of it): the forward over the 3D-aware rows of the
+    voxel tokens (nearest 16 block centroids, built on the GPU), and the
+    learned selection (compressed attention + get_block_score, top-16)."""
+    import sparse.ops as ops
+    from sparse import builders
+
+    dev = q.device
+    n_img = w.n_image_tokens
+    nb_img = w.n_image_blocks
+    nv = w.n - n_img
+    coords = torch.zeros(nv, 4, dtype=torch.int32)
+    coords[:, 1:] = torch.from_numpy(w.voxel_coords)
+    cu_v = (w.cu_block_tokens[nb_img:] - w.cu_block_tokens[nb_img]).to(dev)
+    cu_sb_v = torch.tensor([0, cu_v.numel() - 1], dtype=torch.int32, device=dev)
+    cu_q_v = torch.tensor([0, nv], dtype=torch.int32, device=dev)
+    pts = H.volume_points(coords.to(dev), 64, 1.0)
+    rows = H.nearest_blocks(pts, cu_v, cu_sb_v, cu_q_v, 16, w.hkv)
+    qv, kv, vv = (t[n_img:] for t in (q, k, v))
+    lens = (cu_v[1:] - cu_v[:-1]).long()
+    flops3 = 4.0 * w.d * w.hq * float(lens[rows[0].long().clamp(min=0)].masked_fill(
+        rows[0] < 0, 0).sum())
+    plan3 = H.SelAttnPlan(qv.shape, kv.shape, rows, cu_sb_v, cu_v, cu_q_v)
+    out3 = torch.empty_like(qv)
+    lse3 = torch.empty(w.hq, nv, dtype=torch.float32, device=dev)
+    ms3 = event_time_ms(lambda: plan3.fwd(qv, kv, vv, w.scale, out3, lse3), 5)
+
+    ops.set_validation(False)
+    ck = H.block_mean_pool(k.view(w.n, -1), cu_blk).view(-1, w.hkv, w.d)
+    cv = H.block_mean_pool(v.view(w.n, -1), cu_blk).view(-1, w.hkv, w.d)
+    _, lse = ops.compressed_attention(q, ck, cv, cu_q, cu_sb)
+    ms_ca = event_time_ms(lambda: ops.compressed_attention(q, ck, cv, cu_q, cu_sb), 5)
+    ms_bs = event_time_ms(lambda: ops.get_block_score(q, ck, lse, 16, cu_q, cu_sb, None, None), 5)
+    ops.set_validation(True)
+    return {
+        "attn_fwd_3d_aware_rows": {
+            "ms": round(ms3, 4), "tflops": round(flops3 / (ms3 * 1e-3) / 1e12, 2),
+            "workload": f"{nv} voxel tokens, {cu_v.numel() - 1} blocks, per-token nearest 16 "
+                        f"block centroids, H={w.hq}"},
+        "learned_selection": {"compressed_attn_ms": round(ms_ca, 4),
+                              "get_block_score_ms": round(ms_bs, 4), "topk": 16},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -194,6 +239,7 @@ def main() -> int:
     ms_bwd = event_time_ms(lambda: bplan.bwd(do, q, k, v, out, lse, w.scale),
                            max(2, reps // 4))
     del bplan, do
+    extra = per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q) if args.config == 3 else {}
     nb = w.n_blocks
     pool_bytes = n * hkv * d * 2 + nb * hkv * d * 2 + 4 * (nb + 1)
     attn_tflops = flops / (ms_attn * 1e-3) / 1e12
@@ -232,6 +278,7 @@ def main() -> int:
                          "tflops": round(2.5 * flops / (ms_bwd * 1e-3) / 1e12, 2),
                          "frac_bf16_peak": round(2.5 * flops / (ms_bwd * 1e-3) / 1e12
                                                  / PEAK_BF16_TFLOPS, 4)},
+            **extra,
         },
         "roofline": {
             "bound": "mfma",
