@@ -38,7 +38,9 @@ struct AttnArgs {
   float scale;       // softmax scale
   float scale_log2;  // softmax scale * log2(e)
   TilePlan plan;
-  RevMap rev;        // backward: tile-granular reverse map
+  RevMap rev;        // backward: block -> run tiles that selected it
+  RevMap qrev;       // backward: block -> queries of grouped tiles that
+                     // selected it (one entry per listing, ascending)
   KeyItems items;    // backward: 64-key chunks of every block
 };
 

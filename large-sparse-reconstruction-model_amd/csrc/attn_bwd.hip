@@ -9,22 +9,35 @@
 // LDS rings (swizzled, row-major), S^T = K Q^T and dP^T = V dO^T from
 // row-major reads, dQ^T = K^T dS^T with K^T taken by ds_read_b64_tr_b16.
 //
+// Per-token selection rows (consecutive queries with different rows) come
+// as the plan's grouped tiles: dQ runs them over the union of their blocks
+// with per-row key masks, or run by run.
+//
 // dK/dV follow backward_kernel_dkdv_fastest (same file, 687-923): each
 // workgroup owns one 64-key chunk of one block of one kv head and walks the
-// query tiles that selected the block (tile-granular reverse map, ascending
-// tile order), so every dK/dV element has a single writer and a fixed
-// accumulation order.  The tiles' Q and dO rows are copied into two-slot LDS
+// run tiles that selected the block (tile-granular reverse map, ascending
+// tile order), then the queries of grouped tiles that selected it
+// (query-granular reverse map, ascending, 128 / g queries gathered per
+// step), so every dK/dV element has a single writer and a fixed
+// accumulation order.  The Q and dO rows are copied into two-slot LDS
 // rings; S = Q K^T and dP = dO V^T take the rows directly, dV^T = dO^T P and
 // dK^T = Q^T dS take Q^T / dO^T by transposed reads.  Waves split the chunk
 // 2 (keys) x 2 (rows); the two row halves are added in a fixed order at the
 // end.
+#include <type_traits>
+
 #include "attn.h"
 
 namespace lsrm {
 
 // ------------------------------------------------------------------- dQ --
 
-template <int DT, int D>
+// UNION false: the run tiles of the plan.  UNION true: the grouped tiles,
+// run once over the union of their rows' blocks with per-row key masks, or
+// once per run of identical rows with the other rows' P forced to zero (the
+// passes of the forward's grouped tiles; no softmax state is carried, so
+// either way each row's dQ is a plain sum over the keys it attends).
+template <int DT, int D, bool UNION>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 sel_attn_dq_kernel(AttnArgs a) {
   using G = KvTile<D>;
@@ -33,11 +46,15 @@ sel_attn_dq_kernel(AttnArgs a) {
   __shared__ __align__(1024) char sK[3][G::BYTES];
   __shared__ __align__(1024) char sV[3][G::BYTES];
   __shared__ SelLds sel;
+  __shared__ typename std::conditional<UNION, UnionLds, int>::type ul;
   __shared__ int s_slot;
 
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
-  const int total = a.plan.head_off[a.hkv];
+  const int32_t* head_off = UNION ? a.plan.ghead_off : a.plan.head_off;
+  const int2* tiles = UNION ? a.plan.gtiles : a.plan.tiles;
+  int32_t* queue = a.plan.counter + (UNION ? 4 : 0);
+  const int total = head_off[a.hkv];
 
   int ld_key[G::LPW], ld_byte[G::LPW];
 #pragma unroll
@@ -48,20 +65,40 @@ sel_attn_dq_kernel(AttnArgs a) {
   const uint32_t row_bytes = (uint32_t)a.hkv * D * 2;
 
   for (;;) {
-    const int w = uniform(fetch_work(a.plan.counter, &s_slot));
+    const int w = uniform(fetch_work(queue, &s_slot));
     if (w >= total) break;
-    const int h = head_of(a.plan.head_off, a.hkv, w);
-    const int2 tile = a.plan.tiles[(int64_t)h * a.nq + (w - a.plan.head_off[h])];
-    const int q0 = tile.x, rows = tile.y * a.g;
-    load_selection(a, h, q0, sel);
+    const int h = head_of(head_off, a.hkv, w);
+    const int2 tile = tiles[(int64_t)h * a.nq + (w - head_off[h])];
+    const int q0 = tile.x, qn = tile.y, rows = qn * a.g;
+    // umode 0: a run tile; 1: a grouped tile over the union of its blocks,
+    // rows masked to their own; 2: a grouped tile run by run.
+    int umode = 0, n_pass = 1;
+    if constexpr (UNION) {
+      build_union(a, h, q0, qn, sel, ul);
+      umode = ul.ok ? 1 : 2;
+      n_pass = ul.ok ? 1 : ul.n_runs;
+    } else {
+      load_selection(a, h, q0, sel);
+    }
+    for (int pass = 0; pass < n_pass; ++pass) {
+    int q_lo = 0, q_hi = qn;  // the pass writes the rows of queries [q_lo, q_hi)
+    if constexpr (UNION) {
+      if (umode == 2) {
+        q_lo = ul.run_start[pass];
+        q_hi = ul.run_start[pass + 1];
+        load_selection(a, h, q0 + q_lo, sel);
+      }
+    }
     const int nkeys = sel.cum[sel.n];
     const int ntiles = (nkeys + KT - 1) / KT;
     const int t_safe = sel.n > 0 ? sel.tok[0] : 0;
 
     const int r = wv * 32 + l32;
     const bool row_ok = r < rows;
-    const bool wave_on = wv * 32 < rows;
-    const int64_t qi = q0 + (row_ok ? r / a.g : 0);
+    const int qr = row_ok ? r / a.g : 0;  // the row's query within the tile
+    const bool row_in_pass = row_ok && qr >= q_lo && qr < q_hi;
+    const bool wave_on = wv * 32 < q_hi * a.g && wv * 32 + 32 > q_lo * a.g;
+    const int64_t qi = q0 + qr;
     const int hh = h * a.g + (row_ok ? r % a.g : 0);
     u32x4 qb[NS], dob[NS];
     float dpart = 0.0f;
@@ -85,9 +122,15 @@ sel_attn_dq_kernel(AttnArgs a) {
       }
     }
     const float delta = dpart + __shfl_xor(dpart, 32);
-    // exponent bias -lse (a row outside the tile gets -inf: P = 0)
-    const float bias = row_ok ? -a.lse_in[(int64_t)hh * a.nq + qi] : -__builtin_inf();
-    if (row_ok && hb == 0) a.lse[(int64_t)hh * a.nq + qi] = delta;
+    // Exponent bias -lse.  Rows outside the tile or the pass get -inf (P =
+    // 0), and so does a row that attends nothing (lse = -inf; in a grouped
+    // tile its masked scores would otherwise give -inf + inf).
+    float bias = -__builtin_inf();
+    if (row_in_pass) {
+      const float l = a.lse_in[(int64_t)hh * a.nq + qi];
+      if (l > -__builtin_inf()) bias = -l;
+    }
+    if (row_in_pass && hb == 0) a.lse[(int64_t)hh * a.nq + qi] = delta;
 
     const char* kbase = reinterpret_cast<const char*>(a.k + (int64_t)h * D);
     const char* vbase = reinterpret_cast<const char*>(a.v + (int64_t)h * D);
@@ -139,6 +182,7 @@ sel_attn_dq_kernel(AttnArgs a) {
     for (int i = 0; i < ND; ++i)
 #pragma unroll
       for (int v = 0; v < 16; ++v) dqacc[i][v] = 0.0f;
+    int useg = 0;  // union segment cursor of the key masks
 
     // Prologue: tile 0 resident, tile 1 in flight (a step's copies are
     // consumed two steps later, retired by a counted wait).
@@ -175,7 +219,30 @@ sel_attn_dq_kernel(AttnArgs a) {
           }
         }
         const int kb0 = kt * KT;
-        if (kb0 + KT > nkeys) {
+        if (umode == 1) {
+          if constexpr (UNION) {
+            // Keys of union segments the row's query did not select (and
+            // positions past the stream) score -inf.
+            uint64_t m = 0ull;
+            int sg = useg;
+            while (sel.cum[sg + 1] <= kb0) ++sg;  // stops at the sentinel
+            useg = sg;
+            for (; sg < sel.n && sel.cum[sg] < kb0 + KT; ++sg) {
+              const int lo = sel.cum[sg] > kb0 ? sel.cum[sg] - kb0 : 0;
+              const int hi = sel.cum[sg + 1] - kb0 < KT ? sel.cum[sg + 1] - kb0 : KT;
+              const uint64_t upto = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+              const uint64_t range = upto & ~((1ull << lo) - 1ull);
+              if ((ul.seg_q[sg][qr >> 5] >> (qr & 31)) & 1u) m |= range;
+            }
+            const uint64_t mh = m >> (hb * 4);  // slot v: key (v/4)*8 + hb*4 + v%4
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+              for (int v = 0; v < 16; ++v)
+                if (!((mh >> (blk * 32 + (v / 4) * 8 + (v % 4))) & 1ull))
+                  sacc[blk][v] = -__builtin_inf();
+          }
+        } else if (kb0 + KT > nkeys) {
 #pragma unroll
           for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
@@ -227,7 +294,7 @@ sel_attn_dq_kernel(AttnArgs a) {
       __syncthreads();
     }
 
-    if (row_ok) {
+    if (row_in_pass) {
       uint16_t* drow = a.out + (qi * a.hq + hh) * D;
 #pragma unroll
       for (int db = 0; db < ND; ++db)
@@ -239,9 +306,14 @@ sel_attn_dq_kernel(AttnArgs a) {
                     pack2<DT>(dqacc[db][v + 2], dqacc[db][v + 3])};
         }
     }
+    if (n_pass > 1) {
+      wait_copies();  // this pass's trailing copies land before the next pass
+      __syncthreads();
+    }
+    }  // passes
   }
   wait_copies();  // no copy into LDS outlives the workgroup
-  leave_queue(a.plan.counter, a.plan.counter + 2);
+  leave_queue(queue, queue + 2);
 }
 
 // ----------------------------------------------------------------- dK/dV --
@@ -258,6 +330,7 @@ sel_attn_dkdv_kernel(AttnArgs a) {
   __shared__ __align__(1024) char sO[2][G::BYTES];
   __shared__ __align__(16) float s_lse[2][ROWS];  // lse per row (+inf: none)
   __shared__ __align__(16) float s_dl[2][ROWS];   // delta per row
+  __shared__ int s_qi[2][ROWS];                   // gathered rows' queries
   __shared__ int s_slot;
   float* red = reinterpret_cast<float*>(&sQ[0][0]);
 
@@ -274,6 +347,11 @@ sel_attn_dkdv_kernel(AttnArgs a) {
     ld_byte[j] = (((lane % G::CH) ^ G::swz(ld_row[j])) << 4);
   }
 
+  // The item loop is instantiated twice: with the grouped-query phase, and
+  // without it for plans that have no grouped tiles (its loop then carries
+  // none of that phase's branches or state).
+  auto items_loop = [&](auto qmap) __attribute__((always_inline)) {
+  constexpr bool QM = decltype(qmap)::value != 0;
   for (;;) {
     const int w = uniform(fetch_work(a.plan.counter + 1, &s_slot));
     if (w >= total) break;
@@ -285,6 +363,18 @@ sel_attn_dkdv_kernel(AttnArgs a) {
     if (e1 > a.rev.cap) e1 = a.rev.cap;
     const int n_ent = e1 > e0 ? (int)(e1 - e0) : 0;
     const int32_t* ents = a.rev.rev + (int64_t)h * a.rev.cap + e0;
+    // Then the queries of grouped tiles that selected the block, QC per step.
+    int n_qent = 0;
+    const int32_t* qents = nullptr;
+    if constexpr (QM) {
+      const int64_t f0 = a.qrev.cu_rev[(int64_t)h * (a.nb + 1) + c];
+      int64_t f1 = a.qrev.cu_rev[(int64_t)h * (a.nb + 1) + c + 1];
+      if (f1 > a.qrev.cap) f1 = a.qrev.cap;
+      n_qent = f1 > f0 ? (int)(f1 - f0) : 0;
+      qents = a.qrev.rev + (int64_t)h * a.qrev.cap + f0;
+    }
+    const int QC = ROWS / a.g;
+    const int n_steps = QM ? n_ent + (n_qent + QC - 1) / QC : n_ent;
 
     // This wave's 32 keys as B operands (K^T, V^T columns).
     const int key = kh * 32 + l32;
@@ -309,26 +399,72 @@ sel_attn_dkdv_kernel(AttnArgs a) {
     // Copies of entry e's Q and dO rows into ring slot `slot`, and its lse /
     // delta into registers (stored to LDS by store_stats).
     float lse_r = __builtin_inf(), dl_r = 0.0f;
+    // Step e >= n_ent gathers the rows of queries qents[(e - n_ent) * QC +
+    // r / g]: thread r reads row r's query two steps ahead into nq_r and
+    // publishes it in s_qi[e & 1] (-1 past the list) for the copies.
+    int nq_r = -1;
+    auto fetch_queries = [&](int e) {
+      if (!QM || e < n_ent || e >= n_steps || tid >= ROWS) return;
+      const int i = (e - n_ent) * QC + tid / a.g;
+      nq_r = i < n_qent ? qents[i] : -1;
+    };
+    auto publish_queries = [&](int e) {
+      if (!QM || e < n_ent || e >= n_steps || tid >= ROWS) return;
+      s_qi[e & 1][tid] = nq_r;
+    };
+    // The run tiles of entries tc_base .. tc_base + 63, lane i holding entry
+    // tc_base + i: one load round trip per 64 entries instead of two
+    // dependent ones per step.  Entries are visited in increasing order.
+    int tc_base = -64, tc_x = 0, tc_y = 0;
+    auto tile_of = [&](int e) {
+      if (e - tc_base >= 64) {
+        tc_base = e;
+        int2 t = make_int2(0, 0);
+        if (e + lane < n_ent) t = a.plan.tiles[(int64_t)h * a.nq + ents[e + lane]];
+        tc_x = t.x;
+        tc_y = t.y;
+      }
+      const int sl = e - tc_base;
+      return make_int2(__builtin_amdgcn_readlane(tc_x, sl), __builtin_amdgcn_readlane(tc_y, sl));
+    };
     auto issue = [&](int e, int slot) {
-      const int2 tl = a.plan.tiles[(int64_t)h * a.nq + ents[e]];
-      const int rows = tl.y * a.g;
       const uint32_t dq = lds_addr(sQ[slot]) + wv * G::LPW * 1024;
       const uint32_t dout = lds_addr(sO[slot]) + wv * G::LPW * 1024;
+      int rows;
+      int64_t sqi = -1;  // query of stats row tid (-1: none)
+      if (!QM || e < n_ent) {
+        const int2 tl = tile_of(e);
+        rows = tl.y * a.g;
 #pragma unroll
-      for (int j = 0; j < G::LPW; ++j) {
-        const int rr = ld_row[j] < rows ? ld_row[j] : 0;  // in-bounds filler
-        const uint32_t off =
-            (uint32_t)(((int64_t)(tl.x + rr / a.g) * a.hq + h * a.g + rr % a.g) * D * 2) +
-            ld_byte[j];
-        copy16_to_lds(a.q, off, dq + j * 1024);
-        copy16_to_lds(a.dout, off, dout + j * 1024);
+        for (int j = 0; j < G::LPW; ++j) {
+          const int rr = ld_row[j] < rows ? ld_row[j] : 0;  // in-bounds filler
+          const uint32_t off =
+              (uint32_t)(((int64_t)(tl.x + rr / a.g) * a.hq + h * a.g + rr % a.g) * D * 2) +
+              ld_byte[j];
+          copy16_to_lds(a.q, off, dq + j * 1024);
+          copy16_to_lds(a.dout, off, dout + j * 1024);
+        }
+        if (tid < rows) sqi = tl.x + tid / a.g;
+      } else {
+        const int left = n_qent - (e - n_ent) * QC;
+        rows = (left < QC ? left : QC) * a.g;
+        const int* qi_row = s_qi[e & 1];
+#pragma unroll
+        for (int j = 0; j < G::LPW; ++j) {
+          const int qv = qi_row[ld_row[j]];
+          const int64_t qj = qv >= 0 ? qv : 0;  // query 0: in-bounds filler
+          const uint32_t off =
+              (uint32_t)((qj * a.hq + h * a.g + ld_row[j] % a.g) * D * 2) + ld_byte[j];
+          copy16_to_lds(a.q, off, dq + j * 1024);
+          copy16_to_lds(a.dout, off, dout + j * 1024);
+        }
+        if (tid < rows && qi_row[tid] >= 0) sqi = qi_row[tid];
       }
       if (tid < ROWS) {
-        if (tid < rows) {
-          const int64_t qi = tl.x + tid / a.g;
+        if (sqi >= 0) {
           const int hh = h * a.g + tid % a.g;
-          lse_r = a.lse_in[(int64_t)hh * a.nq + qi];
-          dl_r = a.lse[(int64_t)hh * a.nq + qi];
+          lse_r = a.lse_in[(int64_t)hh * a.nq + sqi];  // consumed by store_stats
+          dl_r = a.lse[(int64_t)hh * a.nq + sqi];
         } else {
           lse_r = __builtin_inf();
           dl_r = 0.0f;
@@ -338,22 +474,33 @@ sel_attn_dkdv_kernel(AttnArgs a) {
     };
     auto store_stats = [&](int slot) {
       if (tid < ROWS) {
-        s_lse[slot][tid] = lse_r;
+        // a row without keys (lse = -inf) gets P = 0
+        s_lse[slot][tid] = lse_r > -__builtin_inf() ? lse_r : __builtin_inf();
         s_dl[slot][tid] = dl_r;
       }
     };
 
     int rows_cur = 0;
-    if (n_ent > 0) {
+    if (n_steps > 0) {
+      if constexpr (QM) {
+        fetch_queries(0);
+        publish_queries(0);
+        fetch_queries(1);
+        publish_queries(1);
+        __syncthreads();
+      }
       rows_cur = issue(0, 0);
       store_stats(0);
     }
     wait_copies();
     __syncthreads();
-    for (int e = 0; e < n_ent; ++e) {
+    for (int e = 0; e < n_steps; ++e) {
       const int slot = e & 1;
       int rows_next = 0;
-      if (e + 1 < n_ent) rows_next = issue(e + 1, slot ^ 1);
+      if (e + 1 < n_steps) {
+        rows_next = issue(e + 1, slot ^ 1);
+        fetch_queries(e + 2);
+      }
       if (rh * 64 < rows_cur && kh * 32 < nk_item) {
         const char* qs = sQ[slot];
         const char* os = sO[slot];
@@ -426,8 +573,9 @@ sel_attn_dkdv_kernel(AttnArgs a) {
             }
         }
       }
-      if (e + 1 < n_ent) store_stats(slot ^ 1);
+      if (e + 1 < n_steps) store_stats(slot ^ 1);
       wait_copies();
+      publish_queries(e + 2);  // s_qi[e & 1] was last read by issue(e)
       __syncthreads();
       rows_cur = rows_next;
     }
@@ -468,16 +616,29 @@ sel_attn_dkdv_kernel(AttnArgs a) {
     }
     __syncthreads();
   }
+  };
+  if (uniform(a.plan.ghead_off[a.hkv]) > 0)
+    items_loop(Phase<1>{});
+  else
+    items_loop(Phase<0>{});
   leave_queue(a.plan.counter + 1, a.plan.counter + 3);
 }
 
 template <int DT, int D>
 int launch_bwd_t(const AttnArgs& a, hipStream_t st) {
   {
-    const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D>);
+    const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D, false>);
     const int grid = persistent_grid(fn, 256, 0);
     if (grid <= 0) return LSRM_ERR_LAUNCH;
-    hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D>), dim3(grid), dim3(256), 0,
+    hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D, false>), dim3(grid), dim3(256), 0,
+                       st, a);
+    LSRM_CHECK_LAUNCH();
+  }
+  if (a.plan.gtiles) {  // the grouped tiles (often none)
+    const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D, true>);
+    const int grid = persistent_grid(fn, 256, 0);
+    if (grid <= 0) return LSRM_ERR_LAUNCH;
+    hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D, true>), dim3(grid), dim3(256), 0,
                        st, a);
     LSRM_CHECK_LAUNCH();
   }

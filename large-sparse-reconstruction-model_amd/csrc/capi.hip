@@ -54,6 +54,7 @@ int persistent_grid(const void* kernel, int block, size_t dyn_lds) {
 struct AttnWs {
   TilePlan plan;
   RevMap rev;
+  RevMap qrev;
   KeyItems items;
 };
 
@@ -65,13 +66,27 @@ int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
               int64_t batch, int g, bool backward, AttnWs& w, hipStream_t st) {
   const int tq = ROWS / g;
   int rc = build_tile_plan(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, tq, ws,
-                           w.plan, st, !backward);
+                           w.plan, st, true);
   if (rc) return rc;
   if (backward) {
+    // dK/dV rows: the run tiles that selected a block, then the queries of
+    // grouped tiles that selected it.
     w.rev = RevMap{};
     w.rev.cap = nq * topk_n;
     rc = build_reverse_map(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, nb, true,
                            &w.plan, ws, w.rev, st);
+    if (rc) return rc;
+    uint8_t* grouped = reinterpret_cast<uint8_t*>(
+        ws.take<int32_t>((size_t)((hkv * nq + 3) / 4 > 0 ? (hkv * nq + 3) / 4 : 1)));
+    if (ws.base && !ws.dry) {
+      if (!ws.ok()) return LSRM_ERR_WORKSPACE;
+      rc = mark_grouped_queries(w.plan, hkv, nq, grouped, st);
+      if (rc) return rc;
+    }
+    w.qrev = RevMap{};
+    w.qrev.cap = nq * topk_n;
+    rc = build_reverse_map(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, nb, false,
+                           nullptr, ws, w.qrev, st, grouped);
     if (rc) return rc;
     rc = build_key_items(cu_blk, nb, nk, ws, w.items, st);
     if (rc) return rc;
@@ -197,6 +212,7 @@ int attn_setup(const void* q, const void* k, const void* v, int dtype,
   a.scale_log2 = softmax_scale * 1.44269504f;  // as the reference (kvcentric:125)
   a.plan = w.plan;
   a.rev = w.rev;
+  a.qrev = w.qrev;
   a.items = w.items;
   return LSRM_OK;
 }

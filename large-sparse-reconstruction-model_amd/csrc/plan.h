@@ -32,20 +32,24 @@ struct RevMap {
 };
 
 // Workspace carving: pass a Carver with base == nullptr to size.
-// group_short: move consecutive short run tiles into grouped tiles (forward
-// plans only; the backward kernels need run tiles).
+// group_short: move consecutive short run tiles into grouped tiles.
 int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
                     int64_t topk_n, const int32_t* cu_q, int64_t batch,
                     const int32_t* cu_sb, int tq, Carver& ws, TilePlan& plan,
                     hipStream_t st, bool group_short = false);
 
 // rows_are_tiles: rows are the tiles of `plan` (row r of head h reads the
-// selection of query tiles[h*nq + r].x); otherwise rows are queries.
+// selection of query tiles[h*nq + r].x); otherwise rows are queries, and
+// with `only` (a [hkv, nq] byte mask) only the queries it marks.
 int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
                       int64_t topk_n, const int32_t* cu_q, int64_t batch,
                       const int32_t* cu_sb, int64_t nb, bool rows_are_tiles,
                       const TilePlan* plan, Carver& ws, RevMap& map,
-                      hipStream_t st);
+                      hipStream_t st, const uint8_t* only = nullptr);
+
+// flags[h, q] = 1 for the queries of the grouped tiles of `plan`, else 0.
+int mark_grouped_queries(const TilePlan& plan, int64_t hkv, int64_t nq,
+                         uint8_t* flags, hipStream_t st);
 
 // Key chunks of at most 64 tokens inside each block (head independent):
 // item i = (block, first token, length) packed in an int4 {c, t0, len, 0}.

@@ -415,16 +415,21 @@ int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
 
 // --------------------------------------------------------- reverse map --
 
-// Row source: row r of head h reads the selection of query `query(h, r)`.
+// Row source: row r of head h reads the selection of query `query(h, r)`;
+// rows that `skip` are not entered.
 struct RowSrc {
   const int2* tiles;      // null: rows are queries
   const int32_t* count;   // rows per head (tiles) or null
   int64_t nq;
+  const uint8_t* only;    // rows are queries: [hkv, nq] mask, or null (all)
   __device__ int64_t n_rows(int h) const {
     return tiles ? (int64_t)count[h] : nq;
   }
   __device__ int64_t query(int h, int64_t r) const {
     return tiles ? (int64_t)tiles[(int64_t)h * nq + r].x : r;
+  }
+  __device__ bool skip(int h, int64_t r) const {
+    return !tiles && only && !only[(int64_t)h * nq + r];
   }
 };
 
@@ -435,7 +440,7 @@ __global__ __launch_bounds__(256) void rev_count_kernel(
     int32_t* __restrict__ counts) {
   const int h = blockIdx.y;
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows.n_rows(h)) return;
+  if (r >= rows.n_rows(h) || rows.skip(h, r)) return;
   const int64_t q = rows.query(h, r);
   int b, bs, nbb;
   bool start;
@@ -456,7 +461,7 @@ __global__ __launch_bounds__(256) void rev_scatter_kernel(
     int32_t* __restrict__ rev, int64_t cap) {
   const int h = blockIdx.y;
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows.n_rows(h)) return;
+  if (r >= rows.n_rows(h) || rows.skip(h, r)) return;
   const int64_t q = rows.query(h, r);
   int b, bs, nbb;
   bool start;
@@ -578,7 +583,7 @@ int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
                       int64_t topk_n, const int32_t* cu_q, int64_t batch,
                       const int32_t* cu_sb, int64_t nb, bool rows_are_tiles,
                       const TilePlan* plan, Carver& ws, RevMap& map,
-                      hipStream_t st) {
+                      hipStream_t st, const uint8_t* only) {
   int32_t* counts = ws.take<int32_t>((size_t)(hkv * (nb > 0 ? nb : 1)));
   int32_t* fill = ws.take<int32_t>((size_t)(hkv * (nb > 0 ? nb : 1)));
   int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, hkv));
@@ -590,7 +595,8 @@ int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
   if (!ws.ok()) return LSRM_ERR_WORKSPACE;
 
   RowSrc rows{rows_are_tiles ? plan->tiles : nullptr,
-              rows_are_tiles ? plan->tile_count : nullptr, nq};
+              rows_are_tiles ? plan->tile_count : nullptr, nq,
+              rows_are_tiles ? nullptr : only};
   int rc = launch_zero_i32(counts, hkv * nb, st);
   if (rc) return rc;
   rc = launch_zero_i32(fill, hkv * nb, st);
@@ -620,6 +626,30 @@ int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
                        map.rev, aux, nb, map.cap, rows);
     LSRM_CHECK_LAUNCH();
   }
+  return LSRM_OK;
+}
+
+__global__ __launch_bounds__(256) void mark_grouped_kernel(const int2* __restrict__ gtiles,
+                                                           const int32_t* __restrict__ gcount,
+                                                           int64_t nq,
+                                                           uint8_t* __restrict__ flags) {
+  const int h = blockIdx.y;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= gcount[h]) return;
+  const int2 g = gtiles[(int64_t)h * nq + t];
+  for (int i = 0; i < g.y; ++i) flags[(int64_t)h * nq + g.x + i] = 1;
+}
+
+int mark_grouped_queries(const TilePlan& plan, int64_t hkv, int64_t nq,
+                         uint8_t* flags, hipStream_t st) {
+  if (nq <= 0) return LSRM_OK;
+  int rc = launch_zero_i32(reinterpret_cast<int32_t*>(flags), (hkv * nq + 3) / 4, st);
+  if (rc) return rc;
+  if (!plan.gtiles) return LSRM_OK;
+  // Grouped tiles hold >= 2 queries, so at most nq / 2 per head.
+  hipLaunchKernelGGL(mark_grouped_kernel, dim3(ceil_div(nq / 2 + 1, 256), (unsigned)hkv),
+                     dim3(256), 0, st, plan.gtiles, plan.gtile_count, nq, flags);
+  LSRM_CHECK_LAUNCH();
   return LSRM_OK;
 }
 

@@ -1,8 +1,10 @@
-"""GPU parity of the forward on per-token selection rows: consecutive
-queries whose rows differ are grouped into tiles that run over the union of
-their blocks with a per-query mask, or run by run (duplicated ids, unions too
-large or more expensive than the runs).  Checked against the fp32 oracle at
-the attention tolerance, including the LSE."""
+"""GPU parity of the forward and backward on per-token selection rows:
+consecutive queries whose rows differ are grouped into tiles that run over
+the union of their blocks with a per-query mask, or run by run (duplicated
+ids, unions too large or more expensive than the runs); dK/dV gather the
+queries of grouped tiles per block.  Checked against the fp32 oracle
+(autograd for the gradients) at the attention tolerance, including the
+LSE."""
 
 import numpy as np
 import pytest
@@ -38,18 +40,32 @@ def _voxel_case(n=16384, hq=2, hkv=2, topk=16, seed=0):
     return q, k, v, topk_idx, cu_sb, torch.from_numpy(cu_v), cu_q
 
 
-def _check(q, k, v, topk_idx, cu_sb, cu_blk, cu_q):
+def _check(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, do=None):
     scale = 1.0 / 8.0
-    o, lse = H.sel_attn_fwd(*(t.to(DEV) for t in (q, k, v, topk_idx, cu_sb, cu_blk, cu_q)),
-                            scale)
-    o_ref, lse_ref = sel_attn_ref(q.float(), k.float(), v.float(), topk_idx, cu_sb, cu_blk,
-                                  cu_q, scale)
+    dev_args = [t.to(DEV) for t in (q, k, v, topk_idx, cu_sb, cu_blk, cu_q)]
+    o, lse = H.sel_attn_fwd(*dev_args, scale)
+    qf, kf, vf = (t.float().requires_grad_(do is not None) for t in (q, k, v))
+    o_ref, lse_ref = sel_attn_ref(qf, kf, vf, topk_idx, cu_sb, cu_blk, cu_q, scale)
     assert_attn_close(o, o_ref, "out")
     lse_c = lse.cpu()
     fin = torch.isfinite(lse_ref)
     assert torch.equal(torch.isfinite(lse_c), fin)
     if fin.any():
         assert float((lse_c[fin] - lse_ref[fin]).abs().max()) <= 2e-2
+    if do is None:
+        return
+    dq, dk, dv, delta = H.sel_attn_bwd(do.to(DEV), *dev_args[:3], o, lse, *dev_args[3:], scale)
+    o_ref.backward(do.float())
+    assert_attn_close(dq, qf.grad, "dq")
+    assert_attn_close(dk, kf.grad, "dk")
+    assert_attn_close(dv, vf.grad, "dv")
+    delta_ref = (o.float().cpu() * do.float()).sum(-1).transpose(0, 1)
+    torch.testing.assert_close(delta.cpu(), delta_ref, rtol=1e-4, atol=1e-4)
+
+
+def _grad_out(q, seed):
+    g = torch.Generator().manual_seed(100 + seed)
+    return (0.5 * torch.randn(q.shape, generator=g)).to(q.dtype)
 
 
 def test_3d_aware_rows_union_tiles():
@@ -96,3 +112,68 @@ def test_two_batch_elements_short_runs():
     rows2 = torch.cat([topk_idx, topk_idx], dim=1)
     _check(q2, k2, v2, rows2, cu_sb2, cu_blk2, cu_q2)
     assert half > 0
+
+
+# ------------------------------------------------------------- backward --
+
+def test_bwd_3d_aware_rows_union_tiles():
+    q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _voxel_case(n=8192, topk=8, seed=5)
+    _check(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, do=_grad_out(q, 5))
+
+
+def test_bwd_3d_aware_rows_gqa():
+    q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _voxel_case(n=4096, hq=8, hkv=2, topk=4, seed=6)
+    _check(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, do=_grad_out(q, 6))
+
+
+def test_bwd_duplicate_ids_and_empty_rows():
+    # Repeated ids (run passes in dQ, repeated entries for dK/dV) and rows
+    # that attend nothing inside grouped tiles (dQ = 0 for them).
+    q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _voxel_case(n=4096, topk=4, seed=7)
+    topk_idx = topk_idx.clone()
+    topk_idx[:, ::3, 3] = topk_idx[:, ::3, 0]
+    topk_idx[:, 5::13, :] = -1
+    _check(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, do=_grad_out(q, 7))
+
+
+def test_bwd_run_tiles_and_grouped_queries_share_blocks():
+    # The first half of the queries share their block's row (long runs: run
+    # tiles), the second half have per-token rows (grouped tiles), so dK/dV
+    # of most blocks take rows from both reverse maps.
+    q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _voxel_case(n=8192, topk=6, seed=8)
+    topk_idx = topk_idx.clone()
+    nv = q.shape[0]
+    cu = cu_blk.tolist()
+    for b in range(len(cu) - 1):
+        s, e = cu[b], cu[b + 1]
+        if e <= nv // 2:
+            topk_idx[:, s:e] = topk_idx[:, s:s + 1]
+    _check(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, do=_grad_out(q, 8))
+
+
+def test_bwd_random_rows_two_batches():
+    w = W.config(2, n=3000, heads=2)
+    q, k, v = W.tensors(w, "cpu")
+    g = torch.Generator().manual_seed(9)
+    nb = w.n_blocks
+    topk_idx = torch.randint(0, nb, (w.hkv, w.n, 6), generator=g, dtype=torch.int32)
+    topk_idx[:, ::5, 4:] = -1
+    topk_idx[:, 1::7, 2] = nb + 5
+    # two batch elements over the same blocks and tokens
+    q2, k2, v2 = torch.cat([q, q]), torch.cat([k, k]), torch.cat([v, v])
+    cu_blk2 = torch.cat([w.cu_block_tokens, w.cu_block_tokens[1:] + w.n])
+    cu_sb2 = torch.tensor([0, nb, 2 * nb], dtype=torch.int32)
+    cu_q2 = torch.tensor([0, w.n, 2 * w.n], dtype=torch.int32)
+    rows2 = torch.cat([topk_idx, topk_idx.flip(1)], dim=1).contiguous()
+    _check(q2, k2, v2, rows2, cu_sb2, cu_blk2, cu_q2, do=_grad_out(q2, 9))
+
+
+def test_bwd_per_token_rows_deterministic():
+    q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _voxel_case(n=16384, topk=16, seed=10)
+    do = _grad_out(q, 10).to(DEV)
+    args = [t.to(DEV) for t in (q, k, v, topk_idx, cu_sb, cu_blk, cu_q)]
+    o, lse = H.sel_attn_fwd(*args, 0.125)
+    first = H.sel_attn_bwd(do, *args[:3], o, lse, *args[3:], 0.125)
+    again = H.sel_attn_bwd(do, *args[:3], o, lse, *args[3:], 0.125)
+    for x, y in zip(first, again):
+        assert torch.equal(x, y)
