@@ -130,6 +130,11 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
     out3 = torch.empty_like(qv)
     lse3 = torch.empty(w.hq, nv, dtype=torch.float32, device=dev)
     ms3 = event_time_ms(lambda: plan3.fwd(qv, kv, vv, w.scale, out3, lse3), 5)
+    bplan3 = H.SelAttnPlan(qv.shape, kv.shape, rows, cu_sb_v, cu_v, cu_q_v, backward=True)
+    do3 = torch.randn(qv.shape, generator=torch.Generator(device=dev).manual_seed(7),
+                      device=dev).to(qv.dtype)
+    ms3b = event_time_ms(lambda: bplan3.bwd(do3, qv, kv, vv, out3, lse3, w.scale), 3)
+    del bplan3
 
     ops.set_validation(False)
     ck = H.block_mean_pool(k.view(w.n, -1), cu_blk).view(-1, w.hkv, w.d)
@@ -143,6 +148,8 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
             "ms": round(ms3, 4), "tflops": round(flops3 / (ms3 * 1e-3) / 1e12, 2),
             "workload": f"{nv} voxel tokens, {cu_v.numel() - 1} blocks, per-token nearest 16 "
                         f"block centroids, H={w.hq}"},
+        "attn_bwd_3d_aware_rows": {
+            "ms": round(ms3b, 4), "tflops": round(2.5 * flops3 / (ms3b * 1e-3) / 1e12, 2)},
         "learned_selection": {"compressed_attn_ms": round(ms_ca, 4),
                               "get_block_score_ms": round(ms_bs, 4), "topk": 16},
     }

@@ -41,7 +41,7 @@ struct AttnArgs {
   RevMap rev;        // backward: block -> run tiles that selected it
   RevMap qrev;       // backward: block -> queries of grouped tiles that
                      // selected it (one entry per listing, ascending)
-  KeyItems items;    // backward: 64-key chunks of every block
+  KeyItems items;    // backward: key chunks of every block
 };
 
 // Compile-time value tag (e.g. a ring-slot phase).
@@ -367,6 +367,53 @@ __device__ inline void leave_queue(int32_t* work, int32_t* exits) {
     __threadfence();
     if (atomicAdd(exits, 1) == (int)(gridDim.x * gridDim.y * gridDim.z) - 1) {
       atomicExch(work, 0);
+      atomicExch(exits, 0);
+    }
+  }
+}
+
+// XCD (accelerator complex die) executing this wave: 0..7 on MI355X.  Each
+// XCD has its own L2, so work that shares inputs should run on one XCD.
+__device__ inline int xcd_id() {
+  unsigned x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(x));
+  return (int)(x & 7u);
+}
+
+constexpr int NXCD = 8;
+
+// XCD-affine work queue over items 0 .. total-1: the items come in segments
+// of `seg` consecutive indices, segment j belonging to XCD j % 8, and
+// counter cnt[x] hands out XCD x's items in increasing order.  A workgroup
+// drains the queue of its own XCD first, then those of the others
+// (`tries` counts the queues it found empty; thread 0 keeps it).  Returns
+// the item (or total once every queue is drained), broadcast through LDS.
+__device__ inline int fetch_work_xcd(int32_t* cnt, int seg, int total, int home,
+                                     int& tries, int* s_slot) {
+  if (threadIdx.x == 0) {
+    int w = total;
+    while (tries < NXCD) {
+      const int x = (home + tries) % NXCD;
+      const int k = atomicAdd(&cnt[x], 1);
+      const int ww = (k / seg) * (NXCD * seg) + x * seg + (k % seg);
+      if (ww < total) {
+        w = ww;
+        break;
+      }
+      ++tries;  // this queue's items only increase with k: it is drained
+    }
+    *s_slot = w;
+  }
+  __syncthreads();
+  return *s_slot;
+}
+
+// leave_queue for the NXCD counters of fetch_work_xcd.
+__device__ inline void leave_queue_xcd(int32_t* cnt, int32_t* exits) {
+  if (threadIdx.x == 0) {
+    __threadfence();
+    if (atomicAdd(exits, 1) == (int)(gridDim.x * gridDim.y * gridDim.z) - 1) {
+      for (int x = 0; x < NXCD; ++x) atomicExch(&cnt[x], 0);
       atomicExch(exits, 0);
     }
   }

@@ -14,16 +14,16 @@
 // with per-row key masks, or run by run.
 //
 // dK/dV follow backward_kernel_dkdv_fastest (same file, 687-923): each
-// workgroup owns one 64-key chunk of one block of one kv head and walks the
+// workgroup owns one key chunk of one block of one kv head and walks the
 // run tiles that selected the block (tile-granular reverse map, ascending
 // tile order), then the queries of grouped tiles that selected it
 // (query-granular reverse map, ascending, 128 / g queries gathered per
 // step), so every dK/dV element has a single writer and a fixed
 // accumulation order.  The Q and dO rows are copied into two-slot LDS
 // rings; S = Q K^T and dP = dO V^T take the rows directly, dV^T = dO^T P and
-// dK^T = Q^T dS take Q^T / dO^T by transposed reads.  Waves split the chunk
-// 2 (keys) x 2 (rows); the two row halves are added in a fixed order at the
-// end.
+// dK^T = Q^T dS take Q^T / dO^T by transposed reads.  Chunks hold up to 128
+// keys: each wave owns 32 of them and runs every step's 128 rows as two
+// 64-row halves, so one copy of a step's Q / dO rows feeds 128 keys.
 #include <type_traits>
 
 #include "attn.h"
@@ -324,36 +324,46 @@ sel_attn_dkdv_kernel(AttnArgs a) {
   using G = KvTile<D, ROWS>;  // 128-row Q / dO tiles
   constexpr int NS = D / 16;
   constexpr int ND = D / 32;
-  constexpr int RED_FLOATS = 2 * 2 * ND * 16 * 64;  // (key half, dk|dv) x acc
-  static_assert(RED_FLOATS * 4 <= 2 * G::BYTES, "reduction area");
   __shared__ __align__(1024) char sQ[2][G::BYTES];
   __shared__ __align__(1024) char sO[2][G::BYTES];
   __shared__ __align__(16) float s_lse[2][ROWS];  // lse per row (+inf: none)
   __shared__ __align__(16) float s_dl[2][ROWS];   // delta per row
   __shared__ int s_qi[2][ROWS];                   // gathered rows' queries
   __shared__ int s_slot;
-  float* red = reinterpret_cast<float*>(&sQ[0][0]);
 
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
-  const int kh = wv & 1, rh = wv >> 1;  // key half, row half of this wave
+  static_assert(KEY_CHUNK == 4 * 32, "four waves of 32 keys cover a chunk");
+  const int kh = wv;  // this wave's 32 keys of the chunk; it covers all rows
   const int n_items = a.items.n_items[0];
   const int total = n_items * a.hkv;
 
   int ld_row[G::LPW], ld_byte[G::LPW];
+  // Row r of a step <-> (query r / g of the step, query head r % g): the
+  // quotients of this lane's copy rows and of stats row tid, computed once.
+  int ld_q[G::LPW], ld_hh[G::LPW];
 #pragma unroll
   for (int j = 0; j < G::LPW; ++j) {
     ld_row[j] = (wv * G::LPW + j) * G::KPL + lane / G::CH;
     ld_byte[j] = (((lane % G::CH) ^ G::swz(ld_row[j])) << 4);
+    ld_q[j] = ld_row[j] / a.g;
+    ld_hh[j] = ld_row[j] - ld_q[j] * a.g;
   }
+  const int st_q = tid / a.g, st_hh = tid - st_q * a.g;
 
   // The item loop is instantiated twice: with the grouped-query phase, and
   // without it for plans that have no grouped tiles (its loop then carries
   // none of that phase's branches or state).
+  // Items (64-key chunks, block-major within a head) are handed out in
+  // segments of 64 per XCD, so the chunks of one block, which read the same
+  // Q / dO tiles in the same order, run side by side on one XCD and share
+  // its L2.
+  const int home = xcd_id();
+  int tries = 0;
   auto items_loop = [&](auto qmap) __attribute__((always_inline)) {
   constexpr bool QM = decltype(qmap)::value != 0;
   for (;;) {
-    const int w = uniform(fetch_work(a.plan.counter + 1, &s_slot));
+    const int w = uniform(fetch_work_xcd(a.plan.counter + 8, 64, total, home, tries, &s_slot));
     if (w >= total) break;
     const int h = w / n_items;
     const int4 item = a.items.items[w - h * n_items];
@@ -403,12 +413,12 @@ sel_attn_dkdv_kernel(AttnArgs a) {
     // r / g]: thread r reads row r's query two steps ahead into nq_r and
     // publishes it in s_qi[e & 1] (-1 past the list) for the copies.
     int nq_r = -1;
-    auto fetch_queries = [&](int e) {
+    auto fetch_queries = [&](int e) __attribute__((always_inline)) {
       if (!QM || e < n_ent || e >= n_steps || tid >= ROWS) return;
-      const int i = (e - n_ent) * QC + tid / a.g;
+      const int i = (e - n_ent) * QC + st_q;
       nq_r = i < n_qent ? qents[i] : -1;
     };
-    auto publish_queries = [&](int e) {
+    auto publish_queries = [&](int e) __attribute__((always_inline)) {
       if (!QM || e < n_ent || e >= n_steps || tid >= ROWS) return;
       s_qi[e & 1][tid] = nq_r;
     };
@@ -416,7 +426,7 @@ sel_attn_dkdv_kernel(AttnArgs a) {
     // tc_base + i: one load round trip per 64 entries instead of two
     // dependent ones per step.  Entries are visited in increasing order.
     int tc_base = -64, tc_x = 0, tc_y = 0;
-    auto tile_of = [&](int e) {
+    auto tile_of = [&](int e) __attribute__((always_inline)) {
       if (e - tc_base >= 64) {
         tc_base = e;
         int2 t = make_int2(0, 0);
@@ -427,9 +437,13 @@ sel_attn_dkdv_kernel(AttnArgs a) {
       const int sl = e - tc_base;
       return make_int2(__builtin_amdgcn_readlane(tc_x, sl), __builtin_amdgcn_readlane(tc_y, sl));
     };
-    auto issue = [&](int e, int slot) {
-      const uint32_t dq = lds_addr(sQ[slot]) + wv * G::LPW * 1024;
-      const uint32_t dout = lds_addr(sO[slot]) + wv * G::LPW * 1024;
+    // prepare(e, slot): the rows of step e (byte offsets of this lane's Q /
+    // dO pieces, which both tensors share) and its lse / delta loads;
+    // copy_part(c) then issues copy c of the 2 * LPW (Q, dO alternating).
+    uint32_t cp_off[G::LPW], cp_dq = 0, cp_do = 0;
+    auto prepare = [&](int e, int slot) __attribute__((always_inline)) {
+      cp_dq = lds_addr(sQ[slot]) + wv * G::LPW * 1024;
+      cp_do = lds_addr(sO[slot]) + wv * G::LPW * 1024;
       int rows;
       int64_t sqi = -1;  // query of stats row tid (-1: none)
       if (!QM || e < n_ent) {
@@ -437,14 +451,13 @@ sel_attn_dkdv_kernel(AttnArgs a) {
         rows = tl.y * a.g;
 #pragma unroll
         for (int j = 0; j < G::LPW; ++j) {
-          const int rr = ld_row[j] < rows ? ld_row[j] : 0;  // in-bounds filler
-          const uint32_t off =
-              (uint32_t)(((int64_t)(tl.x + rr / a.g) * a.hq + h * a.g + rr % a.g) * D * 2) +
-              ld_byte[j];
-          copy16_to_lds(a.q, off, dq + j * 1024);
-          copy16_to_lds(a.dout, off, dout + j * 1024);
+          const bool in = ld_row[j] < rows;  // else an in-bounds filler (row 0)
+          cp_off[j] = (uint32_t)(((int64_t)(tl.x + (in ? ld_q[j] : 0)) * a.hq + h * a.g +
+                                  (in ? ld_hh[j] : 0)) *
+                                 D * 2) +
+                      ld_byte[j];
         }
-        if (tid < rows) sqi = tl.x + tid / a.g;
+        if (tid < rows) sqi = tl.x + st_q;
       } else {
         const int left = n_qent - (e - n_ent) * QC;
         rows = (left < QC ? left : QC) * a.g;
@@ -453,16 +466,13 @@ sel_attn_dkdv_kernel(AttnArgs a) {
         for (int j = 0; j < G::LPW; ++j) {
           const int qv = qi_row[ld_row[j]];
           const int64_t qj = qv >= 0 ? qv : 0;  // query 0: in-bounds filler
-          const uint32_t off =
-              (uint32_t)((qj * a.hq + h * a.g + ld_row[j] % a.g) * D * 2) + ld_byte[j];
-          copy16_to_lds(a.q, off, dq + j * 1024);
-          copy16_to_lds(a.dout, off, dout + j * 1024);
+          cp_off[j] = (uint32_t)((qj * a.hq + h * a.g + ld_hh[j]) * D * 2) + ld_byte[j];
         }
         if (tid < rows && qi_row[tid] >= 0) sqi = qi_row[tid];
       }
       if (tid < ROWS) {
         if (sqi >= 0) {
-          const int hh = h * a.g + tid % a.g;
+          const int hh = h * a.g + st_hh;
           lse_r = a.lse_in[(int64_t)hh * a.nq + sqi];  // consumed by store_stats
           dl_r = a.lse[(int64_t)hh * a.nq + sqi];
         } else {
@@ -472,7 +482,20 @@ sel_attn_dkdv_kernel(AttnArgs a) {
       }
       return rows;
     };
-    auto store_stats = [&](int slot) {
+    auto copy_part = [&](int c) __attribute__((always_inline)) {
+      const int j = c >> 1;
+      if (c & 1)
+        copy16_to_lds(a.dout, cp_off[j], cp_do + j * 1024);
+      else
+        copy16_to_lds(a.q, cp_off[j], cp_dq + j * 1024);
+    };
+    auto issue = [&](int e, int slot) __attribute__((always_inline)) {
+      const int rows = prepare(e, slot);
+#pragma unroll
+      for (int c = 0; c < 2 * G::LPW; ++c) copy_part(c);
+      return rows;
+    };
+    auto store_stats = [&](int slot) __attribute__((always_inline)) {
       if (tid < ROWS) {
         // a row without keys (lse = -inf) gets P = 0
         s_lse[slot][tid] = lse_r > -__builtin_inf() ? lse_r : __builtin_inf();
@@ -497,81 +520,215 @@ sel_attn_dkdv_kernel(AttnArgs a) {
     for (int e = 0; e < n_steps; ++e) {
       const int slot = e & 1;
       int rows_next = 0;
-      if (e + 1 < n_steps) {
-        rows_next = issue(e + 1, slot ^ 1);
+      const bool has_next = e + 1 < n_steps;
+      if (has_next) {
+        rows_next = prepare(e + 1, slot ^ 1);
         fetch_queries(e + 2);
       }
-      if (rh * 64 < rows_cur && kh * 32 < nk_item) {
-        const char* qs = sQ[slot];
-        const char* os = sO[slot];
-        u32x4 pb[2][2], dsb[2][2];
+      const bool computes = kh * 32 < nk_item;
+      if (has_next) {
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-          const int rbase = rh * 64 + rb * 32;
-          f32x16 sacc, dpacc;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) sacc[v] = dpacc[v] = 0.0f;
-#pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const int o = G::off(rbase + l32, 2 * s + hb);
-            sacc = mfma32<DT>(*reinterpret_cast<const u32x4*>(qs + o), kb[s], sacc);
-            dpacc = mfma32<DT>(*reinterpret_cast<const u32x4*>(os + o), vb[s], dpacc);
-          }
-          float p[16], ds[16];
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            // registers 4*g4 .. 4*g4+3 hold rows rbase + g4*8 + hb*4 + 0..3
-            const f32x4 lv = *reinterpret_cast<const f32x4*>(
-                &s_lse[slot][rbase + g4 * 8 + hb * 4]);
-            const f32x4 dv = *reinterpret_cast<const f32x4*>(
-                &s_dl[slot][rbase + g4 * 8 + hb * 4]);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const int v = g4 * 4 + u;
-              p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], a.scale_log2, -lv[u]));
-              ds[v] = a.scale * p[v] * (dpacc[v] - dv[u]);
+        for (int c = 0; c < 2 * G::LPW; ++c) copy_part(c);
+      }
+      if constexpr (D > 64) {
+        // Head dim 128: one block of copies, then the matrix work row block
+        // by row block (the slot schedule below does not fit its registers).
+        if (computes) {
+#pragma unroll 1
+          for (int rh = 0; rh < 2 && rh * 64 < rows_cur; ++rh) {  // row halves
+          const char* qs = sQ[slot];
+          const char* os = sO[slot];
+          u32x4 pb[2][2], dsb[2][2];
+  #pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            const int rbase = rh * 64 + rb * 32;
+            f32x16 sacc, dpacc;
+  #pragma unroll
+            for (int v = 0; v < 16; ++v) sacc[v] = dpacc[v] = 0.0f;
+  #pragma unroll
+            for (int s = 0; s < NS; ++s) {
+              const int o = G::off(rbase + l32, 2 * s + hb);
+              sacc = mfma32<DT>(*reinterpret_cast<const u32x4*>(qs + o), kb[s], sacc);
+              dpacc = mfma32<DT>(*reinterpret_cast<const u32x4*>(os + o), vb[s], dpacc);
+            }
+            float p[16], ds[16];
+  #pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              // registers 4*g4 .. 4*g4+3 hold rows rbase + g4*8 + hb*4 + 0..3
+              const f32x4 lv = *reinterpret_cast<const f32x4*>(
+                  &s_lse[slot][rbase + g4 * 8 + hb * 4]);
+              const f32x4 dv = *reinterpret_cast<const f32x4*>(
+                  &s_dl[slot][rbase + g4 * 8 + hb * 4]);
+  #pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                const int v = g4 * 4 + u;
+                p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], a.scale_log2, -lv[u]));
+                ds[v] = p[v] * (dpacc[v] - dv[u]);
+              }
+            }
+  #pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+              pb[rb][cc] = u32x4{pack2<DT>(p[cc * 8 + 0], p[cc * 8 + 1]),
+                                 pack2<DT>(p[cc * 8 + 2], p[cc * 8 + 3]),
+                                 pack2<DT>(p[cc * 8 + 4], p[cc * 8 + 5]),
+                                 pack2<DT>(p[cc * 8 + 6], p[cc * 8 + 7])};
+              dsb[rb][cc] = u32x4{pack2<DT>(ds[cc * 8 + 0], ds[cc * 8 + 1]),
+                                  pack2<DT>(ds[cc * 8 + 2], ds[cc * 8 + 3]),
+                                  pack2<DT>(ds[cc * 8 + 4], ds[cc * 8 + 5]),
+                                  pack2<DT>(ds[cc * 8 + 6], ds[cc * 8 + 7])};
             }
           }
-#pragma unroll
-          for (int cc = 0; cc < 2; ++cc) {
-            pb[rb][cc] = u32x4{pack2<DT>(p[cc * 8 + 0], p[cc * 8 + 1]),
-                               pack2<DT>(p[cc * 8 + 2], p[cc * 8 + 3]),
-                               pack2<DT>(p[cc * 8 + 4], p[cc * 8 + 5]),
-                               pack2<DT>(p[cc * 8 + 6], p[cc * 8 + 7])};
-            dsb[rb][cc] = u32x4{pack2<DT>(ds[cc * 8 + 0], ds[cc * 8 + 1]),
-                                pack2<DT>(ds[cc * 8 + 2], ds[cc * 8 + 3]),
-                                pack2<DT>(ds[cc * 8 + 4], ds[cc * 8 + 5]),
-                                pack2<DT>(ds[cc * 8 + 6], ds[cc * 8 + 7])};
+          // dV^T += dO^T P and dK^T += Q^T dS: the transposed operands come
+          // from the row-major tiles (slot e of lane (hb, row d) = query row
+          // rh*64 + rb*32 + cc*16 + (e/4)*8 + hb*4 + e%4, the P / dS layout).
+          const int gi = lane & 15, dh = (lane >> 4) & 1;
+  #pragma unroll
+          for (int db = 0; db < ND; ++db) {
+            const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+            const int cb = dcol >> 3, half = (dcol & 4) * 2;
+  #pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+  #pragma unroll
+              for (int cc = 0; cc < 2; ++cc) {
+                const int r0 = rh * 64 + rb * 32 + cc * 16 + hb * 4 + (gi >> 2);
+                const int o0 = G::off(r0, cb) + half, o1 = G::off(r0 + 8, cb) + half;
+                const u32x2 olo = __builtin_bit_cast(
+                    u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(os + o0)));
+                const u32x2 ohi = __builtin_bit_cast(
+                    u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(os + o1)));
+                dvacc[db] = mfma32<DT>(u32x4{olo[0], olo[1], ohi[0], ohi[1]},
+                                       pb[rb][cc], dvacc[db]);
+                const u32x2 qlo = __builtin_bit_cast(
+                    u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(qs + o0)));
+                const u32x2 qhi = __builtin_bit_cast(
+                    u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(qs + o1)));
+                dkacc[db] = mfma32<DT>(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]},
+                                       dsb[rb][cc], dkacc[db]);
+              }
           }
+          }  // row halves
         }
-        // dV^T += dO^T P and dK^T += Q^T dS: the transposed operands come
-        // from the row-major tiles (slot e of lane (hb, row d) = query row
-        // rh*64 + rb*32 + cc*16 + (e/4)*8 + hb*4 + e%4, the P / dS layout).
+      } else if (computes) {
+#pragma unroll 1
+        for (int rh = 0; rh < 2 && rh * 64 < rows_cur; ++rh) {  // row halves
+        const char* qs = sQ[slot];
+        const char* os = sO[slot];
+        // The step's 8 * NS MFMAs in a fixed issue order, in four phases:
+        //   A  S, dP of row block 0          (2 * NS)
+        //   B  S, dP of row block 1          (2 * NS)   + P, dS of row block 0
+        //   C  dV, dK of row block 0         (4 * ND)   + P, dS of row block 1
+        //   D  dV, dK of row block 1         (4 * ND)
+        // so that the vector work of one row block runs while the matrix
+        // core works on the other.  Each slot issues the LDS reads of the
+        // MFMA LA slots ahead, then its MFMA, then its share of the vector
+        // work; scheduling barriers keep the compiler from regrouping the
+        // slots.
+        // dS is kept unscaled (dK is scaled once at the end).
+        constexpr int NA = 2 * NS, NC = 4 * ND, NSLOT = 2 * NA + 2 * NC, LA = 2;
         const int gi = lane & 15, dh = (lane >> 4) & 1;
+        f32x16 sc[2], dp[2];
+        u32x4 pb[2][2], dsb[2][2];
+        f32x4 lv[2][4], dl[2][4];
+        u32x4 opnd[LA + 1];
+        // Operand of MFMA i (row-major Q / dO rows for S, dP; transposed
+        // dO / Q columns for dV, dK: slot e of lane (hb, row d) = query row
+        // rh*64 + rb*32 + cc*16 + (e/4)*8 + hb*4 + e%4, the P / dS layout).
+        auto read_op = [&](int i) __attribute__((always_inline)) {
+          if (i < 2 * NA) {
+            const int rb = i / NA, j = i % NA, sk = j >> 1;
+            const char* src = (j & 1) ? os : qs;
+            opnd[i % (LA + 1)] = *reinterpret_cast<const u32x4*>(
+                src + G::off(rh * 64 + rb * 32 + l32, 2 * sk + hb));
+          } else {
+            const int j = (i - 2 * NA) % NC, rb = (i - 2 * NA) / NC;
+            const int db = j >> 2, cc = (j >> 1) & 1;
+            const char* src = (j & 1) ? qs : os;
+            const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+            const int cb = dcol >> 3, half = (dcol & 4) * 2;
+            const int r0 = rh * 64 + rb * 32 + cc * 16 + hb * 4 + (gi >> 2);
+            const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(src + G::off(r0, cb) + half)));
+            const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(src + G::off(r0 + 8, cb) + half)));
+            opnd[i % (LA + 1)] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          }
+        };
+        // lse / delta of score registers 4*g4 .. 4*g4+3 of row block rb
+        // (rows rh*64 + rb*32 + g4*8 + hb*4 + 0..3)
+        auto read_stats = [&](int rb, int g4) __attribute__((always_inline)) {
+          const int r = rh * 64 + rb * 32 + g4 * 8 + hb * 4;
+          lv[rb][g4] = *reinterpret_cast<const f32x4*>(&s_lse[slot][r]);
+          dl[rb][g4] = *reinterpret_cast<const f32x4*>(&s_dl[slot][r]);
+        };
+        // Slot of softmax pair k of row block rb (pairs spread evenly over
+        // phase B for block 0, phase C for block 1); the stats of a group of
+        // two pairs are read three slots before its first pair.
+        auto pair_slot = [](int rb, int k) constexpr {
+          return rb == 0 ? NA + ((k + 1) * NA + 7) / 8 - 1
+                         : 2 * NA + ((k + 1) * NC + 7) / 8 - 1;
+        };
+        // P and dS of elements 2k, 2k+1 of row block rb, packed.
+        auto softmax_pair = [&](int rb, int k) __attribute__((always_inline)) {
+          const int v0 = 2 * k, g4 = v0 >> 2, u = v0 & 3;
+          const float p0 = __builtin_amdgcn_exp2f(
+              __builtin_fmaf(sc[rb][v0], a.scale_log2, -lv[rb][g4][u]));
+          const float p1 = __builtin_amdgcn_exp2f(
+              __builtin_fmaf(sc[rb][v0 + 1], a.scale_log2, -lv[rb][g4][u + 1]));
+          const float d0 = p0 * (dp[rb][v0] - dl[rb][g4][u]);
+          const float d1 = p1 * (dp[rb][v0 + 1] - dl[rb][g4][u + 1]);
+          pb[rb][k >> 2][k & 3] = pack2<DT>(p0, p1);
+          dsb[rb][k >> 2][k & 3] = pack2<DT>(d0, d1);
+        };
 #pragma unroll
-        for (int db = 0; db < ND; ++db) {
-          const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
-          const int cb = dcol >> 3, half = (dcol & 4) * 2;
+        for (int i = 0; i < LA; ++i) read_op(i);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NSLOT; ++i) {
+          if (i + LA < NSLOT) read_op(i + LA);
 #pragma unroll
           for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-              const int r0 = rh * 64 + rb * 32 + cc * 16 + hb * 4 + (gi >> 2);
-              const int o0 = G::off(r0, cb) + half, o1 = G::off(r0 + 8, cb) + half;
-              const u32x2 olo = __builtin_bit_cast(
-                  u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(os + o0)));
-              const u32x2 ohi = __builtin_bit_cast(
-                  u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(os + o1)));
-              dvacc[db] = mfma32<DT>(u32x4{olo[0], olo[1], ohi[0], ohi[1]},
-                                     pb[rb][cc], dvacc[db]);
-              const u32x2 qlo = __builtin_bit_cast(
-                  u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(qs + o0)));
-              const u32x2 qhi = __builtin_bit_cast(
-                  u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(qs + o1)));
-              dkacc[db] = mfma32<DT>(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]},
-                                     dsb[rb][cc], dkacc[db]);
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const int at = pair_slot(rb, 2 * g4) - 3;
+              if (i == (at > 0 ? at : 0)) read_stats(rb, g4);
             }
+          const u32x4 op = opnd[i % (LA + 1)];
+          if (i < 2 * NA) {
+            const int rb = i / NA, j = i % NA, sk = j >> 1;
+            if (j & 1) {
+              if (sk == 0) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) dp[rb][v] = 0.0f;
+              }
+              dp[rb] = mfma32<DT>(op, vb[sk], dp[rb]);
+            } else {
+              if (sk == 0) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) sc[rb][v] = 0.0f;
+              }
+              sc[rb] = mfma32<DT>(op, kb[sk], sc[rb]);
+            }
+          } else {
+            const int j = (i - 2 * NA) % NC, rb = (i - 2 * NA) / NC;
+            const int db = j >> 2, cc = (j >> 1) & 1;
+            if (j & 1)
+              dkacc[db] = mfma32<DT>(op, dsb[rb][cc], dkacc[db]);
+            else
+              dvacc[db] = mfma32<DT>(op, pb[rb][cc], dvacc[db]);
+          }
+          // vector work: row block 0 during phase B, row block 1 during C
+          if (i >= NA && i < 2 * NA) {
+            const int t = i - NA;
+#pragma unroll
+            for (int k = (t * 8) / NA; k < ((t + 1) * 8) / NA; ++k) softmax_pair(0, k);
+          } else if (i >= 2 * NA && i < 2 * NA + NC) {
+            const int t = i - 2 * NA;
+#pragma unroll
+            for (int k = (t * 8) / NC; k < ((t + 1) * 8) / NC; ++k) softmax_pair(1, k);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
+        }  // row halves
       }
       if (e + 1 < n_steps) store_stats(slot ^ 1);
       wait_copies();
@@ -579,22 +736,9 @@ sel_attn_dkdv_kernel(AttnArgs a) {
       __syncthreads();
       rows_cur = rows_next;
     }
-    // Row-half reduction in a fixed order: rows 0-63 + rows 64-127.  The
-    // reduction area aliases the Q ring (no copies are in flight here).
-    __syncthreads();
-    if (rh == 1) {
-      float* dst = red + kh * (2 * ND * 16 * 64);
-#pragma unroll
-      for (int db = 0; db < ND; ++db)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          dst[((0 * ND + db) * 16 + v) * 64 + lane] = dkacc[db][v];
-          dst[((1 * ND + db) * 16 + v) * 64 + lane] = dvacc[db][v];
-        }
-    }
-    __syncthreads();
-    if (rh == 0 && key_ok) {
-      const float* src = red + kh * (2 * ND * 16 * 64);
+    // Each wave owns its keys: dK (scaled by the softmax scale, dS was kept
+    // unscaled) and dV straight from the accumulators.
+    if (key_ok) {
       const int64_t base = ((int64_t)(t0 + key) * a.hkv + h) * D;
 #pragma unroll
       for (int db = 0; db < ND; ++db)
@@ -603,9 +747,8 @@ sel_attn_dkdv_kernel(AttnArgs a) {
           float kv[4], vv[4];
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            const int v = gi * 4 + u;
-            kv[u] = dkacc[db][v] + src[((0 * ND + db) * 16 + v) * 64 + lane];
-            vv[u] = dvacc[db][v] + src[((1 * ND + db) * 16 + v) * 64 + lane];
+            kv[u] = a.scale * dkacc[db][gi * 4 + u];
+            vv[u] = dvacc[db][gi * 4 + u];
           }
           const int d = db * 32 + gi * 8 + hb * 4;
           *reinterpret_cast<u32x2*>(a.dk + base + d) =
@@ -621,7 +764,7 @@ sel_attn_dkdv_kernel(AttnArgs a) {
     items_loop(Phase<1>{});
   else
     items_loop(Phase<0>{});
-  leave_queue(a.plan.counter + 1, a.plan.counter + 3);
+  leave_queue_xcd(a.plan.counter + 8, a.plan.counter + 3);
 }
 
 template <int DT, int D>

@@ -16,8 +16,8 @@ struct TilePlan {
   int32_t* tile_count;   // [hkv]
   int32_t* head_off;     // [hkv + 1] exclusive prefix of tile_count
   int32_t* counter;      // work counters, zeroed by the plan: [0], [2] run
-                         // tiles (fwd / dq), [1], [3] key chunks (dK/dV),
-                         // [4], [6] grouped tiles
+                         // tiles (fwd / dq), [8..15], [3] key chunks (dK/dV,
+                         // one queue per XCD), [4], [6] grouped tiles
   int2* gtiles;          // [hkv, n_q] grouped tiles (forward plans)
   int32_t* gtile_count;  // [hkv]
   int32_t* ghead_off;    // [hkv + 1]
@@ -51,10 +51,12 @@ int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
 int mark_grouped_queries(const TilePlan& plan, int64_t hkv, int64_t nq,
                          uint8_t* flags, hipStream_t st);
 
-// Key chunks of at most 64 tokens inside each block (head independent):
-// item i = (block, first token, length) packed in an int4 {c, t0, len, 0}.
+// Key chunks of at most KEY_CHUNK tokens inside each block (head
+// independent): item i = (block, first token, length) packed in an int4
+// {c, t0, len, 0}.
+constexpr int KEY_CHUNK = 128;
 struct KeyItems {
-  int4* items;        // [n_blocks + n_k / 64 + 1]
+  int4* items;        // [n_blocks + n_k / KEY_CHUNK + 2]
   int32_t* n_items;   // device scalar
 };
 int build_key_items(const int32_t* cu_blk, int64_t nb, int64_t nk, Carver& ws,

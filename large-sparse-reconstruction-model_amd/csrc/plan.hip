@@ -339,7 +339,7 @@ __global__ void plan_offsets_kernel(const int32_t* n_groups, int32_t* tile_count
       head_off[h + 1] = acc;
       ghead_off[h + 1] = gacc;
     }
-    for (int i = 0; i < 8; ++i) counter[i] = 0;
+    for (int i = 0; i < 16; ++i) counter[i] = 0;
   }
 }
 
@@ -663,7 +663,7 @@ struct KeyChunksF {
     int64_t s = cu[c], e = cu[c + 1];
     s = s < 0 ? 0 : (s > nk ? nk : s);
     e = e < 0 ? 0 : (e > nk ? nk : e);
-    return e > s ? (int)((e - s + 63) / 64) : 0;
+    return e > s ? (int)((e - s + KEY_CHUNK - 1) / KEY_CHUNK) : 0;
   }
 };
 struct KeyChunksW {
@@ -676,8 +676,8 @@ struct KeyChunksW {
     s = s < 0 ? 0 : (s > nk ? nk : s);
     e = e < 0 ? 0 : (e > nk ? nk : e);
     for (int t = 0; t < v && ex + t < cap; ++t) {
-      const int64_t t0 = s + 64 * t;
-      const int64_t len = e - t0 < 64 ? e - t0 : 64;
+      const int64_t t0 = s + (int64_t)KEY_CHUNK * t;
+      const int64_t len = e - t0 < KEY_CHUNK ? e - t0 : KEY_CHUNK;
       items[ex + t] = make_int4((int)c, (int)t0, (int)len, 0);
     }
   }
@@ -685,7 +685,7 @@ struct KeyChunksW {
 
 int build_key_items(const int32_t* cu_blk, int64_t nb, int64_t nk, Carver& ws,
                     KeyItems& ki, hipStream_t st) {
-  const int64_t cap = nb + nk / 64 + 2;
+  const int64_t cap = nb + nk / KEY_CHUNK + 2;
   ki.items = ws.take<int4>((size_t)cap);
   ki.n_items = ws.take<int32_t>(64);
   int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, 1));
