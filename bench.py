@@ -143,6 +143,16 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
     ms_ca = event_time_ms(lambda: ops.compressed_attention(q, ck, cv, cu_q, cu_sb), 5)
     ms_bs = event_time_ms(lambda: ops.get_block_score(q, ck, lse, 16, cu_q, cu_sb, None, None), 5)
     ops.set_validation(True)
+
+    # gated merge of the three branch outputs at the layer shape (streams
+    # gate [N, 3*hidden] and three [N, hidden] inputs, writes [N, hidden])
+    hid = w.hq * w.d
+    gen = torch.Generator(device=dev).manual_seed(11)
+    gate = torch.rand(w.n, 3 * hid, generator=gen, device=dev).to(q.dtype)
+    brs = [torch.randn(w.n, hid, generator=gen, device=dev).to(q.dtype) for _ in range(3)]
+    ms_gm = event_time_ms(lambda: ops.gate_merge(gate, *brs), 10)
+    gm_bytes = 7 * w.n * hid * q.element_size()
+    del gate, brs
     return {
         "attn_fwd_3d_aware_rows": {
             "ms": round(ms3, 4), "tflops": round(flops3 / (ms3 * 1e-3) / 1e12, 2),
@@ -152,6 +162,9 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
             "ms": round(ms3b, 4), "tflops": round(2.5 * flops3 / (ms3b * 1e-3) / 1e12, 2)},
         "learned_selection": {"compressed_attn_ms": round(ms_ca, 4),
                               "get_block_score_ms": round(ms_bs, 4), "topk": 16},
+        "gate_merge": {"ms": round(ms_gm, 4), "bytes": gm_bytes,
+                       "gbs": round(gm_bytes / (ms_gm * 1e-3) / 1e9, 1),
+                       "frac_hbm_peak": round(gm_bytes / (ms_gm * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
     }
 
 

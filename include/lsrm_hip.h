@@ -32,6 +32,8 @@
  *   lsrm_nearest_blocks       misc/sparse_utils.py:1219-1273 (the 3D-aware
  *                             per-token selection of build_volume_to_volume_attn)
  *   lsrm_block_separation     misc/sparse_utils.py:592-641 (compute_block_separation)
+ *   lsrm_gate_merge(_bwd)     sparse/module/spatial_sparse_attention.py:256-269
+ *                             (the gated sum of the attention branches)
  *   lsrm_block_sort           misc/sparse_utils.py:95-152 (sort_image_blocks,
  *                             sort_volume_blocks: the sort permutation)
  */
@@ -341,6 +343,27 @@ size_t lsrm_block_sort_workspace_size(int64_t n_tokens);
 int lsrm_block_sort(const int32_t* coords, int64_t n_tokens, int layout, int64_t block_size,
                     const int64_t* dims, int32_t* perm, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Gated merge of the attention branches
+ * (sparse/module/spatial_sparse_attention.py:256-269):
+ *   out = g[:, 0:H] * o_cmp + g[:, H:2H] * o_slc (+ g[:, 2H:3H] * o_win)
+ *   gate [n_tokens, 2H or 3H], o_* / out [n_tokens, H], one dtype
+ *   (LSRM_BF16, LSRM_F16 or LSRM_F32), row-major contiguous; o_win NULL for
+ *   the two-branch form.  Each product and sum is rounded to the dtype in
+ *   the expression's left-to-right order, as PyTorch evaluates it.
+ *   n_tokens * 3 * hidden must stay below 2^32 (LSRM_ERR_UNSUPPORTED).
+ * lsrm_gate_merge_bwd: autograd of the same expression, d_o_x = dout * g_x
+ *   and d_g_x = dout * o_x rounded to the dtype; d_gate has gate's shape;
+ *   d_win must be NULL exactly when o_win is.
+ * ---------------------------------------------------------------------- */
+int lsrm_gate_merge(const void* gate, const void* o_cmp, const void* o_slc,
+                    const void* o_win, int dtype, int64_t n_tokens, int64_t hidden,
+                    void* out, void* stream);
+int lsrm_gate_merge_bwd(const void* dout, const void* gate, const void* o_cmp,
+                        const void* o_slc, const void* o_win, int dtype, int64_t n_tokens,
+                        int64_t hidden, void* d_gate, void* d_cmp, void* d_slc, void* d_win,
+                        void* stream);
 
 #ifdef __cplusplus
 }

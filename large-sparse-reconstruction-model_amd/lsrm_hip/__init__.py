@@ -87,6 +87,8 @@ _SIGNATURES = {
     "lsrm_block_separation": (_I, [_P, _I64, _I, _P, _P, _I64, _P, _P, _P, _P, _SZ, _P]),
     "lsrm_block_sort_workspace_size": (_SZ, [_I64]),
     "lsrm_block_sort": (_I, [_P, _I64, _I, _I64, _P, _P, _P, _SZ, _P]),
+    "lsrm_gate_merge": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _P, _P]),
+    "lsrm_gate_merge_bwd": (_I, [_P, _P, _P, _P, _P, _I, _I64, _I64, _P, _P, _P, _P, _P]),
 }
 
 
@@ -541,3 +543,58 @@ def block_sort_permutation(coords: torch.Tensor, layout: int, block_size: int, d
                                      _ptr(perm),
                                      _ptr(ws), ws.numel(), _stream(dev)), "lsrm_block_sort")
     return perm.long()
+
+
+def _gate_args(gate, branches):
+    """Shared checks of gate_merge / gate_merge_bwd: one dtype and device,
+    gate [N, k*H] for k branches [N, H]."""
+    for t in branches:
+        if t.dim() != 2 or t.shape != branches[0].shape:
+            raise ValueError("branch outputs must all be [n_tokens, hidden]")
+    n, hid = branches[0].shape
+    if gate.dim() != 2 or gate.shape[0] != n or gate.shape[1] != len(branches) * hid:
+        raise ValueError(f"gate must be [n_tokens, {len(branches)} * hidden]")
+    if any(t.dtype != gate.dtype for t in branches) or gate.dtype not in _DTYPE_CODE:
+        raise TypeError("gate and branch outputs must share one of bf16 / fp16 / fp32")
+    _dev_check(gate, *branches)
+    return n, hid
+
+
+def gate_merge(gate: torch.Tensor, o_cmp: torch.Tensor, o_slc: torch.Tensor,
+               o_win: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """gate[:, :H] * o_cmp + gate[:, H:2H] * o_slc (+ gate[:, 2H:] * o_win),
+    each op rounded to the dtype as PyTorch evaluates the expression."""
+    branches = [o_cmp, o_slc] + ([o_win] if o_win is not None else [])
+    gate = gate.contiguous()
+    branches = [b.contiguous() for b in branches]
+    n, hid = _gate_args(gate, branches)
+    out = torch.empty_like(branches[0])
+    dev = gate.device
+    with torch.cuda.device(dev):
+        _check(lib().lsrm_gate_merge(
+            _ptr(gate), _ptr(branches[0]), _ptr(branches[1]),
+            _ptr(branches[2]) if o_win is not None else None, _DTYPE_CODE[gate.dtype], n, hid,
+            _ptr(out), _stream(dev)), "lsrm_gate_merge")
+    return out
+
+
+def gate_merge_bwd(dout: torch.Tensor, gate: torch.Tensor, o_cmp: torch.Tensor,
+                   o_slc: torch.Tensor, o_win: Optional[torch.Tensor] = None):
+    """Gradients of gate_merge: (d_gate, d_cmp, d_slc, d_win or None)."""
+    branches = [o_cmp, o_slc] + ([o_win] if o_win is not None else [])
+    gate = gate.contiguous()
+    branches = [b.contiguous() for b in branches]
+    dout = dout.contiguous()
+    n, hid = _gate_args(gate, branches)
+    if dout.shape != branches[0].shape or dout.dtype != gate.dtype:
+        raise ValueError("dout must match the branch outputs")
+    d_gate = torch.empty_like(gate)
+    d_br = [torch.empty_like(b) for b in branches]
+    dev = gate.device
+    with torch.cuda.device(dev):
+        _check(lib().lsrm_gate_merge_bwd(
+            _ptr(dout), _ptr(gate), _ptr(branches[0]), _ptr(branches[1]),
+            _ptr(branches[2]) if o_win is not None else None, _DTYPE_CODE[gate.dtype], n, hid,
+            _ptr(d_gate), _ptr(d_br[0]), _ptr(d_br[1]),
+            _ptr(d_br[2]) if o_win is not None else None, _stream(dev)), "lsrm_gate_merge_bwd")
+    return d_gate, d_br[0], d_br[1], (d_br[2] if o_win is not None else None)

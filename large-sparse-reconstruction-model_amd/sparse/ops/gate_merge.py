@@ -1,0 +1,45 @@
+"""Gated merge of the sparse-attention branches.
+
+Replaces the expression of sparse/module/spatial_sparse_attention.py:256-269
+(SpatialSparseAttentionOut.forward):
+
+    gate = self.gate(x)
+    attn_output = gate[:, 0:H] * compressed + gate[:, H:2H] * selection
+                  (+ gate[:, 2H:] * window)
+
+with one streaming HIP kernel each way (lsrm_gate_merge / _bwd) instead of
+five or eight PyTorch elementwise kernels and their intermediates.  Results
+are bit-identical to PyTorch's evaluation of the expression in the tensors'
+dtype (every product and sum rounded to the dtype, left to right).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+import lsrm_hip as _hip
+
+
+class GateMerge(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gate, o_cmp, o_slc, o_win):
+        ctx.save_for_backward(gate, o_cmp, o_slc, o_win)
+        ctx.has_win = o_win is not None
+        return _hip.gate_merge(gate, o_cmp, o_slc, o_win)
+
+    @staticmethod
+    def backward(ctx, dout):
+        gate, o_cmp, o_slc, o_win = ctx.saved_tensors
+        d_gate, d_cmp, d_slc, d_win = _hip.gate_merge_bwd(
+            dout, gate, o_cmp, o_slc, o_win if ctx.has_win else None)
+        return d_gate, d_cmp, d_slc, d_win
+
+
+def gate_merge(gate: torch.Tensor, compressed_attn_output: torch.Tensor,
+               selection_attn_output: torch.Tensor,
+               window_attn_output: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """gate [N, 2H or 3H], branch outputs [N, H] -> [N, H] (differentiable)."""
+    return GateMerge.apply(gate, compressed_attn_output, selection_attn_output,
+                           window_attn_output)

@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def _voxel_case(n=16384, hq=2, hkv=2, topk=16, seed=0):
+def _voxel_case(n=16384, hq=2, hkv=2, topk=16, seed=0, d=64):
     """cfg3-style voxel tokens (Morton-ordered cells of a 64^3 grid cut into
     runs of 32..512) with the 3D-aware per-token rows (nearest centroids)."""
     w = W.config(3, n=n, heads=hkv)
@@ -32,9 +32,9 @@ def _voxel_case(n=16384, hq=2, hkv=2, topk=16, seed=0):
     sel = nearest_blocks_ref(pts, cu_v, np.array([0, len(cu_v) - 1]), np.array([0, nv]), topk)
     topk_idx = torch.from_numpy(np.broadcast_to(sel, (hkv, nv, topk)).copy())
     g = torch.Generator().manual_seed(seed)
-    q = (0.5 * torch.randn(nv, hq, 64, generator=g)).to(torch.bfloat16)
-    k = (0.5 * torch.randn(nv, hkv, 64, generator=g)).to(torch.bfloat16)
-    v = (0.5 * torch.randn(nv, hkv, 64, generator=g)).to(torch.bfloat16)
+    q = (0.5 * torch.randn(nv, hq, d, generator=g)).to(torch.bfloat16)
+    k = (0.5 * torch.randn(nv, hkv, d, generator=g)).to(torch.bfloat16)
+    v = (0.5 * torch.randn(nv, hkv, d, generator=g)).to(torch.bfloat16)
     cu_sb = torch.tensor([0, len(cu_v) - 1], dtype=torch.int32)
     cu_q = torch.tensor([0, nv], dtype=torch.int32)
     return q, k, v, topk_idx, cu_sb, torch.from_numpy(cu_v), cu_q
@@ -177,3 +177,11 @@ def test_bwd_per_token_rows_deterministic():
     again = H.sel_attn_bwd(do, *args[:3], o, lse, *args[3:], 0.125)
     for x, y in zip(first, again):
         assert torch.equal(x, y)
+
+
+def test_gqa16_d32_per_token_rows_fwd_bwd():
+    # 16 query heads per kv head at head dim 32 (the product's grouped
+    # layout): 8 queries per tile, grouped tiles of at most 7 queries.
+    q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _voxel_case(n=4096, hq=32, hkv=2, topk=4, seed=11,
+                                                         d=32)
+    _check(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, do=_grad_out(q, 11))
