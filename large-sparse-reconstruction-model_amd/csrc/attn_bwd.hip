@@ -201,7 +201,129 @@ sel_attn_dq_kernel(AttnArgs a) {
       const int s0 = kt % 3, s2 = (kt + 2) % 3;
       advance();
       load_tiles(s2);
+      if constexpr (D <= 64) {
       if (wave_on) {
+        const char* ks = sK[s0];
+        const char* vs = sV[s0];
+        const int kb0 = kt * KT;
+        // Keys of this tile the row attends (bit p = stream position kb0 + p):
+        // union segments its query selected (umode 1), else the stream tail.
+        uint64_t m = ~0ull;
+        if (umode == 1) {
+          if constexpr (UNION) {
+            m = 0ull;
+            int sg = useg;
+            while (sel.cum[sg + 1] <= kb0) ++sg;  // stops at the sentinel
+            useg = sg;
+            for (; sg < sel.n && sel.cum[sg] < kb0 + KT; ++sg) {
+              const int lo = sel.cum[sg] > kb0 ? sel.cum[sg] - kb0 : 0;
+              const int hi = sel.cum[sg + 1] - kb0 < KT ? sel.cum[sg + 1] - kb0 : KT;
+              const uint64_t upto = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+              const uint64_t range = upto & ~((1ull << lo) - 1ull);
+              if ((ul.seg_q[sg][qr >> 5] >> (qr & 31)) & 1u) m |= range;
+            }
+          }
+        } else if (kb0 + KT > nkeys) {
+          const int hi = nkeys - kb0;
+          m = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+        }
+        const bool masked = uniform(umode == 1 || kb0 + KT > nkeys);
+        const uint64_t mh = m >> (hb * 4);  // slot v: key (v/4)*8 + hb*4 + v%4
+        // The step's MFMAs in a fixed issue order, in four phases:
+        //   A  S^T, dP^T of key block 0     (2 * NS)
+        //   B  S^T, dP^T of key block 1     (2 * NS)   + dS of key block 0
+        //   C  dQ^T += K^T dS^T, block 0    (2 * ND)   + dS of key block 1
+        //   D  dQ^T += K^T dS^T, block 1    (2 * ND)
+        // Each slot issues the LDS reads of the MFMA LA slots ahead, its
+        // MFMA, then its share of the vector work; scheduling barriers keep
+        // the order.  dS is kept unscaled (dQ is scaled once at the end).
+        constexpr int NA = 2 * NS, NC = 2 * ND, NSLOT = 2 * NA + 2 * NC, LA = 2;
+        const int gi = lane & 15, dh = (lane >> 4) & 1;
+        f32x16 sc[2], dp[2];
+        u32x4 dsb[2][2];
+        u32x4 opnd[LA + 1];
+        // Operand of MFMA i: K / V rows (S^T, dP^T), or K^T by transposed
+        // reads (slot e of lane (hb, row d) = key blk*32 + c*16 + (e/4)*8 +
+        // hb*4 + e%4, the score layout).
+        auto read_op = [&](int i) __attribute__((always_inline)) {
+          if (i < 2 * NA) {
+            const int blk = i / NA, j = i % NA, sk = j >> 1;
+            const char* src = (j & 1) ? vs : ks;
+            opnd[i % (LA + 1)] =
+                *reinterpret_cast<const u32x4*>(src + G::off(blk * 32 + l32, 2 * sk + hb));
+          } else {
+            const int j = (i - 2 * NA) % NC, blk = (i - 2 * NA) / NC;
+            const int db = j >> 1, c = j & 1;
+            const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+            const int cb = dcol >> 3, half = (dcol & 4) * 2;
+            const int k0 = blk * 32 + c * 16 + hb * 4 + (gi >> 2);
+            const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(ks + G::off(k0, cb) + half)));
+            const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(ks + G::off(k0 + 8, cb) + half)));
+            opnd[i % (LA + 1)] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          }
+        };
+        auto apply_mask = [&](int blk) __attribute__((always_inline)) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            if (!((mh >> (blk * 32 + (v / 4) * 8 + (v % 4))) & 1ull))
+              sc[blk][v] = -__builtin_inf();
+        };
+        // dS of score registers 2k, 2k+1 of key block blk, packed.
+        auto ds_pair = [&](int blk, int k) __attribute__((always_inline)) {
+          const int v0 = 2 * k;
+          const float p0 =
+              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0], a.scale_log2, bias));
+          const float p1 =
+              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0 + 1], a.scale_log2, bias));
+          dsb[blk][k >> 2][k & 3] =
+              pack2<DT>(p0 * (dp[blk][v0] - delta), p1 * (dp[blk][v0 + 1] - delta));
+        };
+#pragma unroll
+        for (int i = 0; i < LA; ++i) read_op(i);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NSLOT; ++i) {
+          if (i + LA < NSLOT) read_op(i + LA);
+          const u32x4 op = opnd[i % (LA + 1)];
+          if (i < 2 * NA) {
+            const int blk = i / NA, j = i % NA, sk = j >> 1;
+            if (j & 1) {
+              if (sk == 0) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) dp[blk][v] = 0.0f;
+              }
+              dp[blk] = mfma32<DT>(op, dob[sk], dp[blk]);
+            } else {
+              if (sk == 0) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) sc[blk][v] = 0.0f;
+              }
+              sc[blk] = mfma32<DT>(op, qb[sk], sc[blk]);
+            }
+          } else {
+            const int j = (i - 2 * NA) % NC, blk = (i - 2 * NA) / NC;
+            const int db = j >> 1, c = j & 1;
+            dqacc[db] = mfma32<DT>(op, dsb[blk][c], dqacc[db]);
+          }
+          // vector work: key block 0 during phase B, key block 1 during C
+          if (i == NA && masked) apply_mask(0);
+          if (i == 2 * NA && masked) apply_mask(1);
+          if (i >= NA && i < 2 * NA) {
+            const int t = i - NA;
+#pragma unroll
+            for (int k = (t * 8) / NA; k < ((t + 1) * 8) / NA; ++k) ds_pair(0, k);
+          } else if (i >= 2 * NA && i < 2 * NA + NC) {
+            const int t = i - 2 * NA;
+#pragma unroll
+            for (int k = (t * 8) / NC; k < ((t + 1) * 8) / NC; ++k) ds_pair(1, k);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      } else {
+      if (D > 64 && wave_on) {
         const char* ks = sK[s0];
         const char* vs = sV[s0];
         f32x16 sacc[2], dpacc[2];
@@ -256,8 +378,7 @@ sel_attn_dq_kernel(AttnArgs a) {
           float ds[16];
 #pragma unroll
           for (int v = 0; v < 16; ++v)
-            ds[v] = a.scale *
-                    __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[blk][v], a.scale_log2, bias)) *
+            ds[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[blk][v], a.scale_log2, bias)) *
                     (dpacc[blk][v] - delta);
 #pragma unroll
           for (int c = 0; c < 2; ++c)
@@ -290,6 +411,7 @@ sel_attn_dq_kernel(AttnArgs a) {
             }
         }
       }
+      }
       wait_prev_copies<2 * G::LPW>();
       __syncthreads();
     }
@@ -301,9 +423,10 @@ sel_attn_dq_kernel(AttnArgs a) {
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
           const int v = gi * 4;
+          // dS was kept unscaled: dQ = scale * (dS' K)
           *reinterpret_cast<u32x2*>(drow + db * 32 + gi * 8 + hb * 4) =
-              u32x2{pack2<DT>(dqacc[db][v], dqacc[db][v + 1]),
-                    pack2<DT>(dqacc[db][v + 2], dqacc[db][v + 3])};
+              u32x2{pack2<DT>(a.scale * dqacc[db][v], a.scale * dqacc[db][v + 1]),
+                    pack2<DT>(a.scale * dqacc[db][v + 2], a.scale * dqacc[db][v + 3])};
         }
     }
     if (n_pass > 1) {
