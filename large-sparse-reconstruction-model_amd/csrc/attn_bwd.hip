@@ -227,7 +227,13 @@ sel_attn_dq_kernel(AttnArgs a) {
           const int hi = nkeys - kb0;
           m = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
         }
-        const bool masked = uniform(umode == 1 || kb0 + KT > nkeys);
+        // A row attends all of a 64-key tile or none of it except at block
+        // edges and the stream tail: a row with no key here gets the bias
+        // -inf (P = 0); scores are masked one by one only when some row of
+        // the wave attends part of the tile.
+        const bool masked =
+            uniform(__builtin_amdgcn_ballot_w64(m != 0ull && m != ~0ull) != 0 ? 1 : 0) != 0;
+        const float bias_t = m == 0ull ? -__builtin_inf() : bias;
         const uint64_t mh = m >> (hb * 4);  // slot v: key (v/4)*8 + hb*4 + v%4
         // The step's MFMAs in a fixed issue order, in four phases:
         //   A  S^T, dP^T of key block 0     (2 * NS)
@@ -274,9 +280,9 @@ sel_attn_dq_kernel(AttnArgs a) {
         auto ds_pair = [&](int blk, int k) __attribute__((always_inline)) {
           const int v0 = 2 * k;
           const float p0 =
-              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0], a.scale_log2, bias));
+              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0], a.scale_log2, bias_t));
           const float p1 =
-              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0 + 1], a.scale_log2, bias));
+              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0 + 1], a.scale_log2, bias_t));
           dsb[blk][k >> 2][k & 3] =
               pack2<DT>(p0 * (dp[blk][v0] - delta), p1 * (dp[blk][v0 + 1] - delta));
         };

@@ -66,9 +66,9 @@ __device__ inline float row_max(const f32x16* sc) {
 }
 
 // UNION false: the run tiles of the plan (every row of a tile shares one
-// key stream).  UNION true: the grouped tiles (see build_union), run with the
-// exact online-maximum pass and per-row key masks; a separate instantiation
-// so that the run-tile kernel carries none of that code or state.
+// key stream).  UNION true: the grouped tiles (see build_union), run with
+// per-row key masks; a separate instantiation so that the run-tile kernel
+// carries none of that code or state.
 template <int DT, int D, bool UNION>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 sel_attn_fwd_kernel(AttnArgs a) {
@@ -113,7 +113,8 @@ sel_attn_fwd_kernel(AttnArgs a) {
     // (a run tile); umode 1 -- a grouped tile run once over the union of
     // its rows' blocks, each row masked to the blocks it selected; umode 2
     // -- a grouped tile run once per run of identical rows, the other rows
-    // masked off.  Modes 1 and 2 use the exact online-maximum pass.
+    // masked off.  All modes take the fast pass first (modes 1 and 2 with
+    // their key masks), falling back to the exact online-maximum pass.
     int umode = 0, n_pass = 1;
     if constexpr (UNION) {
       build_union(a, h, q0, qn, sel, ul);
@@ -189,6 +190,7 @@ sel_attn_fwd_kernel(AttnArgs a) {
     // Online softmax state of this lane's row: the reference m_run (log2
     // units) and the partial row sum.
     float m_run = 0.0f, l_run = 0.0f;
+    uint64_t km = ~0ull;  // grouped tiles: keys of the current tile the row attends
 
     auto scores = [&](const char* ks, f32x16* sacc) __attribute__((always_inline)) {
 #pragma unroll
@@ -219,11 +221,11 @@ sel_attn_fwd_kernel(AttnArgs a) {
     // query selected (segments are walked with a cursor, `useg`); umode 2:
     // all or nothing by run membership.
     int useg = 0;
-    auto mask_keys = [&](int kt, f32x16* sc) __attribute__((always_inline)) {
-      uint64_t m = 0ull;
-      if constexpr (!UNION) {
-        return;
-      } else if (umode == 1) {
+    auto key_mask = [&](int kt) __attribute__((always_inline)) {
+      uint64_t m = ~0ull;
+      if constexpr (UNION) {
+      if (umode == 1) {
+        m = 0ull;
         const int p0 = kt * KT;
         int sg = useg;
         while (sel.cum[sg + 1] <= p0) ++sg;  // stops at the sentinel
@@ -242,12 +244,19 @@ sel_attn_fwd_kernel(AttnArgs a) {
           m &= hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
         }
       }
+      }
+      return m;
+    };
+    auto apply_mask = [&](uint64_t m, f32x16* sc) __attribute__((always_inline)) {
       const uint64_t mh = m >> (hb * 4);  // position of slot v: (v/4)*8 + hb*4 + v%4
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
         for (int v = 0; v < 16; ++v)
           if (!((mh >> (blk * 32 + (v / 4) * 8 + (v % 4))) & 1ull)) sc[blk][v] = -__builtin_inf();
+    };
+    auto mask_keys = [&](int kt, f32x16* sc) __attribute__((always_inline)) {
+      if constexpr (UNION) apply_mask(key_mask(kt), sc);
     };
 
     // Softmax of one score tile against m_run: P packed to the 16-bit type
@@ -305,10 +314,10 @@ sel_attn_fwd_kernel(AttnArgs a) {
     };
     // One softmax pair (scores 2j, 2j+1 of a lane's 32) against m_run: two
     // exponentials packed to the 16-bit type and added to the row sum.
-    auto softmax_pair = [&](const f32x16* sc, u32x4 (*pb)[2], int j) __attribute__((always_inline)) {
+    auto softmax_pair = [&](const f32x16* sc, u32x4 (*pb)[2], int j, float negm) __attribute__((always_inline)) {
       const int blk = j >> 3, c = (j >> 2) & 1, e = j & 3, v0 = c * 8 + 2 * e;
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0], a.scale_log2, -m_run));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0 + 1], a.scale_log2, -m_run));
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0], a.scale_log2, negm));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0 + 1], a.scale_log2, negm));
       pb[blk][c][e] = pack2<DT>(p0, p1);
       l_run = sum2<DT>(pb[blk][c][e], l_run);
     };
@@ -321,7 +330,8 @@ sel_attn_fwd_kernel(AttnArgs a) {
     // MFMA i are read during score slot i.  Scheduling barriers keep the
     // compiler from regrouping the slots.
     auto fast_body = [&](auto first, const char* ks, const char* vs, const f32x16* sc,
-                         f32x16* sn, const u32x4 (*pp)[2], u32x4 (*pc)[2]) __attribute__((always_inline)) {
+                         f32x16* sn, const u32x4 (*pp)[2], u32x4 (*pc)[2],
+                         float negm) __attribute__((always_inline)) {
       constexpr bool FIRST = decltype(first)::value != 0;
       constexpr int NSM = 2 * NS;              // score MFMAs
       constexpr int NPV = FIRST ? 0 : 4 * ND;  // P.V MFMAs
@@ -362,7 +372,8 @@ sel_attn_fwd_kernel(AttnArgs a) {
           oacc[db] = mfma32<DT>(va[db][blk][c], pp[blk][c], oacc[db]);
         }
 #pragma unroll
-        for (int j = (i * NPAIR) / NSLOT; j < ((i + 1) * NPAIR) / NSLOT; ++j) softmax_pair(sc, pc, j);
+        for (int j = (i * NPAIR) / NSLOT; j < ((i + 1) * NPAIR) / NSLOT; ++j)
+          softmax_pair(sc, pc, j, negm);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -444,7 +455,24 @@ sel_attn_fwd_kernel(AttnArgs a) {
           else
             mask_keys(kt, sc);
         } else {
-          mask_tail(kt, sc);
+          if (umode == 0) {
+            mask_tail(kt, sc);
+          } else {
+            // Grouped tiles.  A 64-key tile mostly lies inside one block, so
+            // a row attends all of it or none of it: a row with no key here
+            // gets the reference +inf (p = 0, no per-score work); scores are
+            // masked one by one only when some row attends part of the tile.
+            km = key_mask(kt);
+            if (__builtin_amdgcn_ballot_w64(km != 0ull && km != ~0ull) != 0) apply_mask(km, sc);
+            // A row that attended nothing so far has l = 0 and O = 0 under
+            // the placeholder reference -1e30; it takes its first attended
+            // tile's row maximum as its reference (no rescale needed).
+            if (__builtin_amdgcn_ballot_w64(m_run <= -1.0e30f && km != 0ull) != 0) {
+              const float m_tile =
+                  __builtin_elementwise_maximum(row_max(sc) * a.scale_log2, -1.0e30f);
+              if (m_run <= -1.0e30f && km != 0ull) m_run = m_tile;
+            }
+          }
         }
         if constexpr (SAFE) {
           if constexpr (!FIRST) pv(sV[k_wr], pp);  // before any rescale of O
@@ -466,7 +494,8 @@ sel_attn_fwd_kernel(AttnArgs a) {
           scores(sK[k_rd], sn);
           softmax(sc, pc);
         } else {
-          fast_body(first, sK[k_rd], sV[k_wr], sc, sn, pp, pc);
+          fast_body(first, sK[k_rd], sV[k_wr], sc, sn, pp, pc,
+                    (UNION && km == 0ull) ? -__builtin_inf() : -m_run);
         }
       }
       // Copies complete in issue order (per step: K, then V).  The next step
@@ -504,17 +533,15 @@ sel_attn_fwd_kernel(AttnArgs a) {
     // result unchanged up to rounding unless P overflows its 16-bit type or
     // the sums grow out of range; a row sum that is not below 2^32 (inf and
     // NaN included) sends the whole tile through the exact online pass.
+    // Grouped tiles run the same fast pass with their key masks; a row's
+    // reference is its first attended tile's row maximum.
     prologue();
-    if (umode == 0) {
-      run(Phase<0>{});
-      const float l_fast = l_run + __shfl_xor(l_run, 32);
-      if (uniform(__syncthreads_or(!(l_fast < 4294967296.0f)))) {
-        wait_copies();  // the fast pass's trailing copies land before reuse
-        __syncthreads();
-        prologue();
-        run(Phase<1>{});
-      }
-    } else {
+    run(Phase<0>{});
+    const float l_fast = l_run + __shfl_xor(l_run, 32);
+    if (uniform(__syncthreads_or(!(l_fast < 4294967296.0f)))) {
+      wait_copies();  // the fast pass's trailing copies land before reuse
+      __syncthreads();
+      prologue();
       run(Phase<1>{});
     }
 
