@@ -294,6 +294,171 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(
   for (int64_t i = lane; i < total; i += 64) dst[i] = ord[i % topk];
 }
 
+// One workgroup per (kv head, query block) row for rows of up to 4 * 64 * M
+// candidates: the forced blocks are taken first; each wave keeps a quarter
+// of the row in registers (M per lane) and picks its best R = k - forced
+// candidates by R rounds of lane-local scan plus wave butterfly (score
+// descending, id ascending); wave 0 then takes the best R of the four lists.
+// Every member of the row's best R is among its quarter's best R, so the
+// result equals a selection over the whole row.
+template <int M>
+__global__ __launch_bounds__(256) void topk_split_kernel(
+    const double* __restrict__ scores, int64_t nb,
+    const int32_t* __restrict__ cu_sb, int64_t batch,
+    const int32_t* __restrict__ cu_blk, int64_t n_tokens, int topk,
+    const int32_t* __restrict__ forced, int n_forced, int force_self,
+    int32_t* __restrict__ topk_idx, int32_t* __restrict__ compact) {
+  __shared__ int s_forced[SEL_MAXK];
+  __shared__ double s_ls[4][SEL_MAXK];  // each wave's picks: score, id
+  __shared__ int s_li[4][SEL_MAXK];
+  __shared__ int s_sel[SEL_MAXK];
+  __shared__ int s_out[SEL_MAXK];
+  __shared__ int s_nf;
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t e = upper_index(cu_sb, 0, batch + 1, b);
+  int32_t* crow = compact + ((int64_t)h * nb + b) * topk;
+  if (e < 0 || e >= batch || b >= cu_sb[e + 1]) {
+    for (int j = tid; j < topk; j += 256) crow[j] = -1;
+    return;
+  }
+  const int64_t cs = cu_sb[e];
+  const int nbb = (int)(cu_sb[e + 1] - cs);
+  const double* row = scores + ((int64_t)h * nb + b) * nb + cs;
+  const int kmax = topk < nbb ? topk : nbb;
+  // Forced blocks in order, distinct, valid, at most kmax.
+  if (tid == 0) {
+    int n = 0;
+    auto add = [&](int id) {
+      if (n >= kmax || id < 0 || id >= nbb) return;
+      for (int t = 0; t < n; ++t)
+        if (s_forced[t] == id) return;
+      s_forced[n++] = id;
+    };
+    if (force_self) add((int)(b - cs));
+    for (int f = 0; f < n_forced; ++f) add(forced[f]);
+    s_nf = n;
+  }
+  __syncthreads();
+  const int nf = s_nf, r_need = kmax - nf;
+  // This wave's quarter [q0, q0 + 64 M) of the row.
+  const int q0 = wv * 64 * M;
+  double v[M];
+  uint32_t taken = 0u;  // bit m: candidate q0 + lane + 64 m is unavailable
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int i = q0 + lane + 64 * m;
+    if (i < nbb) {
+      const double x = row[i];
+      v[m] = (x != x) ? -__builtin_inf() : x;
+    } else {
+      v[m] = -__builtin_inf();
+      taken |= 1u << m;
+    }
+  }
+  for (int t = 0; t < nf; ++t) {
+    const int i = s_forced[t] - q0;
+    if (i >= 0 && i < 64 * M && (i & 63) == lane) taken |= 1u << (i >> 6);
+  }
+  const int avail = (nbb - q0 > 0 ? (nbb - q0 < 64 * M ? nbb - q0 : 64 * M) : 0);
+  const int r_wave = r_need < avail ? r_need : avail;  // forced ones excluded below
+  int nw = 0;
+  for (int n = 0; n < r_wave; ++n) {
+    double bs = -__builtin_inf();
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      if (!((taken >> m) & 1u) && sel_better(v[m], q0 + lane + 64 * m, bs, bi)) {
+        bs = v[m];
+        bi = q0 + lane + 64 * m;
+      }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const double os = __shfl_xor(bs, o);
+      const int oi = __shfl_xor(bi, o);
+      if (sel_better(os, oi, bs, bi)) {
+        bs = os;
+        bi = oi;
+      }
+    }
+    bi = __builtin_amdgcn_readfirstlane(bi);
+    if (bi == 0x7fffffff) break;  // the quarter ran out (forced ones excluded)
+    const int li = bi - q0;
+    if ((li & 63) == lane) taken |= 1u << (li >> 6);
+    if (lane == 0) {
+      s_ls[wv][nw] = bs;
+      s_li[wv][nw] = bi;
+    }
+    ++nw;
+  }
+  if (lane == 0) s_li[wv][SEL_MAXK - 1] = nw;  // list length (nw < SEL_MAXK)
+  __syncthreads();
+  if (wv == 0) {
+    // Merge: the best r_need of the four lists (topk <= 64, so each list
+    // has at most 64 entries: lane l holds entry l of every list).
+    constexpr int T = 4;
+    double cv[T];
+    int ci[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if (lane < s_li[t][SEL_MAXK - 1]) {
+        cv[t] = s_ls[t][lane];
+        ci[t] = s_li[t][lane];
+      } else {
+        cv[t] = -__builtin_inf();
+        ci[t] = 0x7fffffff;
+      }
+    }
+    for (int t = 0; t < nf; ++t)
+      if (lane == 0) s_sel[t] = s_forced[t];
+    for (int n = 0; n < r_need; ++n) {
+      double bs = -__builtin_inf();
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        if (ci[t] != 0x7fffffff && sel_better(cv[t], ci[t], bs, bi)) {
+          bs = cv[t];
+          bi = ci[t];
+        }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const double os = __shfl_xor(bs, o);
+        const int oi = __shfl_xor(bi, o);
+        if (sel_better(os, oi, bs, bi)) {
+          bs = os;
+          bi = oi;
+        }
+      }
+      bi = __builtin_amdgcn_readfirstlane(bi);
+      if (bi == 0x7fffffff) break;
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        if (ci[t] == bi) ci[t] = 0x7fffffff;  // ids are distinct
+      if (lane == 0) s_sel[nf + n] = bi;
+    }
+  }
+  __syncthreads();
+  // Ascending order by rank (ids are distinct), -1 padding.
+  for (int j = tid; j < topk; j += 256) s_out[j] = -1;
+  __syncthreads();
+  for (int j = tid; j < kmax; j += 256) {
+    const int id = s_sel[j];
+    int r = 0;
+    for (int m = 0; m < kmax; ++m) r += s_sel[m] < id;
+    s_out[r] = id;
+  }
+  __syncthreads();
+  for (int j = tid; j < topk; j += 256) crow[j] = s_out[j];
+  int64_t t0 = cu_blk[b], t1 = cu_blk[b + 1];
+  t0 = t0 < 0 ? 0 : (t0 > n_tokens ? n_tokens : t0);
+  t1 = t1 < t0 ? t0 : (t1 > n_tokens ? n_tokens : t1);
+  int32_t* dst = topk_idx + ((int64_t)h * n_tokens + t0) * topk;
+  const int64_t total = (t1 - t0) * topk;
+  for (int64_t i = tid; i < total; i += 256) dst[i] = s_out[i % topk];
+}
+
 struct SelectWs {
   float* pq;
   float* pk;
@@ -388,7 +553,24 @@ extern "C" int lsrm_select_blocks(const void* q, const void* k, int dtype,
     LSRM_TOPK_WAVE(16);
   else if (n_blocks <= 64 * 32)
     LSRM_TOPK_WAVE(32);
-  else
+  else if (n_blocks <= 4 * 64 * 32 && topk <= 64) {
+#define LSRM_TOPK_SPLIT(M)                                                                \
+  hipLaunchKernelGGL(topk_split_kernel<M>, dim3((unsigned)n_blocks, (unsigned)hkv),      \
+                     dim3(256), 0, st, s.scores, n_blocks, cu_seqblocks, batch,            \
+                     cu_block_tokens, n_tokens, (int)topk, forced_blocks, (int)n_forced,   \
+                     force_self, topk_idx, topk_compact)
+    if (n_blocks <= 4 * 64 * 12)
+      LSRM_TOPK_SPLIT(12);
+    else if (n_blocks <= 4 * 64 * 16)
+      LSRM_TOPK_SPLIT(16);
+    else if (n_blocks <= 4 * 64 * 20)
+      LSRM_TOPK_SPLIT(20);
+    else if (n_blocks <= 4 * 64 * 24)
+      LSRM_TOPK_SPLIT(24);
+    else
+      LSRM_TOPK_SPLIT(32);
+#undef LSRM_TOPK_SPLIT
+  } else
     hipLaunchKernelGGL(topk_kernel, dim3((unsigned)n_blocks, (unsigned)hkv),
                        dim3(256), 0, st, s.scores, n_blocks, cu_seqblocks,
                        batch, cu_block_tokens, n_tokens, (int)topk,

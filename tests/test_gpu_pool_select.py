@@ -154,3 +154,33 @@ def test_select_ties_lowest_index():
     for b in range(10):
         expect = sorted(set([b] + [x for x in range(10) if x != b][:2]))
         assert compact[:, b].tolist() == [expect, expect]
+
+
+def test_select_split_path_bitexact():
+    # More than 2048 blocks per batch element: the four-wave split selection
+    # (cfg5's heavy-tailed blocks with near-tie scores, forced ids).
+    w = W.config(5, n=262144, heads=2)
+    assert 2048 < w.n_blocks <= 8192
+    topk_idx, compact, ref = _select_case(w, forced=[0, 5, 17])
+    np.testing.assert_array_equal(compact, ref)
+    np.testing.assert_array_equal(topk_idx, expand_per_token(ref, w.cu_block_tokens.numpy(), w.n))
+
+
+def test_select_split_path_ties_and_nan():
+    # 2200 one-token blocks whose keys are equal (every score ties: the
+    # lowest ids win) except one NaN block (ranked last).
+    n, d, topk = 2200, 64, 5
+    cu = torch.arange(0, n + 1, dtype=torch.int32)
+    q = torch.randn(n, 2, d).to(torch.bfloat16)
+    k = torch.ones(n, 2, d, dtype=torch.bfloat16)
+    k[1] = float("nan")
+    _, compact = H.select_blocks(q.to(DEV), k.to(DEV), torch.tensor([0, n], dtype=torch.int32, device=DEV),
+                                 cu.to(DEV), topk, [7], True)
+    compact = compact.cpu().numpy()
+    for b in (0, 1, 2, 7, 1000, n - 1):
+        chosen = [b] + ([7] if b != 7 else [])
+        rest = [x for x in range(n) if x not in chosen and x != 1]
+        expect = sorted(chosen + rest[:topk - len(chosen)])
+        if b == 1:  # the NaN block's own row: forced ids, then the lowest non-NaN ids
+            expect = sorted([1, 7] + [x for x in range(n) if x not in (1, 7)][:topk - 2])
+        assert compact[:, b].tolist() == [expect, expect], (b, compact[:, b].tolist(), expect)
