@@ -218,3 +218,24 @@ def test_fwd_later_blocks_dominate(dtype):
     topk[:, :, 0] = 0
     q, k, v = (t.to(dtype) for t in (q, k, v))
     _run_case(q, k, v, topk, cu_sb, cu_blk, cu_q, 1.0 / math.sqrt(d))
+
+
+@pytest.mark.parametrize("per_token", [False, True])
+def test_bwd_head_dim_128(per_token):
+    # head dim 128 takes the dQ and dK/dV bodies sized for it (run tiles and
+    # grouped per-token tiles alike)
+    n, hq, hkv, d = 1536, 4, 2, 128
+    rng = np.random.default_rng(12)
+    sizes = W.uniform_partition(n, 16, 160, rng)
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32))
+    gen = torch.Generator().manual_seed(13)
+    q = (0.5 * torch.randn(n, hq, d, generator=gen)).to(torch.bfloat16)
+    k = (0.5 * torch.randn(n, hkv, d, generator=gen)).to(torch.bfloat16)
+    v = (0.5 * torch.randn(n, hkv, d, generator=gen)).to(torch.bfloat16)
+    do = (0.5 * torch.randn(n, hq, d, generator=gen)).to(torch.bfloat16)
+    if per_token:
+        topk = random_topk(hkv, n, len(sizes), 5, gen, pad_frac=0.3)
+    else:
+        topk = random_topk(hkv, n, len(sizes), 5, gen, per_block_cu=cu)
+    _run_case(q, k, v, topk, torch.tensor([0, len(sizes)], dtype=torch.int32), cu,
+              torch.tensor([0, n], dtype=torch.int32), 1.0 / math.sqrt(d), do=do)
