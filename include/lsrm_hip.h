@@ -113,7 +113,8 @@ int lsrm_block_mean_pool(const void* x, int x_dtype, int64_t n_tokens,
  * descending, block id ascending).  Output rows list the selected
  * batch-local ids ascending, padded with -1.
  *   topk_idx     [hkv, n_tokens, topk] int32 (every token of a block gets the
- *                block's row; the layout spatial_selection_attention reads)
+ *                block's row, tokens outside every block get -1 rows; the
+ *                layout spatial_selection_attention reads)
  *   topk_compact [hkv, n_blocks, topk] int32 (one row per query block)
  * No reference function; nearest analogue sparse/ops/block_score.py:16-98.
  * ---------------------------------------------------------------------- */

@@ -459,6 +459,23 @@ __global__ __launch_bounds__(256) void topk_split_kernel(
   for (int64_t i = tid; i < total; i += 256) dst[i] = s_out[i % topk];
 }
 
+// Rows of tokens outside every block ([0, cu_blk[0]) and [cu_blk[nb], n),
+// clamped) are -1: the top-k kernels write only the tokens of blocks.
+__global__ __launch_bounds__(256) void uncovered_rows_kernel(const int32_t* __restrict__ cu_blk,
+                                                             int64_t nb, int64_t n_tokens,
+                                                             int topk,
+                                                             int32_t* __restrict__ topk_idx) {
+  const int h = blockIdx.y;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_tokens) return;
+  int64_t lo = cu_blk[0], hi = cu_blk[nb];
+  lo = lo < 0 ? 0 : (lo > n_tokens ? n_tokens : lo);
+  hi = hi < lo ? lo : (hi > n_tokens ? n_tokens : hi);
+  if (t >= lo && t < hi) return;
+  int32_t* row = topk_idx + ((int64_t)h * n_tokens + t) * topk;
+  for (int j = 0; j < topk; ++j) row[j] = -1;
+}
+
 struct SelectWs {
   float* pq;
   float* pk;
@@ -518,8 +535,16 @@ extern "C" int lsrm_select_blocks(const void* q, const void* k, int dtype,
   const size_t need = lsrm_select_blocks_workspace_size(n_tokens, n_blocks, hq,
                                                         hkv, head_dim);
   if (workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
-  if (n_blocks == 0) return LSRM_OK;
   hipStream_t st = (hipStream_t)stream;
+  if (n_blocks == 0) {  // every token lies outside the (empty) block list
+    if (n_tokens > 0) {
+      hipLaunchKernelGGL(uncovered_rows_kernel, dim3(ceil_div(n_tokens, 256), (unsigned)hkv),
+                         dim3(256), 0, st, cu_block_tokens, n_blocks, n_tokens, (int)topk,
+                         topk_idx);
+      LSRM_CHECK_LAUNCH();
+    }
+    return LSRM_OK;
+  }
   Carver ws{reinterpret_cast<char*>(align_up((size_t)workspace, 256)), 0,
             workspace_bytes - 256};
   SelectWs s;
@@ -577,6 +602,9 @@ extern "C" int lsrm_select_blocks(const void* q, const void* k, int dtype,
                        forced_blocks, (int)n_forced, force_self, topk_idx,
                        topk_compact);
 #undef LSRM_TOPK_WAVE
+  LSRM_CHECK_LAUNCH();
+  hipLaunchKernelGGL(uncovered_rows_kernel, dim3(ceil_div(n_tokens, 256), (unsigned)hkv),
+                     dim3(256), 0, st, cu_block_tokens, n_blocks, n_tokens, (int)topk, topk_idx);
   LSRM_CHECK_LAUNCH();
   return LSRM_OK;
 }

@@ -220,10 +220,12 @@ def select_blocks(q: torch.Tensor, k: torch.Tensor, cu_seqblocks: torch.Tensor,
     forced = None
     if forced_blocks is not None and len(forced_blocks) > 0:
         forced = torch.as_tensor(list(forced_blocks), dtype=torch.int32, device=dev)
-    topk_idx = torch.full((hkv, n, topk), -1, dtype=torch.int32, device=dev)
-    compact = torch.full((hkv, max(nb, 0), topk), -1, dtype=torch.int32, device=dev)
     if nb == 0 or n == 0:
-        return topk_idx, compact
+        return (torch.full((hkv, n, topk), -1, dtype=torch.int32, device=dev),
+                torch.full((hkv, max(nb, 0), topk), -1, dtype=torch.int32, device=dev))
+    # every row is written by the kernels (uncovered tokens get -1 rows)
+    topk_idx = torch.empty((hkv, n, topk), dtype=torch.int32, device=dev)
+    compact = torch.empty((hkv, nb, topk), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         ws_n = lib().lsrm_select_blocks_workspace_size(n, nb, hq, hkv, d)
         ws = _workspace(ws_n, dev)

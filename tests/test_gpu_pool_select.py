@@ -184,3 +184,23 @@ def test_select_split_path_ties_and_nan():
         if b == 1:  # the NaN block's own row: forced ids, then the lowest non-NaN ids
             expect = sorted([1, 7] + [x for x in range(n) if x not in (1, 7)][:topk - 2])
         assert compact[:, b].tolist() == [expect, expect], (b, compact[:, b].tolist(), expect)
+
+
+def test_select_tokens_outside_blocks_get_empty_rows():
+    # the blocks cover tokens [100, n - 50): the other tokens' rows are -1
+    n, d, hq = 2000, 64, 2
+    rng = np.random.default_rng(21)
+    sizes = W.uniform_partition(n - 150, 16, 96, rng)
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32) + 100)
+    g = torch.Generator().manual_seed(22)
+    q = torch.randn(n, hq, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(n, hq, d, generator=g).to(torch.bfloat16)
+    cu_sb = torch.tensor([0, len(sizes)], dtype=torch.int32)
+    topk_idx, compact = H.select_blocks(q.to(DEV), k.to(DEV), cu_sb.to(DEV), cu.to(DEV), 4, None, True)
+    pq = block_mean_pool_ref(_f32(q).reshape(n, -1), cu.numpy()).reshape(-1, hq, d)
+    pk = block_mean_pool_ref(_f32(k).reshape(n, -1), cu.numpy()).reshape(-1, hq, d)
+    ref = select_blocks_ref(pq, pk, cu_sb.numpy(), 4, None, True)
+    np.testing.assert_array_equal(compact.cpu().numpy(), ref)
+    ti = topk_idx.cpu().numpy()
+    assert (ti[:, :100] == -1).all() and (ti[:, n - 50:] == -1).all()
+    np.testing.assert_array_equal(ti, expand_per_token(ref, cu.numpy(), n))
