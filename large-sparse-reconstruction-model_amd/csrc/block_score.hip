@@ -41,6 +41,23 @@ __device__ inline bool ranks_before(float v, int i, float w, int j) {
   return v > w || (v == w && i < j);
 }
 
+// Rank key of a score >= 0 (its bits order as unsigned integers) and an id
+// in [0, 2^31): a larger key ranks before, equal scores by lower id; every
+// key is nonzero, so 0 marks an empty entry.
+__device__ inline uint64_t rank_key(float v, int id) {
+  return ((uint64_t)__float_as_uint(v) << 32) | (0x80000000u | (uint32_t)(0x7fffffff - id));
+}
+
+// Compare-exchange of two rank keys: x gets the larger when desc, else y.
+__device__ inline void key_swap(uint64_t& x, uint64_t& y, bool desc) {
+  const uint64_t hi = x > y ? x : y, lo = x > y ? y : x;
+  x = desc ? hi : lo;
+  y = desc ? lo : hi;
+}
+
+// Capacity (entries per lane) of the LDS buffer of the two-pass selection.
+constexpr int BS_CAP = 32;
+
 template <int DT, int D, int K>
 __global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
   constexpr int NS = D / 16;
@@ -71,6 +88,9 @@ __global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
       tv[i] = -1.0f;  // below every score (scores are >= 0)
       ti[i] = -1;
     }
+    uint64_t tk[K];  // list as rank keys (K <= 32), 0 = empty
+#pragma unroll
+    for (int i = 0; i < K; ++i) tk[i] = 0ull;
     // Inserts (v, id) into the descending list; ids arrive ascending, so an
     // equal score already listed keeps its place.
     auto insert = [&](float v, int id) __attribute__((always_inline)) {
@@ -94,39 +114,194 @@ __global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
         ka[s] = key < nc ? *reinterpret_cast<const u32x4*>(ckh + key * ck_stride + s * 16)
                          : u32x4{0u, 0u, 0u, 0u};
     };
-    u32x4 kbuf[2][NS];
-    if (nc > 0) load_k(0, kbuf[0]);
-    int cur = 0;
-    for (int64_t c0 = 0; c0 < nc; c0 += 32) {
-      if (c0 + 32 < nc) load_k(c0 + 32, kbuf[cur ^ 1]);
-      const u32x4* ka = kbuf[cur];
-      float p[16];
+    // The row's query fragment and log2-scaled lse of query head g of this
+    // kv head: loaded once when the group has one head, else one head ahead
+    // of its use, so no block waits on a query load.
+    auto load_q = [&](int g, u32x4* qb, float& l2) __attribute__((always_inline)) {
+      const int hh = h * a.g + g;
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        qb[s] = row_ok ? *reinterpret_cast<const u32x4*>(
+                             a.q + (row * a.hq + hh) * D + s * 16 + hb * 8)
+                       : u32x4{0u, 0u, 0u, 0u};
+      l2 = row_ok ? a.lse[(int64_t)hh * a.nq + row] * LOG2E_REF : 0.0f;
+    };
+    u32x4 qcur[NS];
+    float l2cur;
+    load_q(0, qcur, l2cur);
+    // p[v] = score of key c0 + acc_row(v, hb) for this lane's row: the sum
+    // over the group's query heads of exp2(s * scale - lse * log2e).
+    auto block_scores = [&](const u32x4* ka, float* p) __attribute__((always_inline)) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) p[v] = 0.0f;
       for (int g = 0; g < a.g; ++g) {
-        const int hh = h * a.g + g;
-        u32x4 qb[NS];
-#pragma unroll
-        for (int s = 0; s < NS; ++s)
-          qb[s] = row_ok ? *reinterpret_cast<const u32x4*>(
-                               a.q + (row * a.hq + hh) * D + s * 16 + hb * 8)
-                         : u32x4{0u, 0u, 0u, 0u};
-        const float l2 = row_ok ? a.lse[(int64_t)hh * a.nq + row] * LOG2E_REF : 0.0f;
+        u32x4 qn[NS];
+        float l2n = 0.0f;
+        if (a.g > 1) load_q(g + 1 < a.g ? g + 1 : 0, qn, l2n);
         f32x16 sacc;
 #pragma unroll
         for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) sacc = mfma32<DT>(ka[s], qb[s], sacc);
+        for (int s = 0; s < NS; ++s) sacc = mfma32<DT>(ka[s], qcur[s], sacc);
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-          p[v] += __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], a.qk_scale, -l2));
+          p[v] += __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], a.qk_scale, -l2cur));
+        if (a.g > 1) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) qcur[s] = qn[s];
+          l2cur = l2n;
+        }
+      }
+    };
+    // Runs body(c0, p) over the element's 32-key blocks in order, two blocks
+    // a step, with the next two blocks' compressed keys loading while the
+    // current two are scored.
+    auto for_blocks = [&](auto&& body) __attribute__((always_inline)) {
+      u32x4 kc[2][NS], kn[2][NS];
+      if (nc > 0) {
+        load_k(0, kc[0]);
+        load_k(32, kc[1]);
+      }
+      for (int64_t c0 = 0; c0 < nc; c0 += 64) {
+        if (c0 + 64 < nc) {
+          load_k(c0 + 64, kn[0]);
+          load_k(c0 + 96, kn[1]);
+        }
+        float p[16];
+        block_scores(kc[0], p);
+        body(c0, p);
+        if (c0 + 32 < nc) {
+          block_scores(kc[1], p);
+          body(c0 + 32, p);
+        }
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          kc[0][s] = kn[0][s];
+          kc[1][s] = kn[1][s];
+        }
+      }
+    };
+
+    if constexpr (K <= 32) {
+      // Merges 16 candidate rank keys (0 = none) into the list: a bitonic
+      // sort of the candidates, then the larger of list[i] and
+      // candidate[K-1-i], a bitonic sequence holding the best K of both, is
+      // sorted by a bitonic merge.
+      auto merge16 = [&](uint64_t* ck) __attribute__((always_inline)) {
+#pragma unroll
+        for (int size = 2; size <= 16; size <<= 1)
+#pragma unroll
+          for (int j = size / 2; j > 0; j >>= 1)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int o = i ^ j;
+              if (o > i) key_swap(ck[i], ck[o], (i & size) == 0);
+            }
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+          const uint64_t bk = K - 1 - i < 16 ? ck[K - 1 - i < 16 ? K - 1 - i : 0] : 0ull;
+          tk[i] = tk[i] > bk ? tk[i] : bk;
+        }
+#pragma unroll
+        for (int j = K / 2; j > 0; j >>= 1)
+#pragma unroll
+          for (int i = 0; i < K; ++i)
+            if ((i & j) == 0) key_swap(tk[i], tk[i | j], true);
+      };
+      // Two passes when the element has many keys per list entry: the first
+      // bounds the row's K-th best score from below by the K-th best of the
+      // per-lane block maxima (each is a distinct key of the row), the second
+      // keeps only keys at or above that bound, appending them to this lane's
+      // LDS buffer, merged 16 at a time.  One pass otherwise: every block's
+      // candidates merged as they come.
+      __shared__ float2 s_buf[4][BS_CAP + 1][64];  // [wave][slot][lane]; slot BS_CAP: discard
+      float2(*buf)[64] = s_buf[threadIdx.x >> 6];
+      if (a.g <= 4 && nc >= 8 * K) {
+        float mk[K];  // descending K best block maxima of this lane
+#pragma unroll
+        for (int i = 0; i < K; ++i) mk[i] = -1.0f;
+        for_blocks([&](int64_t c0, const float* p) __attribute__((always_inline)) {
+          // (fmax ignores a NaN score)
+          const int lim = row_ok ? (int)(nc - c0) : 0;
+          float bm = -1.0f;
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            bm = __builtin_fmaxf(bm, acc_row(v, hb) < lim ? p[v] : -1.0f);
+          // insertion into the descending list: entry i becomes bm clamped
+          // to [mk[i], mk[i-1]]
+          if (__builtin_amdgcn_ballot_w64(bm > mk[K - 1]) != 0) {
+#pragma unroll
+            for (int i = K - 1; i > 0; --i) mk[i] = __builtin_amdgcn_fmed3f(mk[i], bm, mk[i - 1]);
+            mk[0] = __builtin_fmaxf(mk[0], bm);
+          }
+        });
+        float t = __builtin_inff();
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+          const float pm = __shfl_xor(mk[K - 1 - i], 32);
+          t = __builtin_fminf(t, __builtin_fmaxf(mk[i], pm));
+        }
+        // a little below the bound, so a rounding difference between the
+        // passes can never drop a key
+        const float tb = t > 0.0f && t < __builtin_inff() ? t * (1.0f - 0x1p-16f) : t;
+
+        int cnt = 0;
+        auto flush = [&]() __attribute__((always_inline)) {
+          for (int base = 0; __builtin_amdgcn_ballot_w64(base < cnt) != 0; base += 16) {
+            uint64_t ck[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int slot = base + i < BS_CAP ? base + i : BS_CAP;
+              const float2 e = buf[slot][lane];
+              ck[i] = base + i < cnt ? rank_key(e.x, __float_as_int(e.y)) : 0ull;
+            }
+            merge16(ck);
+          }
+          cnt = 0;
+        };
+        for_blocks([&](int64_t c0, const float* p) __attribute__((always_inline)) {
+          if (__builtin_amdgcn_ballot_w64(cnt > BS_CAP - 16) != 0) flush();
+          const int lim = row_ok ? (int)(nc - c0) : 0;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            // (a NaN score fails the comparison, so is never chosen)
+            const bool ok = (acc_row(v, hb) < lim) & (p[v] >= tb);
+            buf[ok ? cnt : BS_CAP][lane] = float2{p[v], __int_as_float((int)c0 + acc_row(v, hb))};
+            cnt += ok ? 1 : 0;
+          }
+        });
+        flush();
+      } else {
+        for_blocks([&](int64_t c0, const float* p) __attribute__((always_inline)) {
+          // candidates that would enter the list; the merge is skipped when
+          // no lane has one
+          uint64_t ck[16];
+          uint64_t best = 0ull;
+          const int lim = (int)(nc - c0);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            // NaN scores are never chosen
+            const bool ok = (acc_row(v, hb) < lim) & (p[v] == p[v]);
+            ck[v] = ok ? rank_key(p[v], (int)c0 + acc_row(v, hb)) : 0ull;
+            best = best > ck[v] ? best : ck[v];
+          }
+          const bool enter = best > tk[K - 1];
+          if (__builtin_amdgcn_ballot_w64(enter) != 0) merge16(ck);
+        });
       }
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t key = c0 + acc_row(v, hb);
-        if (key < nc) insert(p[v], (int)key);
+      for (int i = 0; i < K; ++i) {
+        tv[i] = tk[i] != 0ull ? __uint_as_float((uint32_t)(tk[i] >> 32)) : -1.0f;
+        ti[i] = tk[i] != 0ull ? 0x7fffffff - (int)((uint32_t)tk[i] & 0x7fffffffu) : -1;
       }
-      cur ^= 1;
+    } else {
+      for_blocks([&](int64_t c0, const float* p) __attribute__((always_inline)) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t key = c0 + acc_row(v, hb);
+          if (key < nc) insert(p[v], (int)key);
+        }
+      });
     }
 
     // Merge with the partner lane's list (same row, the other 16 keys of

@@ -152,3 +152,35 @@ def test_learned_selection_path_end_to_end():
                                           lse.cpu().numpy(), 8, w.cu_seqlens.numpy(),
                                           cu_sb.numpy(), return_scores=True)
     _check_selection(topk_idx, ref_sel, scores, 8, w.cu_seqlens, cu_sb)
+
+
+@pytest.mark.parametrize("hq,hkv,d,topk", [
+    (4, 4, 64, 16),      # MHA, the BASELINE head_dim
+    (8, 4, 64, 24),      # G = 2, topk not a power of two
+    (8, 2, 64, 32),      # G = 4
+    (2, 2, 128, 8),      # D = 128
+])
+def test_block_score_many_keys(hq, hkv, d, topk):
+    """Elements with at least 8 topk keys take the two-pass selection (a
+    lower bound on the row's topk-th score from block maxima, then a
+    filtered buffer); the last element stays on the one-pass merge."""
+    q_lens, c_lens = [157, 300, 45, 70], [462, 300, 1030, 100]
+    q, ck, cv, cu_q, cu_c = _case(4, q_lens, c_lens, hq, hkv, d)
+    _, lse = compressed_attention_ref(q, ck, cv, cu_q, cu_c)
+    got = ops.get_block_score(q.to(DEV), ck.to(DEV), lse.to(DEV), topk, cu_q.to(DEV),
+                              cu_c.to(DEV), None, None)
+    ref, scores = get_block_score_ref(q.float().numpy(), ck.float().numpy(), lse.numpy(),
+                                      topk, cu_q.numpy(), cu_c.numpy(), return_scores=True)
+    mism = _check_selection(got, ref, scores, topk, cu_q, cu_c)
+    assert mism <= 0.01 * q.shape[0] * hkv + 2
+
+
+def test_block_score_many_keys_all_tied():
+    # 300 identical compressed keys: every key reaches the two-pass bound, the
+    # buffer fills and is merged repeatedly; ties still take the lowest ids
+    q, ck, cv, cu_q, cu_c = _case(5, [96], [300], 2, 2, 64)
+    ck = ck[:1].expand(300, 2, 64).contiguous()
+    lse = torch.zeros(2, 96)
+    got = ops.get_block_score(q.to(DEV), ck.to(DEV), lse.to(DEV), 16, cu_q.to(DEV),
+                              cu_c.to(DEV), None, None)
+    assert (got.cpu() == torch.arange(16)).all()
