@@ -91,6 +91,8 @@ __global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
     uint64_t tk[K];  // list as rank keys (K <= 32), 0 = empty
 #pragma unroll
     for (int i = 0; i < K; ++i) tk[i] = 0ull;
+    uint64_t mk_out[K];  // the row's merged list as rank keys (K <= 32)
+    int mi[K];           // the row's best ids, best first (-1 = none)
     // Inserts (v, id) into the descending list; ids arrive ascending, so an
     // equal score already listed keeps its place.
     auto insert = [&](float v, int id) __attribute__((always_inline)) {
@@ -289,11 +291,25 @@ __global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
           if (__builtin_amdgcn_ballot_w64(enter) != 0) merge16(ck);
         });
       }
+      // Merge with the partner lane's list (same row, the other 16 keys of
+      // every block): the larger of own[i] and partner[K-1-i] is a bitonic
+      // sequence holding the row's best K, sorted by a bitonic merge.
 #pragma unroll
       for (int i = 0; i < K; ++i) {
-        tv[i] = tk[i] != 0ull ? __uint_as_float((uint32_t)(tk[i] >> 32)) : -1.0f;
-        ti[i] = tk[i] != 0ull ? 0x7fffffff - (int)((uint32_t)tk[i] & 0x7fffffffu) : -1;
+        const uint64_t x = tk[K - 1 - i];
+        const uint32_t plo = (uint32_t)__shfl_xor((int)(uint32_t)x, 32);
+        const uint32_t phi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), 32);
+        const uint64_t pk = ((uint64_t)phi << 32) | plo;
+        mk_out[i] = tk[i] > pk ? tk[i] : pk;
       }
+#pragma unroll
+      for (int j = K / 2; j > 0; j >>= 1)
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+          if ((i & j) == 0) key_swap(mk_out[i], mk_out[i | j], true);
+#pragma unroll
+      for (int i = 0; i < K; ++i)
+        mi[i] = mk_out[i] != 0ull ? 0x7fffffff - (int)((uint32_t)mk_out[i] & 0x7fffffffu) : -1;
     } else {
       for_blocks([&](int64_t c0, const float* p) __attribute__((always_inline)) {
 #pragma unroll
@@ -304,29 +320,30 @@ __global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
       });
     }
 
-    // Merge with the partner lane's list (same row, the other 16 keys of
-    // every block): the better of (own[i], partner[K-1-i]) is a bitonic
-    // sequence holding the row's best K, sorted by a bitonic merge.
-    float mv[K];
-    int mi[K];
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      const float pv = __shfl_xor(tv[K - 1 - i], 32);
-      const int pi = __shfl_xor(ti[K - 1 - i], 32);
-      const bool own = ti[i] >= 0 && (pi < 0 || ranks_before(tv[i], ti[i], pv, pi));
-      mv[i] = own ? tv[i] : pv;
-      mi[i] = own ? ti[i] : pi;
-    }
-#pragma unroll
-    for (int j = K / 2; j > 0; j >>= 1) {
+    if constexpr (K > 32) {
+      // Merge with the partner lane's list (same row, the other 16 keys of
+      // every block): the better of (own[i], partner[K-1-i]) is a bitonic
+      // sequence holding the row's best K, sorted by a bitonic merge.
+      float mv[K];
 #pragma unroll
       for (int i = 0; i < K; ++i) {
-        if ((i & j) == 0) {
-          const int o = i | j;
-          const bool keep = mi[i] >= 0 && (mi[o] < 0 || ranks_before(mv[i], mi[i], mv[o], mi[o]));
-          const float v0 = keep ? mv[i] : mv[o], v1 = keep ? mv[o] : mv[i];
-          const int i0 = keep ? mi[i] : mi[o], i1 = keep ? mi[o] : mi[i];
-          mv[i] = v0; mv[o] = v1; mi[i] = i0; mi[o] = i1;
+        const float pv = __shfl_xor(tv[K - 1 - i], 32);
+        const int pi = __shfl_xor(ti[K - 1 - i], 32);
+        const bool own = ti[i] >= 0 && (pi < 0 || ranks_before(tv[i], ti[i], pv, pi));
+        mv[i] = own ? tv[i] : pv;
+        mi[i] = own ? ti[i] : pi;
+      }
+#pragma unroll
+      for (int j = K / 2; j > 0; j >>= 1) {
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+          if ((i & j) == 0) {
+            const int o = i | j;
+            const bool keep = mi[i] >= 0 && (mi[o] < 0 || ranks_before(mv[i], mi[i], mv[o], mi[o]));
+            const float v0 = keep ? mv[i] : mv[o], v1 = keep ? mv[o] : mv[i];
+            const int i0 = keep ? mi[i] : mi[o], i1 = keep ? mi[o] : mi[i];
+            mv[i] = v0; mv[o] = v1; mi[i] = i0; mi[o] = i1;
+          }
         }
       }
     }
