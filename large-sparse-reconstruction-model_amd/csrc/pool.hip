@@ -14,7 +14,8 @@
 //   pool_combine : one thread per (block, 8-channel group) adds the block's
 //                  partials in chunk order, divides by the length and rounds.
 // Every add is sequential, so the result is a fixed function of the input
-// (the contract the CPU oracle restates bit for bit).
+// (the contract the CPU oracle restates bit for bit).  Input rows are read
+// exactly once, with nontemporal loads (measured +8% on the cfg3 K tensor).
 #include "common.h"
 
 namespace lsrm {
@@ -26,8 +27,8 @@ template <int DT>
 struct Vec8 {
   // Loads channels [c, c+8) of row r as fp32.
   __device__ static inline void load(const void* x, int64_t off, float* v) {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(
-        reinterpret_cast<const uint16_t*>(x) + off);
+    const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+        reinterpret_cast<const uint16_t*>(x) + off));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       v[2 * i] = to_f32<DT>((uint16_t)(w[i] & 0xffffu));
@@ -38,11 +39,10 @@ struct Vec8 {
 template <>
 struct Vec8<LSRM_F32> {
   __device__ static inline void load(const void* x, int64_t off, float* v) {
-    const float4* p =
-        reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + off);
-    float4 a = p[0], b = p[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    const f32x4* p = reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(x) + off);
+    const f32x4 a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
+    v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+    v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
   }
 };
 
@@ -113,8 +113,8 @@ __global__ __launch_bounds__(256) void pool_pieces(
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t rr = r + u < r1 ? r + u : r1 - 1;
-        raw[u] = *reinterpret_cast<const u32x4*>(
-            reinterpret_cast<const uint16_t*>(x) + rr * ch + c0);
+        raw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            reinterpret_cast<const uint16_t*>(x) + rr * ch + c0));
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) asm volatile("" ::"v"(raw[u]));
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256) void pool_pieces_slab(
 #pragma unroll
     for (int u = 0; u < POOL_G; ++u) {
       const int64_t rr = r + u < r1 ? r + u : r1 - 1;
-      dst[u] = *reinterpret_cast<const u32x4*>(xp + rr * ch);
+      dst[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xp + rr * ch));
     }
   };
   load_group(buf[0], r0);
