@@ -5,8 +5,10 @@ A step is one layer over synthetic, HBM-resident inputs (B=1, N=131072
 tokens: 8 image blocks of 1024 + 122880 Morton-ordered voxel tokens in runs of
 32-512, H=24, D=64, bf16, top-16 with the image blocks and the own block
 forced):
-  1. key and value block compression (lsrm_block_mean_pool, x2),
-  2. per-query-block selection (pool Q/K in fp32, fp64 scores, top-k),
+  1. key and value block compression (lsrm_block_mean_pool: keys once in fp32,
+     shared with the selection and rounded to bf16 for the compressed keys;
+     values on a second stream, concurrent with steps 2-3),
+  2. per-query-block selection (pool Q in fp32, fp64 scores, top-k),
   3. selected-block attention forward (device plan + MFMA kernel).
 `value` is the layer's effective TFLOP/s on the attended FLOPs
 (4 * D * sum over heads and queries of the attended key count).  The
@@ -210,11 +212,25 @@ def main() -> int:
     k2 = k.view(n, hkv * d)
     v2 = v.view(n, hkv * d)
 
+    # Value compression does not feed the selection or the forward: it runs on
+    # a second stream (default priority) beside them and joins before the step
+    # ends.  Keys are pooled once in fp32: the selection takes those means and
+    # the compressed keys are their rounding to bf16 (what block_mean_pool
+    # with a bf16 output returns).
+    side = torch.cuda.Stream(device=dev)
+
     def layer():
-        ck = H.block_mean_pool(k2, cu_blk)
-        cv = H.block_mean_pool(v2, cu_blk)
-        topk_idx, compact = H.select_blocks(q, k, cu_sb, cu_blk, w.topk, w.forced_blocks, True)
+        main = torch.cuda.current_stream(dev)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            cv = H.block_mean_pool(v2, cu_blk)
+        pk = H.block_mean_pool(k2, cu_blk, torch.float32)
+        ck = pk.to(k2.dtype)
+        topk_idx, compact = H.select_blocks(q, k, cu_sb, cu_blk, w.topk, w.forced_blocks, True,
+                                            pooled_k=pk)
         o, lse = H.sel_attn_fwd(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, w.scale)
+        main.wait_stream(side)
+        cv.record_stream(main)
         return ck, cv, topk_idx, compact, o, lse
 
     # Work count from the actual selection.

@@ -13,8 +13,8 @@
  *   lsrm_block_mean_pool      sparse/module/spatial_sparse_attention.py:27-37
  *                             (SpatialSparseAttentionIn.sparse3d_compression,
  *                              torch.segment_reduce(reduce="mean"))
- *   lsrm_select_blocks        no reference function (the block-selection rule
- *                             of the benchmark); nearest analogue
+ *   lsrm_select_blocks(_pooled) no reference function (the block-selection
+ *                             rule of the benchmark); nearest analogue
  *                             sparse/ops/block_score.py:16-98
  *   lsrm_sel_attn_validate    the asserts of
  *                             sparse/ops/triton_native_sparse_attention_impl_kvcentric.py:1295-1301
@@ -130,6 +130,20 @@ int lsrm_select_blocks(const void* q, const void* k, int dtype,
                        int force_self, int32_t* topk_idx,
                        int32_t* topk_compact, void* workspace,
                        size_t workspace_bytes, void* stream);
+/* Same selection with k already pooled: pooled_k is the fp32 block mean of
+ * k, [n_blocks, hkv * head_dim] (lsrm_block_mean_pool with out_dtype
+ * LSRM_F32), so a caller that also needs the compressed keys pools k once
+ * (rounding that fp32 mean to the key dtype gives the same compressed keys).
+ * No reference function; the same rule as lsrm_select_blocks. */
+int lsrm_select_blocks_pooled(const void* q, const float* pooled_k, int dtype,
+                              int64_t n_tokens, int64_t hq, int64_t hkv,
+                              int64_t head_dim, const int32_t* cu_seqblocks,
+                              int64_t batch, const int32_t* cu_block_tokens,
+                              int64_t n_blocks, int64_t topk,
+                              const int32_t* forced_blocks, int64_t n_forced,
+                              int force_self, int32_t* topk_idx,
+                              int32_t* topk_compact, void* workspace,
+                              size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Metadata validation for the selected-attention entry points.  Writes the

@@ -511,21 +511,19 @@ extern "C" size_t lsrm_select_blocks_workspace_size(int64_t n_tokens,
   return ws.used + 256;
 }
 
-extern "C" int lsrm_select_blocks(const void* q, const void* k, int dtype,
-                                  int64_t n_tokens, int64_t hq, int64_t hkv,
-                                  int64_t head_dim, const int32_t* cu_seqblocks,
-                                  int64_t batch,
-                                  const int32_t* cu_block_tokens,
-                                  int64_t n_blocks, int64_t topk,
-                                  const int32_t* forced_blocks,
-                                  int64_t n_forced, int force_self,
-                                  int32_t* topk_idx, int32_t* topk_compact,
-                                  void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+// Shared body of lsrm_select_blocks (k given: pooled here) and
+// lsrm_select_blocks_pooled (pooled_k given: the fp32 block means of k).
+static int select_blocks_impl(const void* q, const void* k, const float* pooled_k, int dtype,
+                              int64_t n_tokens, int64_t hq, int64_t hkv, int64_t head_dim,
+                              const int32_t* cu_seqblocks, int64_t batch,
+                              const int32_t* cu_block_tokens, int64_t n_blocks, int64_t topk,
+                              const int32_t* forced_blocks, int64_t n_forced, int force_self,
+                              int32_t* topk_idx, int32_t* topk_compact, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   if (n_tokens < 0 || hq <= 0 || hkv <= 0 || head_dim <= 0 || batch <= 0 ||
       n_blocks < 0 || topk <= 0 || n_forced < 0 || !cu_seqblocks ||
       !cu_block_tokens || (n_forced > 0 && !forced_blocks) ||
-      (n_tokens > 0 && (!q || !k || !topk_idx)) ||
+      (n_tokens > 0 && (!q || !(k || pooled_k) || !topk_idx)) ||
       (n_blocks > 0 && !topk_compact))
     return LSRM_ERR_INVALID_ARG;
   if (hq % hkv != 0) return LSRM_ERR_INVALID_ARG;
@@ -555,13 +553,16 @@ extern "C" int lsrm_select_blocks(const void* q, const void* k, int dtype,
                                   cu_block_tokens, n_blocks, s.pq, LSRM_F32,
                                   s.partial, s.first, st);
   if (rc) return rc;
-  rc = launch_block_mean_pool(k, dtype, n_tokens, hkv * head_dim,
-                              cu_block_tokens, n_blocks, s.pk, LSRM_F32,
-                              s.partial, s.first, st);
-  if (rc) return rc;
+  const float* pk = pooled_k;
+  if (!pk) {
+    rc = launch_block_mean_pool(k, dtype, n_tokens, hkv * head_dim, cu_block_tokens, n_blocks,
+                                s.pk, LSRM_F32, s.partial, s.first, st);
+    if (rc) return rc;
+    pk = s.pk;
+  }
   const unsigned nt = (unsigned)ceil_div(n_blocks, SCORE_TILE);
   hipLaunchKernelGGL(score_kernel, dim3(nt, nt, (unsigned)hkv), dim3(256), 0,
-                     st, s.pq, s.pk, n_blocks, (int)hq, (int)hkv,
+                     st, s.pq, pk, n_blocks, (int)hq, (int)hkv,
                      (int)head_dim, s.scores);
   LSRM_CHECK_LAUNCH();
   const unsigned rows4 = (unsigned)ceil_div(n_blocks * hkv, 4);
@@ -607,4 +608,34 @@ extern "C" int lsrm_select_blocks(const void* q, const void* k, int dtype,
                      dim3(256), 0, st, cu_block_tokens, n_blocks, n_tokens, (int)topk, topk_idx);
   LSRM_CHECK_LAUNCH();
   return LSRM_OK;
+}
+
+extern "C" int lsrm_select_blocks(const void* q, const void* k, int dtype, int64_t n_tokens,
+                                  int64_t hq, int64_t hkv, int64_t head_dim,
+                                  const int32_t* cu_seqblocks, int64_t batch,
+                                  const int32_t* cu_block_tokens, int64_t n_blocks, int64_t topk,
+                                  const int32_t* forced_blocks, int64_t n_forced, int force_self,
+                                  int32_t* topk_idx, int32_t* topk_compact, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  if (n_tokens > 0 && !k) return LSRM_ERR_INVALID_ARG;
+  return select_blocks_impl(q, k, nullptr, dtype, n_tokens, hq, hkv, head_dim, cu_seqblocks,
+                            batch, cu_block_tokens, n_blocks, topk, forced_blocks, n_forced,
+                            force_self, topk_idx, topk_compact, workspace, workspace_bytes,
+                            stream);
+}
+
+extern "C" int lsrm_select_blocks_pooled(const void* q, const float* pooled_k, int dtype,
+                                         int64_t n_tokens, int64_t hq, int64_t hkv,
+                                         int64_t head_dim, const int32_t* cu_seqblocks,
+                                         int64_t batch, const int32_t* cu_block_tokens,
+                                         int64_t n_blocks, int64_t topk,
+                                         const int32_t* forced_blocks, int64_t n_forced,
+                                         int force_self, int32_t* topk_idx,
+                                         int32_t* topk_compact, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  if (n_blocks > 0 && !pooled_k) return LSRM_ERR_INVALID_ARG;
+  return select_blocks_impl(q, nullptr, pooled_k, dtype, n_tokens, hq, hkv, head_dim,
+                            cu_seqblocks, batch, cu_block_tokens, n_blocks, topk, forced_blocks,
+                            n_forced, force_self, topk_idx, topk_compact, workspace,
+                            workspace_bytes, stream);
 }

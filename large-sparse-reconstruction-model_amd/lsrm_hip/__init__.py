@@ -50,6 +50,11 @@ _SIGNATURES = {
         [_P, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I,
          _P, _P, _P, _SZ, _P],
     ),
+    "lsrm_select_blocks_pooled": (
+        _I,
+        [_P, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I,
+         _P, _P, _P, _SZ, _P],
+    ),
     "lsrm_sel_attn_validate": (
         _I, [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _P, _P]),
     "lsrm_sel_attn_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I]),
@@ -193,12 +198,14 @@ def block_mean_pool(x: torch.Tensor, cu_block_tokens: torch.Tensor,
 def select_blocks(q: torch.Tensor, k: torch.Tensor, cu_seqblocks: torch.Tensor,
                   cu_block_tokens: torch.Tensor, topk: int,
                   forced_blocks: Optional[Sequence[int]] = None,
-                  force_self: bool = True):
+                  force_self: bool = True,
+                  pooled_k: Optional[torch.Tensor] = None):
     """Per-query-block top-k selection (self attention).
 
     q [N, Hq, D], k [N, Hkv, D].  Returns (topk_idx [Hkv, N, topk],
     topk_compact [Hkv, n_blocks, topk]) int32, ids batch-local, ascending,
-    -1 padded.
+    -1 padded.  pooled_k, when given, is block_mean_pool(k.view(N, -1),
+    cu_block_tokens, torch.float32): the selection then skips pooling k.
     """
     if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
         raise ValueError("q [N, Hq, D] and k [N, Hkv, D] must share N and D")
@@ -208,7 +215,8 @@ def select_blocks(q: torch.Tensor, k: torch.Tensor, cu_seqblocks: torch.Tensor,
         raise ValueError("Hq must be a multiple of Hkv")
     if topk <= 0:
         raise ValueError("topk must be positive")
-    dev = _dev_check(q, k, cu_seqblocks, cu_block_tokens)
+    dev = _dev_check(q, k, cu_seqblocks, cu_block_tokens,
+                     *([] if pooled_k is None else [pooled_k]))
     q = q.contiguous()
     k = k.contiguous()
     cu_sb = _i32(cu_seqblocks)
@@ -229,11 +237,17 @@ def select_blocks(q: torch.Tensor, k: torch.Tensor, cu_seqblocks: torch.Tensor,
     with torch.cuda.device(dev):
         ws_n = lib().lsrm_select_blocks_workspace_size(n, nb, hq, hkv, d)
         ws = _workspace(ws_n, dev)
-        _check(lib().lsrm_select_blocks(
-            _ptr(q), _ptr(k), _DTYPE_CODE[q.dtype], n, hq, hkv, d, _ptr(cu_sb), batch,
+        if pooled_k is not None:
+            if pooled_k.dtype != torch.float32 or tuple(pooled_k.shape) != (nb, hkv * d):
+                raise ValueError(f"pooled_k must be float32 [{nb}, {hkv * d}]")
+            pooled_k = pooled_k.contiguous()
+        entry = lib().lsrm_select_blocks if pooled_k is None else lib().lsrm_select_blocks_pooled
+        _check(entry(
+            _ptr(q), _ptr(k if pooled_k is None else pooled_k), _DTYPE_CODE[q.dtype], n, hq,
+            hkv, d, _ptr(cu_sb), batch,
             _ptr(cu), nb, topk, _ptr(forced), 0 if forced is None else forced.numel(),
             1 if force_self else 0, _ptr(topk_idx), _ptr(compact), _ptr(ws), ws.numel(),
-            _stream(dev)), "lsrm_select_blocks")
+            _stream(dev)), "lsrm_select_blocks" if pooled_k is None else "lsrm_select_blocks_pooled")
     return topk_idx, compact
 
 

@@ -127,6 +127,28 @@ def test_select_bitexact(cfg, n, heads):
     assert (compact == np.arange(nb)[None, :, None]).any(-1).all()
 
 
+
+@pytest.mark.parametrize("cfg,n,heads,hq", [(3, 16384, 4, 4), (2, 8192, 2, 8)])
+def test_select_with_pooled_keys_matches(cfg, n, heads, hq):
+    """lsrm_select_blocks_pooled (keys pooled once in fp32 by the caller)
+    selects exactly what lsrm_select_blocks does, and rounding those fp32
+    means gives the bf16 compressed keys block_mean_pool returns."""
+    w = W.config(cfg, n=n, heads=heads)
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(w.n, hq, w.d, generator=g).bfloat16().to(DEV)
+    k = torch.randn(w.n, w.hkv, w.d, generator=g).bfloat16().to(DEV)
+    cu_sb, cu = w.cu_seqblocks.to(DEV), w.cu_block_tokens.to(DEV)
+    a_idx, a_cmp = H.select_blocks(q, k, cu_sb, cu, w.topk, w.forced_blocks, w.force_self)
+    pk = H.block_mean_pool(k.view(w.n, -1), cu, torch.float32)
+    b_idx, b_cmp = H.select_blocks(q, k, cu_sb, cu, w.topk, w.forced_blocks, w.force_self,
+                                   pooled_k=pk)
+    assert torch.equal(a_idx, b_idx) and torch.equal(a_cmp, b_cmp)
+    ck = H.block_mean_pool(k.view(w.n, -1), cu)
+    assert torch.equal(pk.to(torch.bfloat16).view(torch.int16), ck.view(torch.int16))
+    with pytest.raises(ValueError):
+        H.select_blocks(q, k, cu_sb, cu, w.topk, w.forced_blocks, w.force_self,
+                        pooled_k=pk.bfloat16())
+
 def test_select_gqa_bitexact():
     w = W.config(2, n=4096)
     topk_idx, compact, ref = _select_case(w, hq=8, hkv=2)
