@@ -11,13 +11,16 @@
 //
 // One wave per (kv head, 32-token tile).  S^T = Ck Q^T on 32x32x16 MFMA:
 // the compressed keys (A operand, 16 contiguous bytes per lane) come
-// straight from global memory, one 32-key block ahead of their use; a lane
-// owns one query row and 16 of every 32 keys.  Each lane keeps a running
-// top-K list (K >= topk, a power of two) of its candidates in registers,
-// sorted by (score desc, id asc); at the end the two lanes of a row merge
-// their lists with a bitonic network and the chosen ids are sorted
-// ascending.  Tiles that straddle a batch boundary are processed once per
-// batch element they touch.
+// straight from global memory, two 32-key blocks ahead of their use; a lane
+// owns one query row and 16 of every 32 keys.  Each lane keeps a top-K list
+// (K >= topk, a power of two) of its candidates in registers, sorted by
+// (score desc, id asc) as 64-bit rank keys; with many keys per list entry a
+// first pass bounds the row's K-th score from below and the second keeps
+// only keys above the bound (in an LDS buffer, merged 16 at a time).  At the
+// end the two lanes of a row merge their lists with a bitonic network and
+// the chosen ids are sorted ascending.  Tiles that straddle a batch boundary
+// are processed once per batch element they touch; rows of tokens outside
+// every element are written as -1 rows.
 #include "common.h"
 
 namespace lsrm {
@@ -73,6 +76,12 @@ __global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
   const int64_t row = t0 + l32;
   const int64_t ck_stride = (int64_t)a.hkv * D;
 
+  // Every row of the output is written here: tokens outside every batch
+  // element get -1 rows, the loop below the rest.
+  if (hb == 0 && row < a.nq && (row < a.cu_q[0] || row >= a.cu_q[a.batch])) {
+    int32_t* dst = a.out + ((int64_t)h * a.nq + row) * a.topk;
+    for (int i = 0; i < a.topk; ++i) dst[i] = -1;
+  }
   for (int b = b0 < 0 ? 0 : b0; b <= b1 && b < a.batch; ++b) {
     const int64_t qs = a.cu_q[b], qe = a.cu_q[b + 1];
     if (qe <= t0 || qs > t_last) continue;

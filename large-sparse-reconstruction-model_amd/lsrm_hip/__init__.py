@@ -455,9 +455,9 @@ def block_score(q: torch.Tensor, compressed_k: torch.Tensor, lse: torch.Tensor, 
     cu_q = _i32(cu_seqlens_q)
     cu_c = _i32(compressed_cu_seqlens)
     batch = cu_q.numel() - 1
-    out = torch.full((hkv, nq, topk), -1, dtype=torch.int32, device=dev)
     if nq == 0 or batch <= 0:
-        return out
+        return torch.full((hkv, nq, topk), -1, dtype=torch.int32, device=dev)
+    out = torch.empty((hkv, nq, topk), dtype=torch.int32, device=dev)  # the kernel writes every row
     with torch.cuda.device(dev):
         _check(lib().lsrm_block_score(
             _ptr(q), _ptr(ck), _DTYPE_CODE[q.dtype], _ptr(lse), nq, hq, hkv, d, _ptr(cu_q),

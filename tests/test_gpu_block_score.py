@@ -184,3 +184,18 @@ def test_block_score_many_keys_all_tied():
     got = ops.get_block_score(q.to(DEV), ck.to(DEV), lse.to(DEV), 16, cu_q.to(DEV),
                               cu_c.to(DEV), None, None)
     assert (got.cpu() == torch.arange(16)).all()
+
+
+def test_block_score_tokens_outside_every_element():
+    # cu_seqlens_q starts at 10 and ends at 100 of 130 tokens: rows 0-9 and
+    # 100-129 belong to no batch element and come back as -1 rows
+    q, ck, cv, cu_q, cu_c = _case(6, [130], [70], 4, 2, 64)
+    cu_q = torch.tensor([10, 60, 100], dtype=torch.int32)
+    cu_c = torch.tensor([0, 40, 70], dtype=torch.int32)
+    lse = torch.randn(4, 130).abs() + 1.0
+    got = ops.get_block_score(q.to(DEV), ck.to(DEV), lse.to(DEV), 8, cu_q.to(DEV),
+                              cu_c.to(DEV), None, None).cpu()
+    assert (got[:, :10] == -1).all() and (got[:, 100:] == -1).all()
+    ref, scores = get_block_score_ref(q.float().numpy(), ck.float().numpy(), lse.numpy(), 8,
+                                      cu_q.numpy(), cu_c.numpy(), return_scores=True)
+    _check_selection(got, ref, scores, 8, cu_q, cu_c)
