@@ -194,6 +194,11 @@ int lsrm_sel_attn_fwd(const void* q, const void* k, const void* v, int dtype,
  * kernels.  The plan's work queues reset themselves at the end of each
  * launch, so a plan can be replayed any number of times on one stream.
  * lsrm_sel_attn_fwd == lsrm_sel_attn_plan + lsrm_sel_attn_fwd_run.
+ * Precondition of lsrm_sel_attn_bwd_run: the plan was built with
+ * backward != 0.  A plan built with backward == 0 carries no reverse maps;
+ * the backward kernels detect it (a marker word the backward build writes
+ * into the plan) and exit without reading or writing anything, leaving
+ * dq / dk / dv / delta as they were.
  * ---------------------------------------------------------------------- */
 int lsrm_sel_attn_plan(const int32_t* topk_idx, int64_t n_q, int64_t n_k,
                        int64_t hq, int64_t hkv, int64_t topk,

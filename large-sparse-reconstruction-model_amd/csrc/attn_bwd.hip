@@ -54,6 +54,8 @@ sel_attn_dq_kernel(AttnArgs a) {
   const int32_t* head_off = UNION ? a.plan.ghead_off : a.plan.head_off;
   const int2* tiles = UNION ? a.plan.gtiles : a.plan.tiles;
   int32_t* queue = a.plan.counter + (UNION ? 4 : 0);
+  // A plan built without its backward part: nothing here is valid to read.
+  if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC) return;
   const int total = head_off[a.hkv];
 
   int ld_key[G::LPW], ld_byte[G::LPW];
@@ -464,6 +466,8 @@ sel_attn_dkdv_kernel(AttnArgs a) {
   const int hb = lane >> 5, l32 = lane & 31;
   static_assert(KEY_CHUNK == 4 * 32, "four waves of 32 keys cover a chunk");
   const int kh = wv;  // this wave's 32 keys of the chunk; it covers all rows
+  // A plan built without its backward part: no reverse maps or key chunks.
+  if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC) return;
   const int n_items = a.items.n_items[0];
   const int total = n_items * a.hkv;
 

@@ -90,6 +90,10 @@ int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
     if (rc) return rc;
     rc = build_key_items(cu_blk, nb, nk, ws, w.items, st);
     if (rc) return rc;
+    if (ws.base && !ws.dry) {
+      rc = mark_backward_plan(w.plan.counter, st);
+      if (rc) return rc;
+    }
   }
   return LSRM_OK;
 }

@@ -17,11 +17,20 @@ struct TilePlan {
   int32_t* head_off;     // [hkv + 1] exclusive prefix of tile_count
   int32_t* counter;      // work counters, zeroed by the plan: [0], [2] run
                          // tiles (fwd / dq), [8..15], [3] key chunks (dK/dV,
-                         // one queue per XCD), [4], [6] grouped tiles
+                         // one queue per XCD), [4], [6] grouped tiles;
+                         // [PLAN_BWD_SLOT] = PLAN_BWD_MAGIC once the backward
+                         // part (reverse maps, key chunks) is built
   int2* gtiles;          // [hkv, n_q] grouped tiles (forward plans)
   int32_t* gtile_count;  // [hkv]
   int32_t* ghead_off;    // [hkv + 1]
 };
+
+// Marks a plan whose backward part was built: the backward kernels exit
+// without touching memory when the slot does not hold the magic word (a
+// forward-only plan in a workspace large enough for the backward).
+constexpr int PLAN_BWD_SLOT = 32;
+constexpr int32_t PLAN_BWD_MAGIC = 0x4c42574b;
+int mark_backward_plan(int32_t* counter, hipStream_t st);
 
 // CSR map block -> rows (tiles or queries) that selected it, per kv head.
 struct RevMap {

@@ -340,7 +340,18 @@ __global__ void plan_offsets_kernel(const int32_t* n_groups, int32_t* tile_count
       ghead_off[h + 1] = gacc;
     }
     for (int i = 0; i < 16; ++i) counter[i] = 0;
+    counter[PLAN_BWD_SLOT] = 0;  // set again by mark_backward_plan
   }
+}
+
+__global__ void mark_backward_plan_kernel(int32_t* counter) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) counter[PLAN_BWD_SLOT] = PLAN_BWD_MAGIC;
+}
+
+int mark_backward_plan(int32_t* counter, hipStream_t st) {
+  hipLaunchKernelGGL(mark_backward_plan_kernel, dim3(1), dim3(64), 0, st, counter);
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
 }
 
 int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,

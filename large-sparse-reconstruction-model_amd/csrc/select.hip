@@ -80,6 +80,21 @@ __global__ __launch_bounds__(256) void score_kernel(
   }
 }
 
+// A block outside every batch element selects nothing: its compact row and
+// the per-token rows of its tokens (clamped to [0, n_tokens)) become -1.
+// `first` / `step` spread the stores over the calling threads.
+__device__ inline void clear_block_rows(const int32_t* __restrict__ cu_blk, int64_t b,
+                                        int64_t n_tokens, int topk, int32_t* crow,
+                                        int32_t* head_rows, int first, int step) {
+  for (int j = first; j < topk; j += step) crow[j] = -1;
+  int64_t t0 = cu_blk[b], t1 = cu_blk[b + 1];
+  t0 = t0 < 0 ? 0 : (t0 > n_tokens ? n_tokens : t0);
+  t1 = t1 < t0 ? t0 : (t1 > n_tokens ? n_tokens : t1);
+  int32_t* dst = head_rows + t0 * topk;
+  const int64_t total = (t1 - t0) * topk;
+  for (int64_t i = first; i < total; i += step) dst[i] = -1;
+}
+
 __device__ inline bool sel_better(double s1, int i1, double s2, int i2) {
   return s1 > s2 || (s1 == s2 && i1 < i2);
 }
@@ -105,7 +120,8 @@ __global__ __launch_bounds__(256) void topk_kernel(
   const int64_t e = upper_index(cu_sb, 0, batch + 1, b);
   int32_t* crow = compact + ((int64_t)h * nb + b) * topk;
   if (e < 0 || e >= batch || b >= cu_sb[e + 1]) {
-    for (int j = tid; j < topk; j += 256) crow[j] = -1;
+    clear_block_rows(cu_blk, b, n_tokens, topk, crow, topk_idx + (int64_t)h * n_tokens * topk,
+                     tid, 256);
     return;
   }
   const int64_t cs = cu_sb[e];
@@ -222,7 +238,8 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(
   const int64_t e = upper_index(cu_sb, 0, batch + 1, b);
   int32_t* crow = compact + ((int64_t)h * nb + b) * topk;
   if (e < 0 || e >= batch || b >= cu_sb[e + 1]) {
-    for (int j = lane; j < topk; j += 64) crow[j] = -1;
+    clear_block_rows(cu_blk, b, n_tokens, topk, crow, topk_idx + (int64_t)h * n_tokens * topk,
+                     lane, 64);
     return;
   }
   const int64_t cs = cu_sb[e];
@@ -321,7 +338,8 @@ __global__ __launch_bounds__(256) void topk_split_kernel(
   const int64_t e = upper_index(cu_sb, 0, batch + 1, b);
   int32_t* crow = compact + ((int64_t)h * nb + b) * topk;
   if (e < 0 || e >= batch || b >= cu_sb[e + 1]) {
-    for (int j = tid; j < topk; j += 256) crow[j] = -1;
+    clear_block_rows(cu_blk, b, n_tokens, topk, crow, topk_idx + (int64_t)h * n_tokens * topk,
+                     tid, 256);
     return;
   }
   const int64_t cs = cu_sb[e];

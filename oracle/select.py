@@ -27,17 +27,43 @@ import numpy as np
 
 
 def block_scores_ref(pq: np.ndarray, pk: np.ndarray, h: int) -> np.ndarray:
-    """fp64 score matrix [nbq, nbk] for kv head h (sequential over g, d)."""
+    """fp64 score matrix [nbq, nbk] for kv head h (sequential over g, d).
+
+    Rows are computed in chunks (cache-sized temporaries); every element is
+    still the sum over g, then d, of exact fp64 products, in that order."""
     hq, hkv = pq.shape[1], pk.shape[1]
     g_n = hq // hkv
     d = pq.shape[2]
-    s = np.zeros((pq.shape[0], pk.shape[0]), dtype=np.float64)
-    for g in range(g_n):
-        a = pq[:, h * g_n + g, :].astype(np.float64)
-        kk = pk[:, h, :].astype(np.float64)
-        for dd in range(d):
-            s = s + a[:, dd, None] * kk[None, :, dd]
+    nbq, nbk = pq.shape[0], pk.shape[0]
+    kt = np.ascontiguousarray(pk[:, h, :].astype(np.float64).T)  # [d, nbk]
+    s = np.empty((nbq, nbk), dtype=np.float64)
+    chunk = max(1, (1 << 17) // max(nbk, 1))
+    for r0 in range(0, nbq, chunk):
+        r1 = min(nbq, r0 + chunk)
+        acc = np.zeros((r1 - r0, nbk), dtype=np.float64)
+        for g in range(g_n):
+            a = pq[r0:r1, h * g_n + g, :].astype(np.float64)
+            for dd in range(d):
+                acc += a[:, dd, None] * kt[dd][None, :]
+        s[r0:r1] = acc
     return s
+
+
+def _best_remaining(row: np.ndarray, chosen: list, need: int) -> list:
+    """The `need` best ids of `row` outside `chosen` by (score descending, id
+    ascending): every id scoring above the need-th best remaining score,
+    then the lowest ids among those equal to it."""
+    nbb = row.shape[0]
+    avail = np.ones(nbb, dtype=bool)
+    avail[chosen] = False
+    ids = np.nonzero(avail)[0]
+    vals = row[ids]
+    if need >= ids.shape[0]:
+        return ids.tolist()
+    thr = np.partition(vals, ids.shape[0] - need)[ids.shape[0] - need]
+    above = ids[vals > thr]
+    tied = ids[vals == thr]
+    return above.tolist() + tied[: need - above.shape[0]].tolist()
 
 
 def select_blocks_ref(pq: np.ndarray, pk: np.ndarray, cu_seqblocks: np.ndarray, topk: int,
@@ -55,7 +81,6 @@ def select_blocks_ref(pq: np.ndarray, pk: np.ndarray, cu_seqblocks: np.ndarray, 
         if nbb <= 0:
             continue
         kmax = min(topk, nbb)
-        idx = np.arange(nbb)
         for h in range(hkv):
             s = block_scores_ref(pq[cs:ce], pk[cs:ce], h)
             s = np.where(np.isnan(s), -np.inf, s)
@@ -67,14 +92,8 @@ def select_blocks_ref(pq: np.ndarray, pk: np.ndarray, cu_seqblocks: np.ndarray, 
                         break
                     if 0 <= f < nbb and f not in chosen:
                         chosen.append(f)
-                order = np.lexsort((idx, -s[b]))
-                taken = set(chosen)
-                for c in order:
-                    if len(chosen) >= kmax:
-                        break
-                    if int(c) not in taken:
-                        chosen.append(int(c))
-                        taken.add(int(c))
+                if len(chosen) < kmax:
+                    chosen += _best_remaining(s[b], chosen, kmax - len(chosen))
                 out[h, cs + b, :kmax] = np.sort(np.asarray(chosen, dtype=np.int32))
     return out
 

@@ -239,3 +239,48 @@ def test_bwd_head_dim_128(per_token):
         topk = random_topk(hkv, n, len(sizes), 5, gen, per_block_cu=cu)
     _run_case(q, k, v, topk, torch.tensor([0, len(sizes)], dtype=torch.int32), cu,
               torch.tensor([0, n], dtype=torch.int32), 1.0 / math.sqrt(d), do=do)
+
+
+def test_bwd_run_rejects_forward_only_plan():
+    # A forward-only plan (no reverse maps) in a workspace sized for the
+    # backward: lsrm_sel_attn_bwd_run's kernels see the missing backward
+    # marker and leave every output untouched; the same workspace replanned
+    # with backward=1 then gives the normal gradients.
+    w = W.config(4, n=2048, heads=2)
+    q, k, v, do = (t.to(DEV) for t in W.tensors(w, "cpu", with_grad_out=True))
+    gen = torch.Generator().manual_seed(3)
+    topk = _blocks_topk(w, w.topk, gen).to(DEV)
+    cu_sb, cu_blk, cu_q = (t.to(DEV) for t in (w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens))
+    o, lse = H.sel_attn_fwd(q, k, v, topk, cu_sb, cu_blk, cu_q, w.scale)
+    lib = H.lib()
+    nb, n = w.n_blocks, w.n
+    ws_n = lib.lsrm_sel_attn_workspace_size(n, n, w.hq, w.hkv, w.topk, nb, 1)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = [torch.full_like(q, 7.0), torch.full_like(k, 7.0), torch.full_like(v, 7.0),
+            torch.full((w.hq, n), 7.0, device=DEV)]
+
+    def bwd_run():
+        return lib.lsrm_sel_attn_bwd_run(
+            do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+            lse.data_ptr(), H.BF16, n, n, w.hq, w.hkv, w.d, topk.data_ptr(), w.topk,
+            cu_sb.data_ptr(), cu_blk.data_ptr(), nb, cu_q.data_ptr(), 1, w.scale,
+            *[t.data_ptr() for t in outs], ws.data_ptr(), ws_n, stream)
+
+    for backward in (1, 0):  # a backward plan first, then a forward-only one over it
+        assert lib.lsrm_sel_attn_plan(topk.data_ptr(), n, n, w.hq, w.hkv, w.topk,
+                                      cu_sb.data_ptr(), cu_blk.data_ptr(), nb, cu_q.data_ptr(),
+                                      1, backward, ws.data_ptr(), ws_n, stream) == 0
+    assert bwd_run() == 0
+    torch.cuda.synchronize()
+    for t in outs:
+        assert (t == 7.0).all()
+    assert lib.lsrm_sel_attn_plan(topk.data_ptr(), n, n, w.hq, w.hkv, w.topk, cu_sb.data_ptr(),
+                                  cu_blk.data_ptr(), nb, cu_q.data_ptr(), 1, 1, ws.data_ptr(),
+                                  ws_n, stream) == 0
+    outs[1].zero_()
+    outs[2].zero_()
+    assert bwd_run() == 0
+    dq, dk, dv, delta = H.sel_attn_bwd(do, q, k, v, o, lse, topk, cu_sb, cu_blk, cu_q, w.scale)
+    for a, b in zip(outs, (dq, dk, dv, delta)):
+        assert torch.equal(a, b)

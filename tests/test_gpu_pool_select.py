@@ -226,3 +226,33 @@ def test_select_tokens_outside_blocks_get_empty_rows():
     ti = topk_idx.cpu().numpy()
     assert (ti[:, :100] == -1).all() and (ti[:, n - 50:] == -1).all()
     np.testing.assert_array_equal(ti, expand_per_token(ref, cu.numpy(), n))
+
+
+@pytest.mark.parametrize("n_blocks,topk", [(300, 8), (2100, 16), (2100, 80)])
+def test_select_blocks_outside_every_batch_element(n_blocks, topk):
+    # cu_seqblocks[-1] < n_blocks: the trailing blocks belong to no batch
+    # element, so their tokens' rows must be -1 (the output is allocated
+    # uninitialised, over memory pre-filled with valid-looking ids).  The
+    # three sizes take the wave, split and workgroup top-k kernels.
+    rng = np.random.default_rng(n_blocks + topk)
+    sizes = rng.integers(1, 6, size=n_blocks)
+    cu_np = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    n = int(cu_np[-1])
+    inside = (n_blocks * 2) // 3
+    cu_sb = torch.tensor([0, inside // 2, inside], dtype=torch.int32)
+    g = torch.Generator().manual_seed(3)
+    hq, hkv, d = 4, 2, 64
+    q = torch.randn(n, hq, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+    for _ in range(2):
+        junk = torch.full((hkv, n, topk), 3, dtype=torch.int32, device=DEV)
+        junk2 = torch.full((hkv, n_blocks, topk), 3, dtype=torch.int32, device=DEV)
+        del junk, junk2
+        topk_idx, compact = H.select_blocks(q.to(DEV), k.to(DEV), cu_sb.to(DEV),
+                                            torch.from_numpy(cu_np).to(DEV), topk, [], True)
+        pq = block_mean_pool_ref(_f32(q).reshape(n, -1), cu_np).reshape(-1, hq, d)
+        pk = block_mean_pool_ref(_f32(k).reshape(n, -1), cu_np).reshape(-1, hkv, d)
+        ref = select_blocks_ref(pq, pk, cu_sb.numpy(), topk, [], True)
+        np.testing.assert_array_equal(compact.cpu().numpy(), ref)
+        np.testing.assert_array_equal(topk_idx.cpu().numpy(), expand_per_token(ref, cu_np, n))
+        assert (topk_idx[:, int(cu_np[inside]):].cpu() == -1).all()

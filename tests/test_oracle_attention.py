@@ -23,7 +23,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from oracle.attention import LOG2E, attended_pairs, sel_attn_ref
+from oracle.attention import LOG2E, attended_pairs, sel_attn_bwd_ref, sel_attn_ref
 
 
 def _problem(n=96, hq=4, hkv=2, d=16, sizes=(10, 30, 5, 21, 30), seed=0, dtype=torch.float64):
@@ -123,3 +123,39 @@ def test_backward_gradcheck_fp64():
     k.requires_grad_()
     v.requires_grad_()
     assert torch.autograd.gradcheck(fn, (q, k, v), eps=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("case", ["gqa_batches", "duplicates_empty", "per_token"])
+def test_explicit_backward_equals_autograd(case):
+    # sel_attn_bwd_ref (run by run, no graph) against torch.autograd through
+    # sel_attn_ref, in fp64: GQA over two batch elements with padding and
+    # out-of-range ids; a block listed twice plus empty rows; and per-token
+    # rows (every query its own run).
+    q, k, v, cu = _problem(seed=11)
+    g = torch.Generator().manual_seed(12)
+    do = torch.randn(q.shape, generator=g, dtype=q.dtype)
+    cu_sb = torch.tensor([0, 2, 5])
+    cu_q = torch.tensor([0, 40, 96])
+    topk = torch.full((2, 96, 4), -1, dtype=torch.int32)
+    if case == "gqa_batches":
+        topk[:, :40, 0], topk[:, :40, 1] = 0, 1
+        topk[:, 40:, 0], topk[:, 40:, 1], topk[:, 40:, 2] = 2, 0, 1
+        topk[1, 60:70, 3] = 9              # out of range for batch 1 -> ignored
+    elif case == "duplicates_empty":
+        topk[:, :, 0], topk[:, :, 1] = 1, 1
+        topk[:, 20:25] = -1
+        topk[:, 50:80, 2] = 2
+    else:
+        topk = torch.stack([torch.stack([torch.randperm(2, generator=g) if i < 40 else
+                                         torch.randperm(3, generator=g)[:2]
+                                         for i in range(96)]) for _ in range(2)]).to(torch.int32)
+    meta = (topk, cu_sb, cu, cu_q)
+    qa, ka, va = (t.clone().requires_grad_() for t in (q, k, v))
+    o, _ = sel_attn_ref(qa, ka, va, *meta, 0.3)
+    o.backward(do)
+    dq, dk, dv, delta = sel_attn_bwd_ref(q, k, v, do, *meta, 0.3)
+    torch.testing.assert_close(dq, qa.grad, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(dk, ka.grad, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(dv, va.grad, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(delta, (o.detach() * do).sum(-1).transpose(0, 1),
+                               rtol=1e-10, atol=1e-12)

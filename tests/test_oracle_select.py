@@ -141,3 +141,32 @@ def test_selection_from_pooled_tokens_end_to_end():
     pk = block_mean_pool_ref(k, cu).reshape(-1, 2, 4)
     out = select_blocks_ref(pq, pk, np.array([0, 10]), 4, [9], True)
     np.testing.assert_array_equal(out, _brute(pq, pk, [0, 10], 4, [9], True))
+
+
+@pytest.mark.parametrize("seed,topk,forced", [(0, 3, []), (1, 5, [2]), (2, 4, [7, 0])])
+def test_brute_force_many_ties(seed, topk, forced):
+    # Small-integer pooled values make many scores equal, so the top-k cut
+    # falls inside groups of tied scores (lowest ids must win) and forced ids
+    # can sit inside or outside a tied group.
+    rng = np.random.default_rng(100 + seed)
+    nb, d = 11, 3
+    pq = rng.integers(-1, 2, size=(nb, 2, d)).astype(np.float32)
+    pk = rng.integers(-1, 2, size=(nb, 1, d)).astype(np.float32)
+    cu_sb = np.array([0, nb])
+    out = select_blocks_ref(pq, pk, cu_sb, topk, forced, True)
+    np.testing.assert_array_equal(out, _brute(pq, pk, cu_sb, topk, forced, True))
+    out = select_blocks_ref(pq, pk, cu_sb, topk, forced, False)
+    np.testing.assert_array_equal(out, _brute(pq, pk, cu_sb, topk, forced, False))
+
+
+def test_brute_force_nan_scores():
+    # NaN pooled keys rank below every finite score; among themselves by id:
+    # 5 finite ids fill five of six slots, the sixth goes to NaN id 1.
+    rng = np.random.default_rng(5)
+    nb = 8
+    pq = rng.standard_normal((nb, 1, 4)).astype(np.float32)
+    pk = rng.standard_normal((nb, 1, 4)).astype(np.float32)
+    pk[[1, 4, 6], 0, 2] = np.nan
+    out = select_blocks_ref(pq, pk, np.array([0, nb]), 6, [], False)
+    for b in range(nb):
+        assert out[0, b].tolist() == [0, 1, 2, 3, 5, 7]
