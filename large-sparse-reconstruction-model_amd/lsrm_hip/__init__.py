@@ -614,3 +614,7 @@ def gate_merge_bwd(dout: torch.Tensor, gate: torch.Tensor, o_cmp: torch.Tensor,
             _ptr(d_gate), _ptr(d_br[0]), _ptr(d_br[1]),
             _ptr(d_br[2]) if o_win is not None else None, _stream(dev)), "lsrm_gate_merge_bwd")
     return d_gate, d_br[0], d_br[1], (d_br[2] if o_win is not None else None)
+
+
+# The functions above registered as torch operators (torch.ops.lsrm_hip.*).
+from . import torch_ops  # noqa: E402,F401

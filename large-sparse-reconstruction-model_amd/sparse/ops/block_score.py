@@ -3,7 +3,8 @@
 get_block_score keeps the reference signature and output layout
 ([num_kv_heads, total_q, topk] int32, batch-local compressed-key ids
 ascending, -1 padded) and runs on the gfx950 kernel lsrm_block_score (one
-launch, no host synchronisation; the reference loops over batch elements and
+launch through the operator torch.ops.lsrm_hip.block_score, no host
+synchronisation; the reference loops over batch elements and
 kv heads with .item() calls and a dense [q_len, n_compressed] score matrix
 per head).  seqlens_q / compressed_seqlens are accepted and unused, as the
 lengths follow from the cumulative arrays.
@@ -15,7 +16,7 @@ import math
 
 import torch
 
-import lsrm_hip as _hip
+import lsrm_hip  # noqa: F401  (registers torch.ops.lsrm_hip)
 
 
 def get_block_score(
@@ -41,5 +42,5 @@ def get_block_score(
     """
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(q.shape[-1])
-    return _hip.block_score(q, compressed_k, lse, topk, cu_seqlens_q, compressed_cu_seqlens,
-                            sm_scale)
+    return torch.ops.lsrm_hip.block_score(q, compressed_k, lse, int(topk), cu_seqlens_q,
+                                          compressed_cu_seqlens, float(sm_scale))

@@ -27,5 +27,5 @@ def sparse_window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     n = q.shape[0]
     cu_seqblocks = torch.tensor([0, nb], dtype=torch.int32, device=dev)
     cu_seqlens = torch.tensor([0, n], dtype=torch.int32, device=dev)
-    ids = _hip.block_ids(cu_seqblocks, cu, n, k.shape[1])
+    ids = torch.ops.lsrm_hip.block_ids(cu_seqblocks, cu, n, k.shape[1])
     return native_sparse_attend(q, k, v, ids, cu_seqblocks, cu, cu_seqlens, cu_seqlens)

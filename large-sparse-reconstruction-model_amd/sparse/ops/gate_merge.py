@@ -7,7 +7,8 @@ Replaces the expression of sparse/module/spatial_sparse_attention.py:256-269
     attn_output = gate[:, 0:H] * compressed + gate[:, H:2H] * selection
                   (+ gate[:, 2H:] * window)
 
-with one streaming HIP kernel each way (lsrm_gate_merge / _bwd) instead of
+with one streaming HIP kernel each way (lsrm_gate_merge / _bwd, operators
+torch.ops.lsrm_hip.gate_merge / gate_merge_bwd) instead of
 five or eight PyTorch elementwise kernels and their intermediates.  Results
 are bit-identical to PyTorch's evaluation of the expression in the tensors'
 dtype (every product and sum rounded to the dtype, left to right).
@@ -19,7 +20,7 @@ from typing import Optional
 
 import torch
 
-import lsrm_hip as _hip
+import lsrm_hip  # noqa: F401  (registers torch.ops.lsrm_hip)
 
 
 class GateMerge(torch.autograd.Function):
@@ -27,14 +28,14 @@ class GateMerge(torch.autograd.Function):
     def forward(ctx, gate, o_cmp, o_slc, o_win):
         ctx.save_for_backward(gate, o_cmp, o_slc, o_win)
         ctx.has_win = o_win is not None
-        return _hip.gate_merge(gate, o_cmp, o_slc, o_win)
+        return torch.ops.lsrm_hip.gate_merge(gate, o_cmp, o_slc, o_win)
 
     @staticmethod
     def backward(ctx, dout):
         gate, o_cmp, o_slc, o_win = ctx.saved_tensors
-        d_gate, d_cmp, d_slc, d_win = _hip.gate_merge_bwd(
-            dout, gate, o_cmp, o_slc, o_win if ctx.has_win else None)
-        return d_gate, d_cmp, d_slc, d_win
+        grads = torch.ops.lsrm_hip.gate_merge_bwd(
+            dout.contiguous(), gate, o_cmp, o_slc, o_win if ctx.has_win else None)
+        return grads[0], grads[1], grads[2], (grads[3] if ctx.has_win else None)
 
 
 def gate_merge(gate: torch.Tensor, compressed_attn_output: torch.Tensor,

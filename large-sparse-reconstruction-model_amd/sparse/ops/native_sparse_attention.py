@@ -5,7 +5,8 @@ sparse/ops/triton_native_sparse_attention_impl_kvcentric.py:1272-1435
 (set_variant, NSA, native_sparse_attend) and
 sparse/ops/triton_native_sparse_attention.py:17-41
 (spatial_selection_attention); the kernels behind them are the HIP kernels of
-liblsrm_hip.so (lsrm_sel_attn_fwd / lsrm_sel_attn_bwd).
+liblsrm_hip.so (lsrm_sel_attn_fwd / lsrm_sel_attn_bwd), reached through the
+registered operators torch.ops.lsrm_hip.sel_attn_fwd / sel_attn_bwd.
 """
 
 from __future__ import annotations
@@ -81,8 +82,9 @@ class NSA(torch.autograd.Function):
 
         _check_meta(q, k, topk_idx, cu_seqblocks, cu_block_include_tokens, cu_seqlens_q,
                     cu_seqlens_k)
-        o, lse = _hip.sel_attn_fwd(q, k, v, topk_idx, cu_seqblocks, cu_block_include_tokens,
-                                   cu_seqlens_q, softmax_scale)
+        o, lse = torch.ops.lsrm_hip.sel_attn_fwd(q, k, v, topk_idx, cu_seqblocks,
+                                                 cu_block_include_tokens, cu_seqlens_q,
+                                                 float(softmax_scale))
         ctx.save_for_backward(q, k, v, o, lse, cu_seqlens_q, cu_seqlens_k, topk_idx,
                               cu_seqblocks, cu_block_include_tokens)
         ctx.softmax_scale = softmax_scale
@@ -96,9 +98,9 @@ class NSA(torch.autograd.Function):
         do = do.contiguous()
         if do.dtype != q.dtype:
             do = do.to(q.dtype)
-        dq, dk, dv, _delta = _hip.sel_attn_bwd(
+        dq, dk, dv, _delta = torch.ops.lsrm_hip.sel_attn_bwd(
             do, q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_include_tokens,
-            cu_seqlens_q, ctx.softmax_scale)
+            cu_seqlens_q, float(ctx.softmax_scale))
         return dq, dk, dv, None, None, None, None, None, None
 
 

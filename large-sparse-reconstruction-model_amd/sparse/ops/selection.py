@@ -16,7 +16,7 @@ from typing import Optional, Sequence
 
 import torch
 
-import lsrm_hip as _hip
+import lsrm_hip  # noqa: F401  (registers torch.ops.lsrm_hip)
 
 
 def select_blocks(q: torch.Tensor, k: torch.Tensor, cu_seqblocks: torch.Tensor,
@@ -25,8 +25,9 @@ def select_blocks(q: torch.Tensor, k: torch.Tensor, cu_seqblocks: torch.Tensor,
                   return_compact: bool = False):
     """q [N, Hq, D], k [N, Hkv, D] -> block_topk [Hkv, N, topk] int32
     (and the per-block rows [Hkv, n_blocks, topk] when return_compact)."""
-    topk_idx, compact = _hip.select_blocks(q, k, cu_seqblocks, cu_block_include_tokens, topk,
-                                           forced_blocks, force_self)
+    topk_idx, compact = torch.ops.lsrm_hip.select_blocks(
+        q, k, cu_seqblocks, cu_block_include_tokens, int(topk),
+        [int(b) for b in (forced_blocks or [])], bool(force_self), None)
     if return_compact:
         return topk_idx, compact
     return topk_idx
