@@ -60,7 +60,9 @@ enum lsrm_status {
   LSRM_ERR_INVALID_ARG = 1, /* null pointer, negative size, bad combination */
   LSRM_ERR_UNSUPPORTED = 2, /* dtype / head_dim / group size not built      */
   LSRM_ERR_WORKSPACE = 3,   /* workspace smaller than *_workspace_size()    */
-  LSRM_ERR_LAUNCH = 4       /* a HIP launch or device query failed          */
+  LSRM_ERR_LAUNCH = 4,      /* a HIP launch or device query failed          */
+  LSRM_ERR_SCRATCH = 5      /* input larger than the fixed scratch of an
+                               allocation-free entry point                  */
 };
 
 /* Bits of the flag word written by lsrm_sel_attn_validate. */
@@ -96,6 +98,22 @@ int lsrm_block_mean_pool(const void* x, int x_dtype, int64_t n_tokens,
                          int64_t channels, const int32_t* cu_block_tokens,
                          int64_t n_blocks, void* out, int out_dtype,
                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Allocation-free variant of lsrm_block_mean_pool (no counterpart in the
+ * reference): for callers that cannot allocate device memory or pass a
+ * workspace (code under HIP graph capture, tight serving loops).  Same
+ * arguments and results without the workspace; the kernels use a scratch
+ * array of LSRM_POOL_SCRATCH_BYTES that the library holds in device memory
+ * on every GPU it runs on until the process ends.  Inputs whose workspace
+ * (lsrm_block_mean_pool_workspace_size) exceeds it return LSRM_ERR_SCRATCH
+ * without launching anything.  Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (different streams, or host
+ * threads without ordering) race and must be serialised by the caller. */
+#define LSRM_POOL_SCRATCH_BYTES (64ull << 20)
+int lsrm_block_mean_pool_noalloc(const void* x, int x_dtype, int64_t n_tokens,
+                                 int64_t channels, const int32_t* cu_block_tokens,
+                                 int64_t n_blocks, void* out, int out_dtype,
+                                 void* stream);
 
 /* ------------------------------------------------------------------------
  * Per-query-block top-k block selection (self attention: queries and keys

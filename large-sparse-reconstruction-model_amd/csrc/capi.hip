@@ -130,6 +130,8 @@ extern "C" const char* lsrm_status_string(int status) {
     case LSRM_ERR_UNSUPPORTED: return "unsupported dtype, head_dim, group size or size";
     case LSRM_ERR_WORKSPACE: return "workspace too small";
     case LSRM_ERR_LAUNCH: return "HIP launch or device query failed";
+    case LSRM_ERR_SCRATCH:
+      return "input larger than the fixed scratch of the allocation-free entry point";
     default: return "unknown status";
   }
 }

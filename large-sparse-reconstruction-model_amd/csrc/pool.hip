@@ -16,6 +16,8 @@
 // Every add is sequential, so the result is a fixed function of the input
 // (the contract the CPU oracle restates bit for bit).  Input rows are read
 // exactly once, with nontemporal loads (measured +8% on the cfg3 K tensor).
+#include <mutex>
+
 #include "common.h"
 
 namespace lsrm {
@@ -425,6 +427,37 @@ int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
 
 }  // namespace lsrm
 
+// Scratch of lsrm_block_mean_pool_noalloc: the piece partials and the
+// chunk -> first-block table, laid out as in a caller's workspace.  Every
+// GPU holds its own copy; host code reaches it only through the per-device
+// address from hipGetSymbolAddress (the array's name on the host is not a
+// device address).  Nothing in it needs to start at zero: every partial and
+// table entry a launch reads was written earlier in the same launch.
+static __device__ __align__(256) char scratch[LSRM_POOL_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {nullptr};
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+int scratch_address(void** ptr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return LSRM_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p)
+      return LSRM_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return LSRM_OK;
+}
+
+}  // namespace
+
 extern "C" size_t lsrm_block_mean_pool_workspace_size(int64_t n_tokens,
                                                       int64_t channels,
                                                       int64_t n_blocks) {
@@ -454,4 +487,20 @@ extern "C" int lsrm_block_mean_pool(const void* x, int x_dtype,
   return lsrm::launch_block_mean_pool(x, x_dtype, n_tokens, channels,
                                       cu_block_tokens, n_blocks, out, out_dtype,
                                       partial, first, (hipStream_t)stream);
+}
+
+extern "C" int lsrm_block_mean_pool_noalloc(const void* x, int x_dtype, int64_t n_tokens,
+                                            int64_t channels,
+                                            const int32_t* cu_block_tokens,
+                                            int64_t n_blocks, void* out, int out_dtype,
+                                            void* stream) {
+  if (n_tokens < 0 || channels <= 0 || n_blocks < 0) return LSRM_ERR_INVALID_ARG;
+  if (lsrm_block_mean_pool_workspace_size(n_tokens, channels, n_blocks) >
+      LSRM_POOL_SCRATCH_BYTES)
+    return LSRM_ERR_SCRATCH;
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return lsrm_block_mean_pool(x, x_dtype, n_tokens, channels, cu_block_tokens, n_blocks, out,
+                              out_dtype, ws, LSRM_POOL_SCRATCH_BYTES, stream);
 }

@@ -44,6 +44,7 @@ _SIGNATURES = {
     "lsrm_version": (_I, []),
     "lsrm_block_mean_pool_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "lsrm_block_mean_pool": (_I, [_P, _I, _I64, _I64, _P, _I64, _P, _I, _P, _SZ, _P]),
+    "lsrm_block_mean_pool_noalloc": (_I, [_P, _I, _I64, _I64, _P, _I64, _P, _I, _P]),
     "lsrm_select_blocks_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "lsrm_select_blocks": (
         _I,
