@@ -30,7 +30,14 @@
  *                             the learned per-token block selection)
  *   lsrm_volume_points        misc/sparse_utils.py:644-650 (from_volcoords_to_points)
  *   lsrm_nearest_blocks       misc/sparse_utils.py:1219-1273 (the 3D-aware
- *                             per-token selection of build_volume_to_volume_attn)
+ *                             per-token selection of build_volume_to_volume_attn;
+ *                             with image points as queries, 960-980 of
+ *                             build_image_to_volume_attn)
+ *   lsrm_image_points         misc/sparse_utils.py:653-688 (from_imcoords_to_points)
+ *   lsrm_image_block_rank     misc/sparse_utils.py:690-898, 991-1200 (the 3D-aware
+ *                             per-token selection of build_image_to_image_attn and
+ *                             build_volume_to_image_attn) and 16-57
+ *                             (compute_block_topk_dist_chunked)
  *   lsrm_block_separation     misc/sparse_utils.py:592-641 (compute_block_separation)
  *   lsrm_gate_merge(_bwd)     sparse/module/spatial_sparse_attention.py:256-269
  *                             (the gated sum of the attention branches)
@@ -343,6 +350,53 @@ int lsrm_nearest_blocks(const float* points, const float* centroids,
                         const int32_t* cu_seqlens, const int32_t* cu_seqblocks,
                         int64_t batch, int64_t n_tokens, int64_t topk, int64_t hkv,
                         int32_t* block_topk, void* stream);
+
+/* ------------------------------------------------------------------------
+ * 3D-aware per-token selection on the image side.
+ * lsrm_image_points: imcoords [n_tokens, 4] int32 (batch, image, patch row,
+ *   patch column), surface_points [batch, n_images, dense_res, dense_res, 3]
+ *   fp32, masks [batch, n_images, dense_res, dense_res] fp32 -> points
+ *   [n_tokens, 3] fp32: the point of the token's patch (dense_res /
+ *   patch_res pixels a side) with the largest mask value, the first in
+ *   (row, column) order among equal maxima; NaN for coordinates outside the
+ *   arrays.  Replaces misc/sparse_utils.py:653-688 (from_imcoords_to_points).
+ * lsrm_image_block_rank: for every query point (qpoints [n_q, 3] fp32,
+ *   batch elements by cu_seqlens_q [batch + 1]) and every image m of its
+ *   batch element b, with the per-image records
+ *     cameras [batch, n_images, 18] fp32: rows 0..2 of the world-to-camera
+ *       matrix (12), tan(fov / 2), crop flag, origin_size - 1, crop x0,
+ *       crop y0, crop_size - 1;
+ *     image_meta [batch, n_images, 4] int32: kept blocks of the image, their
+ *       offset in kept_blocks, the image's first candidate column, the
+ *       image's first block id (kept blocks of the earlier images);
+ *     kept_blocks: row-major block numbers (blocks_w blocks a row) of the
+ *       kept blocks, image after image;
+ *   projects the point into the image, takes the win nearest kept block
+ *   centres (fp32 squared distance in block units, ties to the lower kept
+ *   number), measures each candidate's smallest 3D distance to its valid
+ *   dense points (ibs x ibs points of surface_points under the block,
+ *   valid where dense_masks > 0.2, an invalid point counting max_dist),
+ *   and writes the min(topk, candidates of b) nearest candidates (ties to
+ *   the earlier column; cols_per_batch[b] columns) in column order as block
+ *   ids, -1 padded, identically for hkv heads: block_topk [hkv, n_q, topk]
+ *   int32.  win <= 16, cols (the widest batch element) <= 1024.
+ * Replaces the use_3d_aware_attn branches of misc/sparse_utils.py:690-898
+ * (build_image_to_image_attn) and 991-1200 (build_volume_to_image_attn),
+ * with compute_block_topk_dist_chunked (16-57).
+ * ---------------------------------------------------------------------- */
+int lsrm_image_points(const int32_t* imcoords, int64_t n_tokens,
+                      const float* surface_points, const float* masks, int64_t batch,
+                      int64_t n_images, int64_t dense_res, int64_t patch_res, float* points,
+                      void* stream);
+size_t lsrm_image_block_rank_workspace_size(int64_t n_q, int64_t cols);
+int lsrm_image_block_rank(const float* qpoints, int64_t n_q, const int32_t* cu_seqlens_q,
+                          int64_t batch, int64_t n_images, const float* cameras,
+                          const int32_t* image_meta, const int32_t* kept_blocks,
+                          const int32_t* cols_per_batch, int64_t cols, int64_t blocks_w,
+                          int64_t dense_res, int64_t ibs, const float* surface_points,
+                          const float* dense_masks, int64_t win, int64_t topk,
+                          float max_dist, int64_t hkv, int32_t* block_topk,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Block separation (compute_block_separation).

@@ -89,6 +89,11 @@ _SIGNATURES = {
         _I, [_P, _P, _I, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _F, _P, _P]),
     "lsrm_volume_points": (_I, [_P, _I64, _I64, _F, _P, _P]),
     "lsrm_nearest_blocks": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
+    "lsrm_image_points": (_I, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
+    "lsrm_image_block_rank_workspace_size": (_SZ, [_I64, _I64]),
+    "lsrm_image_block_rank": (
+        _I, [_P, _I64, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64,
+             _I64, _F, _I64, _P, _P, _SZ, _P]),
     "lsrm_block_separation_workspace_size": (_SZ, [_I64, _I, _P, _P]),
     "lsrm_block_separation": (_I, [_P, _I64, _I, _P, _P, _I64, _P, _P, _P, _P, _SZ, _P]),
     "lsrm_block_sort_workspace_size": (_SZ, [_I64]),
@@ -507,6 +512,96 @@ def nearest_blocks(points: torch.Tensor, cu_block_tokens: torch.Tensor,
         _check(lib().lsrm_nearest_blocks(_ptr(points), _ptr(centroids), _ptr(cu_q),
                                          _ptr(cu_sb), batch, n, topk, num_kv_heads,
                                          _ptr(out), _stream(dev)), "lsrm_nearest_blocks")
+    return out
+
+
+def nearest_blocks_to(qpoints: torch.Tensor, key_points: torch.Tensor,
+                      cu_block_tokens: torch.Tensor, cu_seqblocks: torch.Tensor,
+                      cu_seqlens_q: torch.Tensor, topk: int,
+                      num_kv_heads: int = 2) -> torch.Tensor:
+    """Per query point, the nearest block centroids of another token set
+    (centroid = block mean of key_points) -> [num_kv_heads, Nq, topk] int32
+    (batch-local ids ascending, -1 padded)."""
+    for t in (qpoints, key_points):
+        if t.dim() != 2 or t.shape[1] != 3 or t.dtype != torch.float32:
+            raise ValueError("points must be [N, 3] float32")
+    if topk <= 0:
+        raise ValueError("topk must be positive")
+    dev = _dev_check(qpoints, key_points, cu_block_tokens, cu_seqblocks, cu_seqlens_q)
+    qpoints = qpoints.contiguous()
+    n = qpoints.shape[0]
+    cu_q = _i32(cu_seqlens_q)
+    cu_sb = _i32(cu_seqblocks)
+    centroids = block_mean_pool(key_points.contiguous(), cu_block_tokens, torch.float32)
+    out = torch.full((num_kv_heads, n, topk), -1, dtype=torch.int32, device=dev)
+    batch = cu_q.numel() - 1
+    if n == 0 or batch <= 0:
+        return out
+    with torch.cuda.device(dev):
+        _check(lib().lsrm_nearest_blocks(_ptr(qpoints), _ptr(centroids), _ptr(cu_q), _ptr(cu_sb),
+                                         batch, n, topk, num_kv_heads, _ptr(out), _stream(dev)),
+               "lsrm_nearest_blocks")
+    return out
+
+
+def image_points(imcoords: torch.Tensor, surface_points: torch.Tensor, masks: torch.Tensor,
+                 patch_res: int) -> torch.Tensor:
+    """from_imcoords_to_points: imcoords [N, 4] (batch, image, patch row,
+    patch column), surface_points [B, M, S, S, 3] fp32, masks B*M*S*S values
+    -> [N, 3] fp32 points (NaN for coordinates outside the arrays)."""
+    if imcoords.dim() != 2 or imcoords.shape[1] != 4:
+        raise ValueError("imcoords must be [N, 4]")
+    if surface_points.dim() != 5 or surface_points.shape[-1] != 3 or \
+            surface_points.shape[2] != surface_points.shape[3]:
+        raise ValueError("surface_points must be [B, M, S, S, 3]")
+    b, m, s = surface_points.shape[:3]
+    if masks.numel() != b * m * s * s:
+        raise ValueError("masks must hold B * M * S * S values")
+    dev = _dev_check(imcoords, surface_points, masks)
+    c = _i32(imcoords)
+    sp = surface_points.contiguous().float()
+    mk = masks.contiguous().float()
+    out = torch.empty(c.shape[0], 3, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib().lsrm_image_points(_ptr(c), c.shape[0], _ptr(sp), _ptr(mk), b, m, s,
+                                       int(patch_res), _ptr(out), _stream(dev)),
+               "lsrm_image_points")
+    return out
+
+
+def image_block_rank(qpoints: torch.Tensor, cu_seqlens_q: torch.Tensor, cameras: torch.Tensor,
+                     image_meta: torch.Tensor, kept_blocks: torch.Tensor,
+                     cols_per_batch: torch.Tensor, cols: int, blocks_w: int, ibs: int,
+                     surface_points: torch.Tensor, dense_masks: torch.Tensor, win: int,
+                     topk: int, max_dist: float, num_kv_heads: int = 2) -> torch.Tensor:
+    """The per-token image-block rows of build_image_to_image_attn /
+    build_volume_to_image_attn from the per-image records the sparse.builders
+    host code prepares (cameras [B, M, 18] fp32, image_meta [B, M, 4] int32)
+    -> [num_kv_heads, Nq, topk] int32 (position order, -1 padded)."""
+    dev = _dev_check(qpoints, cu_seqlens_q, cameras, image_meta, cols_per_batch,
+                     surface_points, dense_masks)
+    b, m, s = surface_points.shape[:3]
+    n = qpoints.shape[0]
+    out = torch.full((num_kv_heads, n, topk), -1, dtype=torch.int32, device=dev)
+    if n == 0:
+        return out
+    kept = _i32(kept_blocks) if kept_blocks.numel() else torch.zeros(1, dtype=torch.int32,
+                                                                       device=dev)
+    qp = qpoints.contiguous().float()
+    sp = surface_points.contiguous().float()
+    dm = dense_masks.contiguous().float()
+    cam = cameras.contiguous().float()
+    meta = _i32(image_meta)
+    cpb = _i32(cols_per_batch)
+    cu_q = _i32(cu_seqlens_q)
+    with torch.cuda.device(dev):
+        ws_n = lib().lsrm_image_block_rank_workspace_size(n, int(cols))
+        ws = _workspace(ws_n, dev)
+        _check(lib().lsrm_image_block_rank(
+            _ptr(qp), n, _ptr(cu_q), cu_q.numel() - 1, m, _ptr(cam), _ptr(meta), _ptr(kept),
+            _ptr(cpb), int(cols), int(blocks_w), s, int(ibs), _ptr(sp), _ptr(dm), int(win),
+            int(topk), float(max_dist), num_kv_heads, _ptr(out), _ptr(ws), ws.numel(),
+            _stream(dev)), "lsrm_image_block_rank")
     return out
 
 

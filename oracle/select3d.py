@@ -46,11 +46,21 @@ def nearest_blocks_ref(points: np.ndarray, cu_block_tokens: np.ndarray,
                        cu_seqblocks: np.ndarray, cu_seqlens: np.ndarray, topk: int,
                        chunk: int = 4096) -> np.ndarray:
     """points [N, 3] fp32 -> [N, topk] int32 batch-local block ids."""
-    pts = np.asarray(points, dtype=np.float32)
+    return nearest_blocks_to_ref(points, points, cu_block_tokens, cu_seqblocks, cu_seqlens, topk,
+                                 chunk)
+
+
+def nearest_blocks_to_ref(qpoints: np.ndarray, key_points: np.ndarray,
+                          cu_block_tokens: np.ndarray, cu_seqblocks: np.ndarray,
+                          cu_seqlens_q: np.ndarray, topk: int, chunk: int = 4096) -> np.ndarray:
+    """Query points [Nq, 3] against the block centroids of other key points
+    (build_image_to_volume_attn, misc/sparse_utils.py:960-980: image token
+    points against volume-block centroids) -> [Nq, topk] int32."""
+    pts = np.asarray(qpoints, dtype=np.float32)
     cu_blk = np.asarray(cu_block_tokens, dtype=np.int64)
-    cen = block_mean_pool_ref(pts, cu_blk)                   # [nb, 3] fp32
+    cen = block_mean_pool_ref(np.asarray(key_points, dtype=np.float32), cu_blk)  # [nb, 3]
     cu_sb = np.asarray(cu_seqblocks, dtype=np.int64)
-    cu_q = np.asarray(cu_seqlens, dtype=np.int64)
+    cu_q = np.asarray(cu_seqlens_q, dtype=np.int64)
     out = np.full((pts.shape[0], topk), -1, dtype=np.int32)
     for b in range(cu_q.shape[0] - 1):
         qs, qe = int(cu_q[b]), int(cu_q[b + 1])
