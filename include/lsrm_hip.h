@@ -319,7 +319,9 @@ int lsrm_block_ids(const int32_t* cu_seqblocks, int64_t batch,
  * first among equal scores, NaN never chosen) are written to
  *   block_topk [hkv, n_q, topk] int32 as batch-local ids ascending, the row
  *   padded with -1 (all -1 for a batch element without compressed keys).
- * topk <= 64; head_dim in {32, 64, 128}.  No workspace.
+ * topk <= 128 (above 64 in two launches: the best min(64, topk - 2), then
+ * the best of the keys ranking after them); head_dim in {32, 64, 128}.
+ * No workspace.
  * Replaces sparse/ops/block_score.py:16-98.
  * ---------------------------------------------------------------------- */
 int lsrm_block_score(const void* q, const void* compressed_k, int dtype,
@@ -341,7 +343,7 @@ int lsrm_block_score(const void* q, const void* compressed_k, int dtype,
  *   min(topk, blocks of its batch element) blocks with the nearest centroid
  *   (squared distance in fp64, ties to the lower id), batch-local ids
  *   ascending, -1 padded, written identically for each of the hkv heads:
- *   block_topk [hkv, n_tokens, topk] int32.  topk <= 64.  No workspace.
+ *   block_topk [hkv, n_tokens, topk] int32.  topk <= 128.  No workspace.
  * Replaces misc/sparse_utils.py:1219-1273 (use_3d_aware_attn branch).
  * ---------------------------------------------------------------------- */
 int lsrm_volume_points(const int32_t* coords, int64_t n_tokens, int64_t volume_res,

@@ -21,6 +21,13 @@
 // the chosen ids are sorted ascending.  Tiles that straddle a batch boundary
 // are processed once per batch element they touch; rows of tokens outside
 // every element are written as -1 rows.
+//
+// topk in (64, 128]: two launches of the 64-entry selection.  The first
+// writes the row's best k1 = min(64, topk - 2) ids (ascending) and, in slots
+// k1 and k1 + 1, its k1-th best (score bits, id) as a bound; the second
+// keeps only keys that rank after the bound, selects the best topk - k1 of
+// them and merges both ascending lists into the row (every id of one list
+// differs from every id of the other, so a rank count places each).
 #include "common.h"
 
 namespace lsrm {
@@ -36,8 +43,13 @@ struct BlockScoreArgs {
   int32_t* out;
   int64_t nq, batch;
   int hq, hkv, g, topk;
+  int kout;  // ids this launch selects per row (topk, or k1 / topk - k1)
+  int k1;    // two-pass selection: ids of the first pass
   float qk_scale;
 };
+
+// Launch roles: the whole selection, or the two passes for topk > 64.
+constexpr int BS_ONE = 0, BS_FIRST = 1, BS_SECOND = 2;
 
 // (v, i) ranks before (w, j): larger score, equal scores by lower id.
 __device__ inline bool ranks_before(float v, int i, float w, int j) {
@@ -61,8 +73,9 @@ __device__ inline void key_swap(uint64_t& x, uint64_t& y, bool desc) {
 // Capacity (entries per lane) of the LDS buffer of the two-pass selection.
 constexpr int BS_CAP = 32;
 
-template <int DT, int D, int K>
+template <int DT, int D, int K, int MODE>
 __global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
+  static_assert(MODE == BS_ONE || K == 64, "the two-pass roles use the 64-entry lists");
   constexpr int NS = D / 16;
   const int lane = threadIdx.x & 63, hb = lane >> 5, l32 = lane & 31;
   const int64_t tiles = (a.nq + 31) / 32;
@@ -88,7 +101,17 @@ __global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
     const bool row_ok = row >= qs && row < qe && row < a.nq;
     const int64_t ks = a.cu_c[b];
     const int64_t nc = (int64_t)a.cu_c[b + 1] - ks;
-    const int kk = nc <= 0 ? 0 : (nc < a.topk ? (int)nc : a.topk);
+    const int kk = nc <= 0 ? 0 : (nc < a.kout ? (int)nc : a.kout);
+    // second pass: only keys ranking after the first pass's 64th best
+    float bnd_v = -2.0f;
+    int bnd_i = -1;
+    if constexpr (MODE == BS_SECOND) {
+      if (row_ok) {
+        const int32_t* src = a.out + ((int64_t)h * a.nq + row) * a.topk;
+        bnd_v = __int_as_float(src[a.k1]);
+        bnd_i = src[a.k1 + 1];
+      }
+    }
 
     float tv[K];
     int ti[K];
@@ -324,16 +347,20 @@ __global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int64_t key = c0 + acc_row(v, hb);
-          if (key < nc) insert(p[v], (int)key);
+          if constexpr (MODE == BS_SECOND) {
+            if (key < nc && ranks_before(bnd_v, bnd_i, p[v], (int)key)) insert(p[v], (int)key);
+          } else {
+            if (key < nc) insert(p[v], (int)key);
+          }
         }
       });
     }
 
+    float mv[K];  // the row's merged scores, best first (K > 32)
     if constexpr (K > 32) {
       // Merge with the partner lane's list (same row, the other 16 keys of
       // every block): the better of (own[i], partner[K-1-i]) is a bitonic
       // sequence holding the row's best K, sorted by a bitonic merge.
-      float mv[K];
 #pragma unroll
       for (int i = 0; i < K; ++i) {
         const float pv = __shfl_xor(tv[K - 1 - i], 32);
@@ -379,19 +406,77 @@ __global__ __launch_bounds__(256) void block_score_kernel(BlockScoreArgs a) {
     }
     if (row_ok && hb == 0) {
       int32_t* dst = a.out + ((int64_t)h * a.nq + row) * a.topk;
+      if constexpr (MODE == BS_ONE) {
 #pragma unroll
-      for (int i = 0; i < K; ++i)
-        if (i < a.topk) dst[i] = (i < kk && ids[i] != 0x7fffffff) ? ids[i] : -1;
+        for (int i = 0; i < K; ++i)
+          if (i < a.topk) dst[i] = (i < kk && ids[i] != 0x7fffffff) ? ids[i] : -1;
+      } else if constexpr (MODE == BS_FIRST) {
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+          if (i < a.k1) dst[i] = (i < kk && ids[i] != 0x7fffffff) ? ids[i] : -1;
+        // bound: the k1-th best when the row has k1 chosen keys, else a value
+        // nothing ranks after
+        float bv = -2.0f;
+        int bi = -1;
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+          if (i == a.k1 - 1 && kk == a.k1 && mi[i] >= 0) {
+            bv = mv[i];
+            bi = mi[i];
+          }
+        dst[a.k1] = __float_as_int(bv);
+        dst[a.k1 + 1] = bi;
+      } else {
+        // merge with the first pass's k1 ascending ids (0x7fffffff = none)
+        int first[K];
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+          const int x = i < a.k1 ? dst[i] : -1;
+          first[i] = x >= 0 ? x : 0x7fffffff;
+        }
+        int n1 = 0, n2 = 0;
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+          n1 += first[i] != 0x7fffffff ? 1 : 0;
+          n2 += (i < kk && ids[i] != 0x7fffffff) ? 1 : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+          int r1 = i, r2 = i;  // output slots: own index + ids of the other list below
+#pragma unroll
+          for (int j = 0; j < K; ++j) {
+            const int y = (j < kk) ? ids[j] : 0x7fffffff;
+            r1 += y < first[i] ? 1 : 0;
+            r2 += first[j] < ids[i] ? 1 : 0;
+          }
+          if (first[i] != 0x7fffffff) dst[r1] = first[i];
+          if (i < kk && ids[i] != 0x7fffffff) dst[r2] = ids[i];
+        }
+        for (int i = n1 + n2; i < a.topk; ++i) dst[i] = -1;
+      }
     }
   }
 }
 
 template <int DT, int D>
-int launch_block_score_d(const BlockScoreArgs& a, hipStream_t st) {
-  const int64_t waves = (a.nq + 31) / 32 * a.hkv;
+int launch_block_score_d(const BlockScoreArgs& a0, hipStream_t st) {
+  const int64_t waves = (a0.nq + 31) / 32 * a0.hkv;
   const dim3 grid((unsigned)((waves + 3) / 4));
-#define LSRM_BS_K(KV)                                                            \
-  hipLaunchKernelGGL((block_score_kernel<DT, D, KV>), grid, dim3(256), 0, st, a); \
+  if (a0.topk > 64) {
+    BlockScoreArgs a = a0;
+    a.k1 = a0.topk - 2 < 64 ? a0.topk - 2 : 64;
+    a.kout = a.k1;
+    hipLaunchKernelGGL((block_score_kernel<DT, D, 64, BS_FIRST>), grid, dim3(256), 0, st, a);
+    LSRM_CHECK_LAUNCH();
+    a.kout = a0.topk - a.k1;
+    hipLaunchKernelGGL((block_score_kernel<DT, D, 64, BS_SECOND>), grid, dim3(256), 0, st, a);
+    LSRM_CHECK_LAUNCH();
+    return LSRM_OK;
+  }
+  BlockScoreArgs a = a0;
+  a.kout = a0.topk;
+#define LSRM_BS_K(KV)                                                                    \
+  hipLaunchKernelGGL((block_score_kernel<DT, D, KV, BS_ONE>), grid, dim3(256), 0, st, a); \
   break;
   switch (a.topk <= 8 ? 8 : a.topk <= 16 ? 16 : a.topk <= 32 ? 32 : 64) {
     case 8: LSRM_BS_K(8)
@@ -419,7 +504,7 @@ extern "C" int lsrm_block_score(const void* q, const void* compressed_k, int dty
       (n_q > 0 && (!q || !compressed_k || !lse || !block_topk)))
     return LSRM_ERR_INVALID_ARG;
   if (dtype != LSRM_F16 && dtype != LSRM_BF16) return LSRM_ERR_UNSUPPORTED;
-  if (topk > 64 || (head_dim != 32 && head_dim != 64 && head_dim != 128))
+  if (topk > 128 || (head_dim != 32 && head_dim != 64 && head_dim != 128))
     return LSRM_ERR_UNSUPPORTED;
   if (n_q == 0) return LSRM_OK;
   BlockScoreArgs a;

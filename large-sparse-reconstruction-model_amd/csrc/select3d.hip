@@ -14,6 +14,10 @@
 //     are exact there), ties by the lower block id; one lane per token
 //     keeps a running top-K list in registers while the wave walks the
 //     centroids of its batch element with wave-uniform (scalar) loads.
+//     topk in (64, 128] takes two launches of the 64-entry list: the first
+//     writes its best k1 = min(64, topk - 3) ids and the k1-th (distance,
+//     id) into head 0's row, the second keeps only blocks ranking after
+//     that bound and merges both ascending lists.
 #include "common.h"
 
 namespace lsrm {
@@ -30,11 +34,14 @@ __global__ __launch_bounds__(256) void volume_points_kernel(
   points[i * 3 + 2] = f(c[1]);
 }
 
-template <int K>
+constexpr int NB_ONE = 0, NB_FIRST = 1, NB_SECOND = 2;
+
+template <int K, int MODE>
 __global__ __launch_bounds__(256) void nearest_blocks_kernel(
     const float* __restrict__ points, const float* __restrict__ centroids,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_sb, int64_t batch,
-    int64_t n, int topk, int hkv, int32_t* __restrict__ out) {
+    int64_t n, int topk, int hkv, int k1, int32_t* __restrict__ out) {
+  static_assert(MODE == NB_ONE || K == 64, "the two-pass roles use the 64-entry list");
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t w0 = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~63);
   if (w0 >= n) return;
@@ -53,10 +60,22 @@ __global__ __launch_bounds__(256) void nearest_blocks_kernel(
     tv[k] = __builtin_inf();
     ti[k] = 0x7fffffff;  // empty: any candidate ranks before it
   }
+  // ids this launch selects, and (second pass) the bound to rank after
+  const int kout = MODE == NB_ONE ? topk : (MODE == NB_FIRST ? k1 : topk - k1);
+  double bnd_d = -1.0;
+  int bnd_i = 0x7fffffff;
+  if constexpr (MODE == NB_SECOND) {
+    if (live) {
+      const int32_t* src = out + i * topk;  // head 0's row
+      const uint64_t lo = (uint32_t)src[k1], hi = (uint32_t)src[k1 + 1];
+      bnd_d = __longlong_as_double((long long)((hi << 32) | lo));
+      bnd_i = src[k1 + 2];
+    }
+  }
   int kk = 0;
   for (int b = b_first < 0 ? 0 : b_first; b <= b_last && b < batch; ++b) {
     const int bs = cu_sb[b], be = cu_sb[b + 1];
-    if (my_b == b) kk = be - bs < topk ? (be - bs > 0 ? be - bs : 0) : topk;
+    if (my_b == b) kk = be - bs < kout ? (be - bs > 0 ? be - bs : 0) : kout;
     for (int c = bs; c < be; ++c) {  // wave-uniform: scalar centroid loads
       const double dx = px - (double)centroids[(int64_t)c * 3 + 0];
       const double dy = py - (double)centroids[(int64_t)c * 3 + 1];
@@ -68,7 +87,8 @@ __global__ __launch_bounds__(256) void nearest_blocks_kernel(
       const int id = c - bs;
       // ids arrive ascending: an equal distance already listed keeps its
       // place, an empty slot (id INT_MAX) always yields.
-      if (my_b == b && (d < tv[K - 1] || (d == tv[K - 1] && id < ti[K - 1]))) {
+      const bool after = MODE != NB_SECOND || d > bnd_d || (d == bnd_d && id > bnd_i);
+      if (my_b == b && after && (d < tv[K - 1] || (d == tv[K - 1] && id < ti[K - 1]))) {
 #pragma unroll
         for (int k = K - 1; k >= 0; --k) {
           const int kp = k > 0 ? k - 1 : 0;
@@ -104,11 +124,62 @@ __global__ __launch_bounds__(256) void nearest_blocks_kernel(
       }
     }
   }
-  for (int h = 0; h < hkv; ++h) {
-    int32_t* dst = out + ((int64_t)h * n + i) * topk;
+  if constexpr (MODE == NB_ONE) {
+    for (int h = 0; h < hkv; ++h) {
+      int32_t* dst = out + ((int64_t)h * n + i) * topk;
 #pragma unroll
-    for (int k = 0; k < K; ++k)
-      if (k < topk) dst[k] = (k < kk && ids[k] != 0x7fffffff) ? ids[k] : -1;
+      for (int k = 0; k < K; ++k)
+        if (k < topk) dst[k] = (k < kk && ids[k] != 0x7fffffff) ? ids[k] : -1;
+    }
+  } else if constexpr (MODE == NB_FIRST) {
+    int32_t* dst = out + i * topk;  // head 0's row holds the first pass
+    double bd = __builtin_inf();
+    int bi = -1;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (k < k1) dst[k] = (k < kk && ids[k] != 0x7fffffff) ? ids[k] : -1;
+      if (k == k1 - 1 && kk == k1 && ti[k] != 0x7fffffff) {  // the k1-th nearest
+        bd = tv[k];
+        bi = ti[k];
+      }
+    }
+    // without k1 chosen blocks nothing may follow: +inf and the largest id
+    const uint64_t bits = (uint64_t)__double_as_longlong(bd);
+    dst[k1] = (int32_t)(uint32_t)bits;
+    dst[k1 + 1] = (int32_t)(uint32_t)(bits >> 32);
+    dst[k1 + 2] = bi >= 0 ? bi : 0x7fffffff;
+  } else {
+    // merge with the first pass's k1 ascending ids (0x7fffffff = none)
+    const int32_t* src = out + i * topk;
+    int first[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int x = k < k1 ? src[k] : -1;
+      first[k] = x >= 0 ? x : 0x7fffffff;
+    }
+    int n1 = 0, n2 = 0, slot1[K], slot2[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      n1 += first[k] != 0x7fffffff ? 1 : 0;
+      n2 += ids[k] != 0x7fffffff ? 1 : 0;
+      int r1 = k, r2 = k;  // own index + ids of the other list below
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        r1 += ids[j] < first[k] ? 1 : 0;
+        r2 += first[j] < ids[k] ? 1 : 0;
+      }
+      slot1[k] = r1;
+      slot2[k] = r2;
+    }
+    for (int h = 0; h < hkv; ++h) {
+      int32_t* dst = out + ((int64_t)h * n + i) * topk;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        if (first[k] != 0x7fffffff) dst[slot1[k]] = first[k];
+        if (ids[k] != 0x7fffffff) dst[slot2[k]] = ids[k];
+      }
+      for (int k = n1 + n2; k < topk; ++k) dst[k] = -1;
+    }
   }
 }
 
@@ -135,14 +206,26 @@ extern "C" int lsrm_nearest_blocks(const float* points, const float* centroids,
   if (n_tokens < 0 || batch <= 0 || topk <= 0 || hkv <= 0 || !cu_seqlens || !cu_seqblocks ||
       (n_tokens > 0 && (!points || !centroids || !block_topk)))
     return LSRM_ERR_INVALID_ARG;
-  if (topk > 64) return LSRM_ERR_UNSUPPORTED;
+  if (topk > 128) return LSRM_ERR_UNSUPPORTED;
   if (n_tokens == 0) return LSRM_OK;
   const dim3 grid((unsigned)((n_tokens + 255) / 256));
   hipStream_t st = (hipStream_t)stream;
-#define LSRM_NB_K(KV)                                                                     \
-  hipLaunchKernelGGL(nearest_blocks_kernel<KV>, grid, dim3(256), 0, st, points, centroids, \
-                     cu_seqlens, cu_seqblocks, batch, n_tokens, (int)topk, (int)hkv,       \
-                     block_topk);                                                          \
+  if (topk > 64) {
+    const int k1 = topk - 3 < 64 ? (int)topk - 3 : 64;
+    hipLaunchKernelGGL((nearest_blocks_kernel<64, NB_FIRST>), grid, dim3(256), 0, st, points,
+                       centroids, cu_seqlens, cu_seqblocks, batch, n_tokens, (int)topk, (int)hkv,
+                       k1, block_topk);
+    LSRM_CHECK_LAUNCH();
+    hipLaunchKernelGGL((nearest_blocks_kernel<64, NB_SECOND>), grid, dim3(256), 0, st, points,
+                       centroids, cu_seqlens, cu_seqblocks, batch, n_tokens, (int)topk, (int)hkv,
+                       k1, block_topk);
+    LSRM_CHECK_LAUNCH();
+    return LSRM_OK;
+  }
+#define LSRM_NB_K(KV)                                                                   \
+  hipLaunchKernelGGL((nearest_blocks_kernel<KV, NB_ONE>), grid, dim3(256), 0, st, points, \
+                     centroids, cu_seqlens, cu_seqblocks, batch, n_tokens, (int)topk,     \
+                     (int)hkv, 0, block_topk);                                           \
   break;
   switch (topk <= 8 ? 8 : topk <= 16 ? 16 : topk <= 32 ? 32 : 64) {
     case 8: LSRM_NB_K(8)

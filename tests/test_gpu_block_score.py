@@ -67,10 +67,15 @@ def _check_selection(got, ref, scores, topk, cu_q, cu_c):
     (8, 2, 64, 32),      # G = 4
     (32, 2, 32, 16),     # the product's GQA shape: G = 16, D = 32
     (2, 2, 128, 8),      # D = 128
-    (4, 4, 64, 64),      # largest topk
+    (4, 4, 64, 64),      # largest single-launch topk
+    (4, 4, 64, 72),      # two launches: the product's topk_multiimage * 18 images
+    (8, 2, 64, 65),      # two launches, the first selecting 63
+    (4, 4, 64, 128),     # largest topk
 ])
 def test_block_score_matches_oracle(hq, hkv, d, topk):
     q_lens, c_lens = [157, 300, 45], [90, 61, 40]
+    if topk > 64:
+        c_lens = [150, 61, 200]          # one element with fewer keys than topk
     q, ck, cv, cu_q, cu_c = _case(1, q_lens, c_lens, hq, hkv, d)
     _, lse = compressed_attention_ref(q, ck, cv, cu_q, cu_c)      # natural log
     got = ops.get_block_score(q.to(DEV), ck.to(DEV), lse.to(DEV), topk, cu_q.to(DEV),

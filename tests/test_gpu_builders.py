@@ -71,8 +71,9 @@ def test_separation_outside_grid_and_2d():
     assert cu_blk.cpu().numpy().tolist() == ref_blk.tolist()
 
 
-@pytest.mark.parametrize("topk", [8, 16, 24])
+@pytest.mark.parametrize("topk", [8, 16, 24, 65, 66, 67, 72, 128])
 def test_build_volume_to_volume_attn_3d_aware_bitexact(topk):
+    # topk above 64 takes the two-launch selection (first k1 = min(64, topk - 3))
     c = _voxels()
     args = types.SimpleNamespace(volume_res=64, block_size=8, bbox_radius=1.0,
                                  use_3d_aware_attn=True, topk_volume=topk)
