@@ -106,6 +106,21 @@ int lsrm_block_mean_pool(const void* x, int x_dtype, int64_t n_tokens,
                          int64_t n_blocks, void* out, int out_dtype,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* The two sparse3d_compression calls of the compression module (keys and
+ * values: same token count, channels and block partition) in one piece
+ * launch and one combine launch; out_a and out_b may have different dtypes.
+ * Each output equals lsrm_block_mean_pool of its input bit for bit.
+ * Replaces: sparse/module/spatial_sparse_attention.py:49-66 (the pair of
+ * sparse3d_compression calls, each 27-37). */
+size_t lsrm_block_mean_pool2_workspace_size(int64_t n_tokens, int64_t channels,
+                                            int64_t n_blocks);
+int lsrm_block_mean_pool2(const void* x_a, const void* x_b, int x_dtype,
+                          int64_t n_tokens, int64_t channels,
+                          const int32_t* cu_block_tokens, int64_t n_blocks,
+                          void* out_a, int out_a_dtype, void* out_b,
+                          int out_b_dtype, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 /* Allocation-free variant of lsrm_block_mean_pool (no counterpart in the
  * reference): for callers that cannot allocate device memory or pass a
  * workspace (code under HIP graph capture, tight serving loops).  Same

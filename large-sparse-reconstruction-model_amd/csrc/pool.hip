@@ -11,8 +11,11 @@
 //                  is crossed.  Partial (block b, chunk j) lives at row b + j
 //                  of the partial buffer (unique because blocks are
 //                  contiguous and ordered).
-//   pool_combine : one thread per (block, 8-channel group) adds the block's
+//   pool_pieces_slab : the 16-bit, 512-channel-multiple form of pool_pieces
+//                  (one wave per chunk and 512-channel slab, 64 VGPRs).
+//   pool_combine : one thread per (block, 4-channel group) adds the block's
 //                  partials in chunk order, divides by the length and rounds.
+//   pool_combine2: the same for two tensors (keys and values) in one launch.
 // Every add is sequential, so the result is a fixed function of the input
 // (the contract the CPU oracle restates bit for bit).  Input rows are read
 // exactly once, with nontemporal loads (measured +8% on the cfg3 K tensor).
@@ -162,27 +165,42 @@ __global__ __launch_bounds__(256) void pool_pieces(
 }
 
 // 16-bit rows, channel count a multiple of 512: one wave per (64-row chunk,
-// 512-channel slab), 8 channels per lane.  The first eight rows are loaded
-// before the block lookup (so every wave has loads in flight from its first
-// instruction) and rows are then streamed in double-buffered groups of
-// eight.  With IF, the block owning the chunk's first row is found in the
-// kernel (nb + 1 <= 512 offsets: lane l compares entries 8l..8l+7 with the
-// row and the wave counts the hits), otherwise it comes from the
-// pool_chunk_first table.  The sums are the same sequential fp32 sums as in
-// pool_pieces.
-constexpr int POOL_G = 8;  // rows per load group
+// 512-channel slab), 8 channels per lane.  Rows stream in double-buffered
+// groups of POOL_G; the kernel is held to 64 VGPRs (8 waves per SIMD) so a
+// launch of a few thousand waves is resident at once instead of running in
+// one and a half rounds.  With IF, the block owning the chunk's first row is
+// found in the kernel (nb + 1 <= 512 offsets: lane l compares entries
+// 8l..8l+7 with the row and the wave counts the hits); those loads are issued
+// before the first row group, so the wave waits for them alone.  Otherwise
+// the block comes from the pool_chunk_first table.  The end of the next
+// block is loaded one crossing ahead, and row groups that lie inside the
+// current block are added without per-row checks.  The sums are the same
+// sequential fp32 sums as in pool_pieces.
+constexpr int POOL_G = 4;  // rows per load group
 
-template <int DT, bool IF>
-__global__ __launch_bounds__(256) void pool_pieces_slab(
-    const uint16_t* __restrict__ x, int64_t n, int64_t ch,
-    const int32_t* __restrict__ cu, int64_t nb,
-    const int32_t* __restrict__ first, float* __restrict__ partial) {
-  const int64_t n_vec = ch / 8;
-  const int64_t n_chunks = (n + POOL_CHUNK - 1) / POOL_CHUNK;
-  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (item >= n_chunks * n_vec) return;  // whole waves (n_vec % 64 == 0)
-  const int64_t j = __builtin_amdgcn_readfirstlane((int)(item / n_vec));
-  const int64_t c0 = (item - j * n_vec) * 8;
+// NT = 2 pools a second tensor of the same shape and blocks (x2 -> partial2)
+// in the same launch: its items follow the first tensor's.
+template <int DT, bool IF, int NT = 1>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void
+pool_pieces_slab(const uint16_t* __restrict__ x, int64_t n, int64_t ch,
+                 const int32_t* __restrict__ cu, int64_t nb,
+                 const int32_t* __restrict__ first, float* __restrict__ partial,
+                 const uint16_t* __restrict__ x2 = nullptr,
+                 float* __restrict__ partial2 = nullptr) {
+  // Item counts stay below 2^31 (checked by the launcher): 32-bit indexing.
+  const uint32_t n_vec = (uint32_t)(ch / 8);
+  const uint32_t n_chunks = (uint32_t)((n + POOL_CHUNK - 1) / POOL_CHUNK);
+  uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= NT * n_chunks * n_vec) return;  // whole waves (n_vec % 64 == 0)
+  if constexpr (NT == 2) {
+    if (item >= n_chunks * n_vec) {  // wave-uniform: the second tensor
+      item -= n_chunks * n_vec;
+      x = x2;
+      partial = partial2;
+    }
+  }
+  const int64_t j = __builtin_amdgcn_readfirstlane(item / n_vec);
+  const int64_t c0 = (int64_t)(item - (uint32_t)j * n_vec) * 8;
   const int64_t r0 = j * POOL_CHUNK;
   const int64_t r1 = r0 + POOL_CHUNK < n ? r0 + POOL_CHUNK : n;
   const uint16_t* xp = x + c0;
@@ -195,7 +213,6 @@ __global__ __launch_bounds__(256) void pool_pieces_slab(
       dst[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xp + rr * ch));
     }
   };
-  load_group(buf[0], r0);
 
   // b = last block whose start is <= r0 (-1: before the first block,
   // nb: past the last).  bs/be bound the rows block b owns.
@@ -206,14 +223,16 @@ __global__ __launch_bounds__(256) void pool_pieces_slab(
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int64_t idx = 8 * lane + i;
-      cv[i] = idx <= nb ? cu[idx] : 0x7fffffff;
+      cv[i] = cu[idx <= nb ? idx : nb];
     }
+    load_group(buf[0], r0);
     int cnt = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       cnt += __popcll(__ballot((int64_t)cv[i] <= r0 && 8 * lane + i <= nb));
     b = __builtin_amdgcn_readfirstlane(cnt) - 1;
   } else {
+    load_group(buf[0], r0);
     b = first[j];
   }
   int64_t be = b < 0 ? (int64_t)cu[0] : (b < nb ? (int64_t)cu[b + 1] : INT64_MAX);
@@ -248,22 +267,32 @@ __global__ __launch_bounds__(256) void pool_pieces_slab(
     flush();
     return;
   }
+  // bn = end of block b + 1 (its start is be).
+  int64_t bn = b + 1 < nb ? (int64_t)cu[b + 2] : INT64_MAX;
   bool have = false;
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
     if (g + 1 < NG) load_group(buf[(g + 1) & 1], r0 + (g + 1) * POOL_G);
+    const int64_t g0 = r0 + g * POOL_G;
+    if (b >= 0 && b < nb && bs <= g0 && be >= g0 + POOL_G && g0 + POOL_G <= r1) {
+#pragma unroll
+      for (int u = 0; u < POOL_G; ++u) add_row(buf[g & 1][u]);
+      have = true;
+      continue;
+    }
 #pragma unroll
     for (int u = 0; u < POOL_G; ++u) {
-      const int64_t row = r0 + g * POOL_G + u;
+      const int64_t row = g0 + u;
       if (row < r1) {
         while (b < nb && row >= be) {
-          if (have) flush();
+          if (have && b >= 0) flush();
           have = false;
 #pragma unroll
           for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
           ++b;
-          bs = b < nb ? (int64_t)cu[b] : INT64_MAX;
-          be = b < nb ? (int64_t)cu[b + 1] : INT64_MAX;
+          bs = b < nb ? be : INT64_MAX;
+          be = b < nb ? bn : INT64_MAX;
+          bn = b + 1 < nb ? (int64_t)cu[b + 2] : INT64_MAX;
         }
         if (b >= 0 && b < nb && row >= bs) {
           add_row(buf[g & 1][u]);
@@ -302,18 +331,16 @@ __global__ __launch_bounds__(256) void pool_combine(
     const int64_t j0 = s / POOL_CHUNK, j1 = (e - 1) / POOL_CHUNK;
     // Up to PB pieces are loaded before any is added (one memory round trip
     // per PB pieces); the adds stay in chunk order.
-    constexpr int PB = VEC == 8 ? 8 : 16;
+    constexpr int PB = VEC == 1 ? 16 : 8;
     for (int64_t jb = j0; jb <= j1; jb += PB) {
       float v[PB][VEC];
 #pragma unroll
       for (int u = 0; u < PB; ++u) {
         const int64_t j = jb + u <= j1 ? jb + u : j1;
         const float* src = partial + (b + j) * ch + c0;
-        if constexpr (VEC == 8) {
+        if constexpr (VEC == 4) {
           const float4 lo = reinterpret_cast<const float4*>(src)[0];
-          const float4 hi = reinterpret_cast<const float4*>(src)[1];
           v[u][0] = lo.x; v[u][1] = lo.y; v[u][2] = lo.z; v[u][3] = lo.w;
-          v[u][4] = hi.x; v[u][5] = hi.y; v[u][6] = hi.z; v[u][7] = hi.w;
         } else {
           v[u][0] = src[0];
         }
@@ -330,6 +357,58 @@ __global__ __launch_bounds__(256) void pool_combine(
   const float len = e > s ? (float)(e - s) : 0.0f;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) store_out<ODT>(out, b * ch + c0 + i, acc[i] / len);
+}
+
+// Both tensors' combines in one launch: items [0, nb * n_vec) of tensor a,
+// then those of tensor b (output types ODTA, ODTB).
+template <int ODTA, int ODTB>
+__global__ __launch_bounds__(256) void pool_combine2(
+    const float* __restrict__ partial_a, const float* __restrict__ partial_b, int64_t n,
+    int64_t ch, const int32_t* __restrict__ cu, int64_t nb, void* __restrict__ out_a,
+    void* __restrict__ out_b) {
+  constexpr int VEC = 4;
+  const int64_t n_vec = ch / VEC;
+  int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= 2 * nb * n_vec) return;
+  const bool second = item >= nb * n_vec;
+  if (second) item -= nb * n_vec;
+  const float* partial = second ? partial_b : partial_a;
+  const int64_t b = item / n_vec;
+  const int64_t c0 = (item - b * n_vec) * VEC;
+  int64_t s = cu[b], e = cu[b + 1];
+  s = s < 0 ? 0 : (s > n ? n : s);
+  e = e < 0 ? 0 : (e > n ? n : e);
+  float acc[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) acc[i] = 0.0f;
+  if (e > s) {
+    const int64_t j0 = s / POOL_CHUNK, j1 = (e - 1) / POOL_CHUNK;
+    constexpr int PB = 8;
+    for (int64_t jb = j0; jb <= j1; jb += PB) {
+      float v[PB][VEC];
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        const int64_t j = jb + u <= j1 ? jb + u : j1;
+        const float* src = partial + (b + j) * ch + c0;
+        const float4 lo = reinterpret_cast<const float4*>(src)[0];
+        v[u][0] = lo.x; v[u][1] = lo.y; v[u][2] = lo.z; v[u][3] = lo.w;
+      }
+#pragma unroll
+      for (int u = 0; u < PB; ++u)
+        if (jb + u <= j1) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[i] = acc[i] + v[u][i];
+        }
+    }
+  }
+  const float len = e > s ? (float)(e - s) : 0.0f;
+  if (second) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) store_out<ODTB>(out_b, b * ch + c0 + i, acc[i] / len);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) store_out<ODTA>(out_a, b * ch + c0 + i, acc[i] / len);
+  }
 }
 
 int64_t pool_partial_rows(int64_t n, int64_t nb) {
@@ -350,7 +429,8 @@ int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
                    ((uintptr_t)partial % 16) == 0;
   const int64_t n_vec = vec ? ch / POOL_VEC : ch;
   const int64_t n_chunks = (n + POOL_CHUNK - 1) / POOL_CHUNK;
-  const bool slab = vec && x_dtype != LSRM_F32 && n_vec % 64 == 0;
+  const bool slab = vec && x_dtype != LSRM_F32 && n_vec % 64 == 0 &&
+                   n_chunks * n_vec < (int64_t{1} << 31);
   const bool inline_first = slab && nb + 1 <= 512;
   if (n > 0 && slab) {
     if (!inline_first)
@@ -402,12 +482,14 @@ int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
     LSRM_CHECK_LAUNCH();
   }
   {
-    const int64_t items = nb * n_vec;
+    // 4 channels per thread on the vector path (twice the threads of the
+    // piece kernel's 8: more loads in flight for the few blocks).
+    const int64_t items = vec ? nb * (ch / 4) : nb * ch;
     dim3 grid((unsigned)((items + 255) / 256));
 #define LSRM_POOL_C(ODT)                                                     \
   do {                                                                       \
     if (vec)                                                                 \
-      hipLaunchKernelGGL((pool_combine<ODT, 8>), grid, dim3(256), 0, st,     \
+      hipLaunchKernelGGL((pool_combine<ODT, 4>), grid, dim3(256), 0, st,     \
                          partial, n, ch, cu, nb, out);                       \
     else                                                                     \
       hipLaunchKernelGGL((pool_combine<ODT, 1>), grid, dim3(256), 0, st,     \
@@ -420,6 +502,75 @@ int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
       default: return LSRM_ERR_UNSUPPORTED;
     }
 #undef LSRM_POOL_C
+    LSRM_CHECK_LAUNCH();
+  }
+  return LSRM_OK;
+}
+
+// Two tensors of one shape and block partition: one piece launch and one
+// combine launch for both when the slab path applies, otherwise the
+// single-tensor launches one after the other (identical results).
+int launch_block_mean_pool2(const void* xa, const void* xb, int x_dtype, int64_t n, int64_t ch,
+                            const int32_t* cu, int64_t nb, void* out_a, int out_a_dtype,
+                            void* out_b, int out_b_dtype, float* partial_a, float* partial_b,
+                            int32_t* first, hipStream_t st) {
+  if (nb == 0) return LSRM_OK;
+  const bool slab = (ch % POOL_VEC) == 0 && x_dtype != LSRM_F32 && (ch / POOL_VEC) % 64 == 0 &&
+                    ((uintptr_t)xa % 16) == 0 && ((uintptr_t)xb % 16) == 0 &&
+                    ((uintptr_t)partial_a % 16) == 0 && ((uintptr_t)partial_b % 16) == 0 &&
+                    2 * ((n + POOL_CHUNK - 1) / POOL_CHUNK) * (ch / POOL_VEC) < (int64_t{1} << 31);
+  if (!slab || n == 0) {
+    int rc = launch_block_mean_pool(xa, x_dtype, n, ch, cu, nb, out_a, out_a_dtype, partial_a,
+                                    first, st);
+    if (rc) return rc;
+    return launch_block_mean_pool(xb, x_dtype, n, ch, cu, nb, out_b, out_b_dtype, partial_b,
+                                  first, st);
+  }
+  const int64_t n_vec = ch / POOL_VEC;
+  const int64_t n_chunks = (n + POOL_CHUNK - 1) / POOL_CHUNK;
+  const bool inline_first = nb + 1 <= 512;
+  if (!inline_first)
+    hipLaunchKernelGGL(pool_chunk_first, dim3((unsigned)((n_chunks + 255) / 256)), dim3(256), 0,
+                       st, cu, nb, n_chunks, first);
+  {
+    const int64_t items = 2 * n_chunks * n_vec;
+    dim3 grid((unsigned)((items + 255) / 256));
+    const uint16_t* a = reinterpret_cast<const uint16_t*>(xa);
+    const uint16_t* b = reinterpret_cast<const uint16_t*>(xb);
+#define LSRM_POOL2_P(DT)                                                                      \
+  if (inline_first)                                                                           \
+    hipLaunchKernelGGL((pool_pieces_slab<DT, true, 2>), grid, dim3(256), 0, st, a, n, ch, cu, \
+                       nb, first, partial_a, b, partial_b);                                   \
+  else                                                                                        \
+    hipLaunchKernelGGL((pool_pieces_slab<DT, false, 2>), grid, dim3(256), 0, st, a, n, ch,    \
+                       cu, nb, first, partial_a, b, partial_b);
+    if (x_dtype == LSRM_F16) {
+      LSRM_POOL2_P(LSRM_F16)
+    } else {
+      LSRM_POOL2_P(LSRM_BF16)
+    }
+#undef LSRM_POOL2_P
+    LSRM_CHECK_LAUNCH();
+  }
+  {
+    const int64_t items = 2 * nb * (ch / 4);
+    dim3 grid((unsigned)((items + 255) / 256));
+#define LSRM_POOL2_C(A, B)                                                                  \
+  hipLaunchKernelGGL((pool_combine2<A, B>), grid, dim3(256), 0, st, partial_a, partial_b, n, \
+                     ch, cu, nb, out_a, out_b)
+#define LSRM_POOL2_CB(A)                                          \
+  switch (out_b_dtype) {                                          \
+    case LSRM_F32: LSRM_POOL2_C(A, LSRM_F32); break;              \
+    case LSRM_F16: LSRM_POOL2_C(A, LSRM_F16); break;              \
+    default: LSRM_POOL2_C(A, LSRM_BF16); break;                   \
+  }
+    switch (out_a_dtype) {
+      case LSRM_F32: LSRM_POOL2_CB(LSRM_F32) break;
+      case LSRM_F16: LSRM_POOL2_CB(LSRM_F16) break;
+      default: LSRM_POOL2_CB(LSRM_BF16) break;
+    }
+#undef LSRM_POOL2_CB
+#undef LSRM_POOL2_C
     LSRM_CHECK_LAUNCH();
   }
   return LSRM_OK;
@@ -503,4 +654,36 @@ extern "C" int lsrm_block_mean_pool_noalloc(const void* x, int x_dtype, int64_t 
   if (rc) return rc;
   return lsrm_block_mean_pool(x, x_dtype, n_tokens, channels, cu_block_tokens, n_blocks, out,
                               out_dtype, ws, LSRM_POOL_SCRATCH_BYTES, stream);
+}
+
+extern "C" size_t lsrm_block_mean_pool2_workspace_size(int64_t n_tokens, int64_t channels,
+                                                       int64_t n_blocks) {
+  if (n_tokens < 0 || channels < 0 || n_blocks < 0) return 0;
+  return 2 * ((size_t)lsrm::pool_partial_rows(n_tokens, n_blocks) * (size_t)channels *
+              sizeof(float) + 256) +
+         (size_t)lsrm::pool_first_count(n_tokens) * 4 + 256;
+}
+
+extern "C" int lsrm_block_mean_pool2(const void* x_a, const void* x_b, int x_dtype,
+                                     int64_t n_tokens, int64_t channels,
+                                     const int32_t* cu_block_tokens, int64_t n_blocks,
+                                     void* out_a, int out_a_dtype, void* out_b, int out_b_dtype,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_tokens < 0 || channels <= 0 || n_blocks < 0) return LSRM_ERR_INVALID_ARG;
+  if (n_blocks > 0 && (!cu_block_tokens || !out_a || !out_b)) return LSRM_ERR_INVALID_ARG;
+  if (n_tokens > 0 && (!x_a || !x_b)) return LSRM_ERR_INVALID_ARG;
+  if (x_dtype < LSRM_F32 || x_dtype > LSRM_BF16) return LSRM_ERR_UNSUPPORTED;
+  if (out_a_dtype < LSRM_F32 || out_a_dtype > LSRM_BF16 || out_b_dtype < LSRM_F32 ||
+      out_b_dtype > LSRM_BF16)
+    return LSRM_ERR_UNSUPPORTED;
+  const size_t need = lsrm_block_mean_pool2_workspace_size(n_tokens, channels, n_blocks);
+  if (workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
+  const size_t part = (size_t)lsrm::pool_partial_rows(n_tokens, n_blocks) * (size_t)channels;
+  float* partial_a = reinterpret_cast<float*>(lsrm::align_up((size_t)workspace, 256));
+  float* partial_b = reinterpret_cast<float*>(lsrm::align_up((size_t)(partial_a + part), 256));
+  int32_t* first =
+      reinterpret_cast<int32_t*>(lsrm::align_up((size_t)(partial_b + part), 256));
+  return lsrm::launch_block_mean_pool2(x_a, x_b, x_dtype, n_tokens, channels, cu_block_tokens,
+                                       n_blocks, out_a, out_a_dtype, out_b, out_b_dtype,
+                                       partial_a, partial_b, first, (hipStream_t)stream);
 }

@@ -45,6 +45,9 @@ _SIGNATURES = {
     "lsrm_block_mean_pool_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "lsrm_block_mean_pool": (_I, [_P, _I, _I64, _I64, _P, _I64, _P, _I, _P, _SZ, _P]),
     "lsrm_block_mean_pool_noalloc": (_I, [_P, _I, _I64, _I64, _P, _I64, _P, _I, _P]),
+    "lsrm_block_mean_pool2_workspace_size": (_SZ, [_I64, _I64, _I64]),
+    "lsrm_block_mean_pool2": (
+        _I, [_P, _P, _I, _I64, _I64, _P, _I64, _P, _I, _P, _I, _P, _SZ, _P]),
     "lsrm_select_blocks_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "lsrm_select_blocks": (
         _I,
@@ -197,6 +200,38 @@ def block_mean_pool(x: torch.Tensor, cu_block_tokens: torch.Tensor,
             _DTYPE_CODE[out_dtype], _ptr(ws), ws.numel(), _stream(dev)),
             "lsrm_block_mean_pool")
     return out
+
+
+def block_mean_pool2(x_a: torch.Tensor, x_b: torch.Tensor, cu_block_tokens: torch.Tensor,
+                     out_a_dtype: Optional[torch.dtype] = None,
+                     out_b_dtype: Optional[torch.dtype] = None):
+    """block_mean_pool of two [N, C] tensors of one dtype over one block
+    partition (keys and values) in one pair of launches -> (out_a, out_b),
+    each bit for bit equal to block_mean_pool of its input."""
+    if x_a.dim() != 2 or x_a.shape != x_b.shape:
+        raise ValueError("x_a and x_b must be 2-D [n_tokens, channels] of one shape")
+    if x_a.dtype not in _DTYPE_CODE or x_b.dtype != x_a.dtype:
+        raise TypeError(f"unsupported or mismatched dtypes {x_a.dtype}, {x_b.dtype}")
+    out_a_dtype = out_a_dtype or x_a.dtype
+    out_b_dtype = out_b_dtype or x_a.dtype
+    if out_a_dtype not in _DTYPE_CODE or out_b_dtype not in _DTYPE_CODE:
+        raise TypeError(f"unsupported output dtypes {out_a_dtype}, {out_b_dtype}")
+    dev = _dev_check(x_a, x_b, cu_block_tokens)
+    x_a, x_b = x_a.contiguous(), x_b.contiguous()
+    cu = _i32(cu_block_tokens)
+    n, c = x_a.shape
+    nb = cu.numel() - 1
+    out_a = torch.empty(nb, c, dtype=out_a_dtype, device=dev)
+    out_b = torch.empty(nb, c, dtype=out_b_dtype, device=dev)
+    if nb == 0:
+        return out_a, out_b
+    with torch.cuda.device(dev):
+        ws = _workspace(lib().lsrm_block_mean_pool2_workspace_size(n, c, nb), dev)
+        _check(lib().lsrm_block_mean_pool2(
+            _ptr(x_a), _ptr(x_b), _DTYPE_CODE[x_a.dtype], n, c, _ptr(cu), nb, _ptr(out_a),
+            _DTYPE_CODE[out_a_dtype], _ptr(out_b), _DTYPE_CODE[out_b_dtype], _ptr(ws),
+            ws.numel(), _stream(dev)), "lsrm_block_mean_pool2")
+    return out_a, out_b
 
 
 # ------------------------------------------------------------- selection --

@@ -92,6 +92,50 @@ def test_pool_slab_path_small_and_empty_blocks(c, dtype, out_dtype, n_blocks):
         assert torch.equal(out[~nan.all(1)].view(ints), ref[~nan.all(1)].view(ints))
 
 
+@pytest.mark.parametrize("c,n_blocks,out_a,out_b", [
+    (512, 300, torch.float32, None),      # slab path, in-kernel block lookup
+    (1024, 800, None, torch.float32),     # slab path, lookup table
+    (256, 300, torch.float32, None),      # single-tensor fallback (C % 512 != 0)
+])
+def test_pool2_equals_oracle_and_single_calls(c, n_blocks, out_a, out_b):
+    # keys and values pooled in one launch pair: each output bit for bit the
+    # oracle and the single-tensor entry point, also with empty blocks and
+    # rows outside every block.
+    rng = np.random.default_rng(13)
+    sizes = rng.integers(0, 41, size=n_blocks)
+    sizes[[3, 4, 50]] = 0
+    cu_np = np.concatenate([[19], 19 + np.cumsum(sizes)]).astype(np.int32)
+    n = int(cu_np[-1]) + 7
+    g = torch.Generator().manual_seed(2)
+    xa = torch.randn(n, c, generator=g).to(torch.bfloat16)
+    xb = (3.0 * torch.randn(n, c, generator=g)).to(torch.bfloat16)
+    cu = torch.from_numpy(cu_np).to(DEV)
+    pa, pb = H.block_mean_pool2(xa.to(DEV), xb.to(DEV), cu, out_a, out_b)
+    sa = H.block_mean_pool(xa.to(DEV), cu, out_a)
+    sb = H.block_mean_pool(xb.to(DEV), cu, out_b)
+    for got, single, x, od in ((pa, sa, xa, out_a), (pb, sb, xb, out_b)):
+        ref = torch.from_numpy(block_mean_pool_ref(_f32(x), cu_np)).to(od or torch.bfloat16)
+        ints = torch.int16 if got.element_size() == 2 else torch.int32
+        assert got.dtype == (od or torch.bfloat16)
+        assert torch.equal(got.cpu().view(ints), single.cpu().view(ints))
+        nan = torch.isnan(ref)
+        assert torch.equal(torch.isnan(got.cpu()), nan)
+        assert torch.equal(got.cpu()[~nan.all(1)].view(ints), ref[~nan.all(1)].view(ints))
+
+
+def test_pool2_cfg3_shape_bitexact():
+    w = W.config(3)
+    g = torch.Generator(device=DEV).manual_seed(8)
+    k = (0.5 * torch.randn(w.n, w.hkv * w.d, generator=g, device=DEV)).to(torch.bfloat16)
+    v = torch.randn(w.n, w.hkv * w.d, generator=g, device=DEV).to(torch.bfloat16)
+    cu = w.cu_block_tokens.to(DEV)
+    pk, pv = H.block_mean_pool2(k, v, cu, torch.float32, None)
+    assert torch.equal(pk, H.block_mean_pool(k, cu, torch.float32))
+    assert torch.equal(pv.view(torch.int16), H.block_mean_pool(v, cu).view(torch.int16))
+    ref = torch.from_numpy(block_mean_pool_ref(_f32(v), w.cu_block_tokens.numpy()))
+    assert torch.equal(pv.cpu().view(torch.int16), ref.to(torch.bfloat16).view(torch.int16))
+
+
 def _select_case(w, forced=None, hq=None, hkv=None, dtype=None):
     dtype = dtype or w.dtype
     g = torch.Generator().manual_seed(w.seed)
