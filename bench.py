@@ -44,9 +44,11 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 def event_time_ms(fn, reps: int) -> float:
     """Average ms per call of fn() measured with HIP events on torch's
-    current stream (the stream every lsrm_hip call launches on)."""
+    current stream (the stream every lsrm_hip call launches on), after one
+    untimed call (first-call set-up of an operator stays outside)."""
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    fn()
     torch.cuda.synchronize()
     start.record()
     for _ in range(reps):
@@ -73,7 +75,11 @@ def cpu_baseline(w, q, k, v, topk_idx, flops_per_head_q, budget_s: float):
     """Times the CPU oracle head by head until the budget is spent."""
     from oracle.attention import sel_attn_ref  # the checker, timed as the CPU baseline
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    # The GPU box grants one GPU's job a share of 16 host cores, whatever the
+    # affinity mask lists; the thread count is held to that share and both
+    # figures are reported.
+    affinity = len(os.sched_getaffinity(0))
+    cores = min(affinity, 16)
     torch.set_num_threads(cores)
     cu_sb, cu_blk, cu_q = w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens
     heads, flops, elapsed = 0, 0.0, 0.0
@@ -101,7 +107,8 @@ def cpu_baseline(w, q, k, v, topk_idx, flops_per_head_q, budget_s: float):
         "sample": (f"{w.name}: attention forward of kv heads 0..{heads - 1} of {w.hkv} "
                    f"(all {w.n} queries, same selection) with the fp32 PyTorch oracle, "
                    f"{elapsed:.1f} s; extrapolated full-layer attention "
-                   f"{total_flops / (tflops * 1e12) * 1e3:.0f} ms"),
+                   f"{total_flops / (tflops * 1e12) * 1e3:.0f} ms; {cores} threads = the box's "
+                   f"16-core share per GPU (affinity mask lists {affinity} cores)"),
     }
 
 

@@ -10,6 +10,7 @@ Operators (the reference interface each one stands in for):
   sel_attn_fwd     kvcentric:931-1010   native_sparse_attn_forward -> (o, lse)
   sel_attn_bwd     kvcentric:1018-1263  native_sparse_attn_backward -> (dq, dk, dv, delta)
   block_mean_pool  spatial_sparse_attention.py:27-37  sparse3d_compression
+  block_mean_pool2 spatial_sparse_attention.py:49-66  the key and value pair
   select_blocks    the benchmark's per-query-block selection -> (topk_idx, compact)
   block_score      block_score.py:16-98  get_block_score
   gate_merge       spatial_sparse_attention.py:256-269 (the gated branch sum)
@@ -28,6 +29,7 @@ import torch
 from . import (
     block_ids as _block_ids,
     block_mean_pool as _block_mean_pool,
+    block_mean_pool2 as _block_mean_pool2,
     block_score as _block_score,
     gate_merge as _gate_merge,
     gate_merge_bwd as _gate_merge_bwd,
@@ -106,6 +108,23 @@ def block_mean_pool(x: torch.Tensor, cu_block_tokens: torch.Tensor,
 @block_mean_pool.register_fake
 def _(x, cu_block_tokens, out_dtype=None):
     return x.new_empty((cu_block_tokens.shape[0] - 1, x.shape[1]), dtype=out_dtype or x.dtype)
+
+
+@torch.library.custom_op(f"{NS}::block_mean_pool2", mutates_args=())
+def block_mean_pool2(x_a: torch.Tensor, x_b: torch.Tensor, cu_block_tokens: torch.Tensor,
+                     out_a_dtype: Optional[torch.dtype] = None,
+                     out_b_dtype: Optional[torch.dtype] = None
+                     ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Keys and values of one block partition in one launch pair (each
+    output equals block_mean_pool of its input)."""
+    return _block_mean_pool2(x_a, x_b, cu_block_tokens, out_a_dtype, out_b_dtype)
+
+
+@block_mean_pool2.register_fake
+def _(x_a, x_b, cu_block_tokens, out_a_dtype=None, out_b_dtype=None):
+    nb = cu_block_tokens.shape[0] - 1
+    return (x_a.new_empty((nb, x_a.shape[1]), dtype=out_a_dtype or x_a.dtype),
+            x_b.new_empty((nb, x_b.shape[1]), dtype=out_b_dtype or x_b.dtype))
 
 
 @torch.library.custom_op(f"{NS}::select_blocks", mutates_args=())
@@ -195,5 +214,6 @@ def _gm_backward(ctx, dout):
 
 gate_merge.register_autograd(_gm_backward, setup_context=_gm_setup)
 
-OPS = ("sel_attn_fwd", "sel_attn_bwd", "block_mean_pool", "select_blocks", "block_score",
+OPS = ("sel_attn_fwd", "sel_attn_bwd", "block_mean_pool", "block_mean_pool2", "select_blocks",
+       "block_score",
        "block_ids", "gate_merge", "gate_merge_bwd")

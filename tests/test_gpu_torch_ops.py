@@ -75,6 +75,8 @@ def test_opcheck_operators():
                           (qg, kg, vg, topk, *meta, w.scale))
     torch.library.opcheck(torch.ops.lsrm_hip.block_mean_pool.default,
                           (k.view(w.n, -1), meta[1], torch.float32))
+    torch.library.opcheck(torch.ops.lsrm_hip.block_mean_pool2.default,
+                          (k.view(w.n, -1), v.view(w.n, -1), meta[1], torch.float32, None))
     torch.library.opcheck(torch.ops.lsrm_hip.select_blocks.default,
                           (q, k, meta[0], meta[1], 8, [1], True, None))
     torch.library.opcheck(torch.ops.lsrm_hip.block_ids.default, (meta[0], meta[1], w.n, w.hkv))

@@ -58,6 +58,9 @@ def test_fake_pool_selection_score_shapes():
     assert p.shape == (7, 128) and p.dtype == torch.bfloat16
     p32 = torch.ops.lsrm_hip.block_mean_pool(x, cu_blk, torch.float32)
     assert p32.dtype == torch.float32
+    pa, pb = torch.ops.lsrm_hip.block_mean_pool2(x, x, cu_blk, torch.float32, None)
+    assert pa.shape == pb.shape == (7, 128)
+    assert pa.dtype == torch.float32 and pb.dtype == torch.bfloat16
     t, c = torch.ops.lsrm_hip.select_blocks(q, k, cu_sb, cu_blk, 4, [0, 1], True, None)
     assert t.shape == (2, 300, 4) and c.shape == (2, 7, 4) and t.dtype == torch.int32
     ck = torch.empty(7, 2, 64, dtype=torch.bfloat16, device=META)
