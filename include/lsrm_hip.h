@@ -259,6 +259,52 @@ int lsrm_sel_attn_fwd_run(const void* q, const void* k, const void* v,
                           void* stream);
 
 /* ------------------------------------------------------------------------
+ * Plans with flags.  LSRM_PLAN_BACKWARD is the backward != 0 of the calls
+ * above.  LSRM_PLAN_KEY_CENTRIC adds the key-centric forward for per-token
+ * rows without locality (for example learned selections): query tiles of
+ * consecutive queries whose rows differ and whose union of blocks cannot
+ * be run in one masked pass are taken out of the grouped-tile pass; for
+ * every block, the queries that listed it are gathered into tiles of up to
+ * 128 rows that attend that block alone, each writing a partial result
+ * (O over the block normalised by its own sum, in the input type, and the
+ * log2 LSE); a merge combines each query's partials in the order of its
+ * top-k row (M = max LSE_j, W = sum 2^(LSE_j - M), O = sum 2^(LSE_j - M)
+ * O_j / W, LSE = M + log2 W).  Results agree with the other paths to
+ * rounding and are bitwise repeatable run to run (no float atomics).  The
+ * workspace then also holds the partials: hq * n_q * topk * (head_dim * 2
+ * + 4) bytes at most, which is why the part is opt-in.  The key-centric
+ * part is carved after the others, so lsrm_sel_attn_fwd_run and
+ * lsrm_sel_attn_bwd_run accept such a workspace (the former then runs the
+ * flagged tiles in the grouped-tile pass); lsrm_sel_attn_fwd_run2 with the
+ * plan's flags runs the key-centric pass.  head_dim sizes the partials
+ * (ignored without LSRM_PLAN_KEY_CENTRIC).
+ * Replaces: ..._impl_kvcentric.py:931-1010 for per-token rows (the
+ * reference has no key-centric forward; the queries of a block are the
+ * reverse map of 575-684, which its backward builds).
+ * ---------------------------------------------------------------------- */
+#define LSRM_PLAN_BACKWARD 1
+#define LSRM_PLAN_KEY_CENTRIC 2
+size_t lsrm_sel_attn_workspace_size2(int64_t n_q, int64_t n_k, int64_t hq,
+                                     int64_t hkv, int64_t head_dim,
+                                     int64_t topk, int64_t n_blocks, int flags);
+int lsrm_sel_attn_plan2(const int32_t* topk_idx, int64_t n_q, int64_t n_k,
+                        int64_t hq, int64_t hkv, int64_t head_dim,
+                        int64_t topk, const int32_t* cu_seqblocks,
+                        const int32_t* cu_block_tokens, int64_t n_blocks,
+                        const int32_t* cu_seqlens_q, int64_t batch, int flags,
+                        void* workspace, size_t workspace_bytes, void* stream);
+int lsrm_sel_attn_fwd_run2(const void* q, const void* k, const void* v,
+                           int dtype, int64_t n_q, int64_t n_k, int64_t hq,
+                           int64_t hkv, int64_t head_dim,
+                           const int32_t* topk_idx, int64_t topk,
+                           const int32_t* cu_seqblocks,
+                           const int32_t* cu_block_tokens, int64_t n_blocks,
+                           const int32_t* cu_seqlens_q, int64_t batch,
+                           float softmax_scale, void* out, float* lse,
+                           void* workspace, size_t workspace_bytes, int flags,
+                           void* stream);
+
+/* ------------------------------------------------------------------------
  * Selected-block attention, backward.  Inputs as for the forward plus
  * dout [n_q, hq, head_dim] and the forward's out and lse.  Writes
  * dq [n_q, hq, head_dim], dk/dv [n_k, hkv, head_dim] (dtype) and

@@ -42,6 +42,7 @@ struct AttnArgs {
   RevMap qrev;       // backward: block -> queries of grouped tiles that
                      // selected it (one entry per listing, ascending)
   KeyItems items;    // backward: key chunks of every block
+  KcPlan kc;         // forward, key-centric plans only (kc.items null otherwise)
 };
 
 // Compile-time value tag (e.g. a ring-slot phase).
@@ -116,6 +117,31 @@ __device__ inline void load_selection(const AttnArgs& a, int h, int64_t q,
       s.cum[cn + 1] = 0x7fffffff;
       s.tb[cn] = 0;
       s.n = cn;
+    }
+  }
+  __syncthreads();
+}
+
+// All 256 threads: the key stream of one block (global id c, token range
+// clamped as load_selection does), for the gathered tiles of key-centric
+// plans.
+__device__ inline void load_block(const AttnArgs& a, int c, SelLds& s) {
+  if (threadIdx.x == 0) {
+    int64_t s0 = a.cu_blk[c], s1 = a.cu_blk[c + 1];
+    s0 = s0 < 0 ? 0 : (s0 > a.nk ? a.nk : s0);
+    s1 = s1 < s0 ? s0 : (s1 > a.nk ? a.nk : s1);
+    s.cum[0] = 0;
+    if (s1 > s0) {
+      s.tok[0] = (int)s0;
+      s.tb[0] = (int)s0;
+      s.cum[1] = (int)(s1 - s0);
+      s.cum[2] = 0x7fffffff;
+      s.tb[1] = 0;
+      s.n = 1;
+    } else {
+      s.cum[1] = 0x7fffffff;
+      s.tb[0] = 0;
+      s.n = 0;
     }
   }
   __syncthreads();
@@ -428,6 +454,8 @@ __device__ inline int head_of(const int32_t* head_off, int hkv, int w) {
 
 // Persistent-grid size for a kernel: CUs x resident workgroups per CU.
 int persistent_grid(const void* kernel, int block, size_t dyn_lds);
+// Key-centric plans: flags the grouped tiles left to the gathered pass.
+int launch_kc_flags(const AttnArgs& a, uint8_t* gflag, hipStream_t st);
 
 // ------------------------------------------------ LDS tile streaming --
 // Shared by the forward and backward kernels: 16-byte global -> LDS copies,

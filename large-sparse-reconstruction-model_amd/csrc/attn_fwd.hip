@@ -65,13 +65,22 @@ __device__ inline float row_max(const f32x16* sc) {
                                        __builtin_bit_cast(float, (unsigned)sw[1]));
 }
 
-// UNION false: the run tiles of the plan (every row of a tile shares one
-// key stream).  UNION true: the grouped tiles (see build_union), run with
-// per-row key masks; a separate instantiation so that the run-tile kernel
-// carries none of that code or state.
-template <int DT, int D, bool UNION>
+// MODE 0 (FWD_RUN): the run tiles of the plan (every row of a tile shares
+// one key stream).  MODE 1 (FWD_UNION): the grouped tiles (see build_union),
+// run with per-row key masks; in a key-centric plan the flagged ones are
+// left to mode 2.  MODE 2 (FWD_GATHER): gathered tiles of a key-centric plan
+// -- the queries that listed one block, attending that block alone, each row
+// written as a partial result (O over the block normalised by its own sum,
+// in the input type, and its log2 LSE) for kc_merge_kernel.  Separate
+// instantiations, so the run-tile kernel carries none of the other modes'
+// code or state.
+constexpr int FWD_RUN = 0, FWD_UNION = 1, FWD_GATHER = 2;
+
+template <int DT, int D, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 sel_attn_fwd_kernel(AttnArgs a) {
+  constexpr bool UNION = MODE == FWD_UNION;
+  constexpr bool GATHER = MODE == FWD_GATHER;
   using G = KvTile<D>;
   constexpr int NS = D / 16;  // MFMA k-steps over the head dim
   constexpr int ND = D / 32;  // 32-wide output blocks over the head dim
@@ -83,9 +92,10 @@ sel_attn_fwd_kernel(AttnArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
-  const int32_t* head_off = UNION ? a.plan.ghead_off : a.plan.head_off;
+  const int32_t* head_off =
+      GATHER ? a.kc.item_off : (UNION ? a.plan.ghead_off : a.plan.head_off);
   const int2* tiles = UNION ? a.plan.gtiles : a.plan.tiles;
-  int32_t* queue = a.plan.counter + (UNION ? 4 : 0);
+  int32_t* queue = a.plan.counter + (GATHER ? KC_QUEUE_SLOT : (UNION ? 4 : 0));
   const int total = head_off[a.hkv];
 
   // Loader geometry: load j of this wave covers keys (wv*LPW + j)*KPL + ...
@@ -107,8 +117,26 @@ sel_attn_fwd_kernel(AttnArgs a) {
     const int w = uniform(fetch_work(queue, &s_slot));
     if (w >= total) break;
     const int h = head_of(head_off, a.hkv, w);
-    const int2 tile = tiles[(int64_t)h * a.nq + (w - head_off[h])];
-    const int q0 = tile.x, qn = tile.y, rows = qn * a.g;
+    int q0, qn, gblk = 0, ge0 = 0;
+    if constexpr (GATHER) {
+      const int4 it = a.kc.items[(int64_t)h * a.kc.item_cap + (w - head_off[h])];
+      gblk = it.x;
+      ge0 = it.y;
+      q0 = 0;
+      qn = it.z;
+    } else {
+      // Key-centric plans: flagged grouped tiles belong to the gathered pass.
+      if constexpr (UNION) {
+        if (a.kc.gflag && a.kc.gflag[(int64_t)h * a.nq + (w - head_off[h])]) {
+          __syncthreads();  // every wave has read s_slot before it is reused
+          continue;
+        }
+      }
+      const int2 tile = tiles[(int64_t)h * a.nq + (w - head_off[h])];
+      q0 = tile.x;
+      qn = tile.y;
+    }
+    const int rows = qn * a.g;
     // Passes over the tile: umode 0 -- one key stream shared by every row
     // (a run tile); umode 1 -- a grouped tile run once over the union of
     // its rows' blocks, each row masked to the blocks it selected; umode 2
@@ -120,6 +148,8 @@ sel_attn_fwd_kernel(AttnArgs a) {
       build_union(a, h, q0, qn, sel, ul);
       umode = ul.ok ? 1 : 2;
       n_pass = ul.ok ? 1 : ul.n_runs;
+    } else if constexpr (GATHER) {
+      load_block(a, gblk, sel);
     } else {
       load_selection(a, h, q0, sel);
     }
@@ -142,7 +172,16 @@ sel_attn_fwd_kernel(AttnArgs a) {
     const int qr = row_ok ? r / a.g : 0;  // the row's query within the tile
     const bool row_in_pass = row_ok && qr >= q_lo && qr < q_hi;
     const bool wave_on = wv * 32 < q_hi * a.g && wv * 32 + 32 > q_lo * a.g;
-    const int64_t qi = q0 + (row_ok ? r / a.g : 0);
+    // Gathered tiles: row r is listing ge0 + r / g of the block's segment,
+    // which stores query * topk + slot.
+    int64_t qi, gslot = 0;
+    if constexpr (GATHER) {
+      const int64_t lv = a.kc.grev.rev[(int64_t)h * a.kc.grev.cap + ge0 + (row_ok ? r / a.g : 0)];
+      qi = lv / a.topk_n;
+      gslot = lv - qi * a.topk_n;
+    } else {
+      qi = q0 + (row_ok ? r / a.g : 0);
+    }
     const int hh = h * a.g + (row_ok ? r % a.g : 0);
     u32x4 qb[NS];
 #pragma unroll
@@ -545,11 +584,13 @@ sel_attn_fwd_kernel(AttnArgs a) {
       run(Phase<1>{});
     }
 
-    // Epilogue: normalise, store O rows and LSE.
+    // Epilogue: normalise, store O rows and LSE (gathered tiles: the
+    // partial result of the row's listing).
     const float l_tot = l_run + __shfl_xor(l_run, 32);
     if (row_in_pass) {
       const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-      uint16_t* orow = a.out + (qi * a.hq + hh) * D;
+      const int64_t pidx = (((int64_t)h * a.nq + qi) * a.topk_n + gslot) * a.g + (r % a.g);
+      uint16_t* orow = GATHER ? a.kc.part_o + pidx * D : a.out + (qi * a.hq + hh) * D;
 #pragma unroll
       for (int db = 0; db < ND; ++db)
 #pragma unroll
@@ -559,9 +600,13 @@ sel_attn_fwd_kernel(AttnArgs a) {
               u32x2{pack2<DT>(oacc[db][v] * inv, oacc[db][v + 1] * inv),
                     pack2<DT>(oacc[db][v + 2] * inv, oacc[db][v + 3] * inv)};
         }
-      if (hb == 0)
-        a.lse[(int64_t)hh * a.nq + qi] =
-            l_tot > 0.0f ? m_run + log2f(l_tot) : -__builtin_inf();
+      if (hb == 0) {
+        const float lse_row = l_tot > 0.0f ? m_run + log2f(l_tot) : -__builtin_inf();
+        if constexpr (GATHER)
+          a.kc.part_lse[pidx] = lse_row;
+        else
+          a.lse[(int64_t)hh * a.nq + qi] = lse_row;
+      }
     }
     if (n_pass > 1) {
       wait_copies();  // this pass's trailing copies land before the next pass
@@ -573,19 +618,111 @@ sel_attn_fwd_kernel(AttnArgs a) {
   leave_queue(queue, queue + 2);
 }
 
+// Plan step of key-centric plans: gflag[h, t] = 1 for the grouped tiles
+// whose union cannot run in one masked pass (build_union's ok is false:
+// more than MAXSEL union blocks, a row listing a block twice, or a union
+// longer than the runs' own streams together).  One workgroup per tile.
+__global__ __launch_bounds__(256) void kc_flag_kernel(AttnArgs a, uint8_t* gflag) {
+  __shared__ SelLds sel;
+  __shared__ UnionLds ul;
+  const int total = a.plan.ghead_off[a.hkv];
+  for (int w = blockIdx.x; w < total; w += gridDim.x) {
+    const int h = head_of(a.plan.ghead_off, a.hkv, w);
+    const int t = w - a.plan.ghead_off[h];
+    const int2 tile = a.plan.gtiles[(int64_t)h * a.nq + t];
+    build_union(a, h, tile.x, tile.y, sel, ul);
+    if (threadIdx.x == 0) gflag[(int64_t)h * a.nq + t] = ul.ok ? 0 : 1;
+    __syncthreads();  // ul.ok read before the next tile rebuilds the LDS
+  }
+}
+
+int launch_kc_flags(const AttnArgs& a, uint8_t* gflag, hipStream_t st) {
+  hipLaunchKernelGGL(kc_flag_kernel, dim3(2048), dim3(256), 0, st, a, gflag);
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
+}
+
+// Key-centric merge: one thread per (kv head, query, query head, 4 output
+// channels) of the marked queries.  The partials of the row's valid slots
+// (the gathered tiles wrote one per slot naming a block) are combined in
+// slot order: M = max LSE_j, W = sum 2^(LSE_j - M), O = sum 2^(LSE_j - M)
+// O_j / W, LSE = M + log2 W.  A row without a partial that attended a key
+// gives O = 0 and LSE = -inf.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void kc_merge_kernel(AttnArgs a) {
+  constexpr int CPT = 4;  // output channels per thread
+  const int64_t per_q = (int64_t)a.g * (D / CPT);
+  const int64_t n_items = (int64_t)a.hkv * a.nq * per_q;
+  for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
+       it += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t hq_idx = it / per_q;  // h * nq + q
+    if (!a.kc.qmark[hq_idx]) continue;
+    const int sub = (int)(it - hq_idx * per_q);
+    const int gi = sub / (D / CPT), d0 = (sub % (D / CPT)) * CPT;
+    const int h = (int)(hq_idx / a.nq);
+    const int64_t q = hq_idx - (int64_t)h * a.nq;
+    int b, bs, nbb;
+    bool st;
+    query_batch(a.cu_q, a.batch, a.cu_sb, q, &b, &bs, &nbb, &st);
+    const int32_t* row = a.topk + hq_idx * a.topk_n;
+    const int64_t pbase = hq_idx * a.topk_n;  // partial (q, slot 0)
+    float mx = -__builtin_inf();
+    for (int j = 0; j < a.topk_n; ++j) {
+      const int v = row[j];
+      if (v >= 0 && v < nbb && (int64_t)bs + v < a.nb)
+        mx = __builtin_elementwise_maximum(mx, a.kc.part_lse[(pbase + j) * a.g + gi]);
+    }
+    float acc[CPT] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float wsum = 0.0f;
+    if (mx > -__builtin_inf()) {
+      for (int j = 0; j < a.topk_n; ++j) {
+        const int v = row[j];
+        if (!(v >= 0 && v < nbb && (int64_t)bs + v < a.nb)) continue;
+        const int64_t pidx = (pbase + j) * a.g + gi;
+        const float wj = __builtin_amdgcn_exp2f(a.kc.part_lse[pidx] - mx);
+        const u32x2 ov = *reinterpret_cast<const u32x2*>(a.kc.part_o + pidx * D + d0);
+        wsum += wj;
+        acc[0] += wj * to_f32<DT>((uint16_t)(ov[0] & 0xffffu));
+        acc[1] += wj * to_f32<DT>((uint16_t)(ov[0] >> 16));
+        acc[2] += wj * to_f32<DT>((uint16_t)(ov[1] & 0xffffu));
+        acc[3] += wj * to_f32<DT>((uint16_t)(ov[1] >> 16));
+      }
+    }
+    const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+    const int hh = h * a.g + gi;
+    *reinterpret_cast<u32x2*>(a.out + (q * a.hq + hh) * D + d0) =
+        u32x2{pack2<DT>(acc[0] * inv, acc[1] * inv), pack2<DT>(acc[2] * inv, acc[3] * inv)};
+    if (d0 == 0)
+      a.lse[(int64_t)hh * a.nq + q] = wsum > 0.0f ? mx + log2f(wsum) : -__builtin_inf();
+  }
+}
+
 template <int DT, int D>
 int launch_fwd_t(const AttnArgs& a, hipStream_t st) {
-  const void* fn = reinterpret_cast<const void*>(&sel_attn_fwd_kernel<DT, D, false>);
+  const void* fn = reinterpret_cast<const void*>(&sel_attn_fwd_kernel<DT, D, FWD_RUN>);
   const int grid = persistent_grid(fn, 256, 0);
   if (grid <= 0) return LSRM_ERR_LAUNCH;
-  hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, false>), dim3(grid), dim3(256), 0, st,
+  hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, FWD_RUN>), dim3(grid), dim3(256), 0, st,
                      a);
   LSRM_CHECK_LAUNCH();
   if (a.plan.gtiles) {  // forward plans: the grouped tiles (often none)
-    const void* fu = reinterpret_cast<const void*>(&sel_attn_fwd_kernel<DT, D, true>);
+    const void* fu = reinterpret_cast<const void*>(&sel_attn_fwd_kernel<DT, D, FWD_UNION>);
     const int gu = persistent_grid(fu, 256, 0);
     if (gu <= 0) return LSRM_ERR_LAUNCH;
-    hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, true>), dim3(gu), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, FWD_UNION>), dim3(gu), dim3(256), 0, st,
+                       a);
+    LSRM_CHECK_LAUNCH();
+  }
+  if (a.kc.items) {  // key-centric plans: gathered tiles, then the merge
+    const void* fg = reinterpret_cast<const void*>(&sel_attn_fwd_kernel<DT, D, FWD_GATHER>);
+    const int gg = persistent_grid(fg, 256, 0);
+    if (gg <= 0) return LSRM_ERR_LAUNCH;
+    hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, FWD_GATHER>), dim3(gg), dim3(256), 0, st,
+                       a);
+    LSRM_CHECK_LAUNCH();
+    const int gm = device_cu_count() * 16;
+    if (gm <= 0) return LSRM_ERR_LAUNCH;
+    hipLaunchKernelGGL((kc_merge_kernel<DT, D>), dim3(gm), dim3(256), 0, st, a);
     LSRM_CHECK_LAUNCH();
   }
   return LSRM_OK;

@@ -56,14 +56,20 @@ struct AttnWs {
   RevMap rev;
   RevMap qrev;
   KeyItems items;
+  KcPlan kc;
 };
 
 // Carves (or sizes, when ws.base is null) the attention workspace and builds
-// the plan on the stream.
+// the plan on the stream.  flags: LSRM_PLAN_BACKWARD adds the backward part,
+// LSRM_PLAN_KEY_CENTRIC the key-centric forward part (carved last, so that
+// the entry points without flags find the other parts where they expect
+// them); head_dim sizes the key-centric partial results.
 int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
               int64_t hkv, int64_t topk_n, const int32_t* cu_sb,
               const int32_t* cu_blk, int64_t nb, const int32_t* cu_q,
-              int64_t batch, int g, bool backward, AttnWs& w, hipStream_t st) {
+              int64_t batch, int g, int flags, int64_t head_dim, AttnWs& w,
+              hipStream_t st) {
+  const bool backward = (flags & LSRM_PLAN_BACKWARD) != 0;
   const int tq = ROWS / g;
   int rc = build_tile_plan(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, tq, ws,
                            w.plan, st, true);
@@ -94,6 +100,45 @@ int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
       rc = mark_backward_plan(w.plan.counter, st);
       if (rc) return rc;
     }
+  }
+  w.kc = KcPlan{};
+  if (flags & LSRM_PLAN_KEY_CENTRIC) {
+    KcPlan& kc = w.kc;
+    const size_t qwords = (size_t)((hkv * nq + 3) / 4 > 0 ? (hkv * nq + 3) / 4 : 1);
+    kc.gflag = reinterpret_cast<uint8_t*>(ws.take<int32_t>(qwords));
+    kc.qmark = reinterpret_cast<uint8_t*>(ws.take<int32_t>(qwords));
+    if (ws.base && !ws.dry) {
+      if (!ws.ok()) return LSRM_ERR_WORKSPACE;
+      AttnArgs fa{};
+      fa.topk = topk;
+      fa.cu_sb = cu_sb;
+      fa.cu_blk = cu_blk;
+      fa.cu_q = cu_q;
+      fa.nb = nb;
+      fa.batch = batch;
+      fa.nq = nq;
+      fa.nk = nk;
+      fa.topk_n = (int)topk_n;
+      fa.hkv = (int)hkv;
+      fa.hq = (int)hkv * g;
+      fa.g = g;
+      fa.plan = w.plan;
+      rc = launch_kc_flags(fa, kc.gflag, st);
+      if (rc) return rc;
+      rc = mark_flagged_queries(w.plan, kc.gflag, hkv, nq, kc.qmark, st);
+      if (rc) return rc;
+    }
+    kc.grev = RevMap{};
+    kc.grev.cap = nq * topk_n;
+    rc = build_reverse_map(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, nb, false, nullptr,
+                           ws, kc.grev, st, kc.qmark, true);
+    if (rc) return rc;
+    rc = build_kc_items(kc.grev, hkv, nb, tq, ws, kc, w.plan.counter, st);
+    if (rc) return rc;
+    const size_t parts = (size_t)(hkv * (kc.grev.cap > 0 ? kc.grev.cap : 1) * g);
+    kc.part_o = ws.take<uint16_t>(parts * (size_t)(head_dim > 0 ? head_dim : 1));
+    kc.part_lse = ws.take<float>(parts);
+    if (ws.base && !ws.ok()) return LSRM_ERR_WORKSPACE;
   }
   return LSRM_OK;
 }
@@ -138,18 +183,26 @@ extern "C" const char* lsrm_status_string(int status) {
 
 extern "C" int lsrm_version(void) { return 100; }
 
-extern "C" size_t lsrm_sel_attn_workspace_size(int64_t n_q, int64_t n_k,
-                                               int64_t hq, int64_t hkv,
-                                               int64_t topk, int64_t n_blocks,
-                                               int backward) {
+extern "C" size_t lsrm_sel_attn_workspace_size2(int64_t n_q, int64_t n_k, int64_t hq,
+                                                int64_t hkv, int64_t head_dim, int64_t topk,
+                                                int64_t n_blocks, int flags) {
   if (n_q < 0 || n_k < 0 || hq <= 0 || hkv <= 0 || topk <= 0 || n_blocks < 0 ||
-      hq % hkv != 0)
+      hq % hkv != 0 || (flags & ~(LSRM_PLAN_BACKWARD | LSRM_PLAN_KEY_CENTRIC)) != 0 ||
+      ((flags & LSRM_PLAN_KEY_CENTRIC) && head_dim <= 0))
     return 0;
   Carver ws{nullptr, 0, 0};
   AttnWs w{};
   attn_plan(ws, nullptr, n_q, n_k, hkv, topk, nullptr, nullptr, n_blocks,
-            nullptr, 1, (int)(hq / hkv), backward != 0, w, nullptr);
+            nullptr, 1, (int)(hq / hkv), flags, head_dim, w, nullptr);
   return ws.used + 256;
+}
+
+extern "C" size_t lsrm_sel_attn_workspace_size(int64_t n_q, int64_t n_k,
+                                               int64_t hq, int64_t hkv,
+                                               int64_t topk, int64_t n_blocks,
+                                               int backward) {
+  return lsrm_sel_attn_workspace_size2(n_q, n_k, hq, hkv, 0, topk, n_blocks,
+                                       backward ? LSRM_PLAN_BACKWARD : 0);
 }
 
 namespace {
@@ -162,9 +215,10 @@ int attn_setup(const void* q, const void* k, const void* v, int dtype,
                int64_t head_dim, const int32_t* topk_idx, int64_t topk,
                const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
                int64_t n_blocks, const int32_t* cu_seqlens_q, int64_t batch,
-               float softmax_scale, bool backward, bool plan,
+               float softmax_scale, int flags, bool plan,
                void* workspace, size_t workspace_bytes, hipStream_t st,
                AttnArgs& a) {
+  const bool backward = (flags & LSRM_PLAN_BACKWARD) != 0;
   int rc = check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk, n_blocks,
                            batch);
   if (rc) return rc;
@@ -177,24 +231,24 @@ int attn_setup(const void* q, const void* k, const void* v, int dtype,
       !cu_seqlens_q || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
       !(softmax_scale > 0.0f))
     return LSRM_ERR_INVALID_ARG;
-  const size_t need = lsrm_sel_attn_workspace_size(n_q, n_k, hq, hkv, topk,
-                                                   n_blocks, backward ? 1 : 0);
-  if (workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
+  const size_t need = lsrm_sel_attn_workspace_size2(n_q, n_k, hq, hkv, head_dim, topk,
+                                                    n_blocks, flags);
+  if (need == 0 || workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
   Carver ws{reinterpret_cast<char*>(align_up((size_t)workspace, 256)), 0,
             workspace_bytes - 256};
   const int g = (int)(hq / hkv);
   AttnWs w{};
   if (plan) {
     rc = attn_plan(ws, topk_idx, n_q, n_k, hkv, topk, cu_seqblocks,
-                   cu_block_tokens, n_blocks, cu_seqlens_q, batch, g, backward,
-                   w, st);
+                   cu_block_tokens, n_blocks, cu_seqlens_q, batch, g, flags,
+                   head_dim, w, st);
     if (rc) return rc;
   } else {
     // Same carving, no launches: recover the plan built earlier.
     Carver dry{ws.base, 0, ws.cap, true};
     rc = attn_plan(dry, topk_idx, n_q, n_k, hkv, topk, cu_seqblocks,
-                   cu_block_tokens, n_blocks, cu_seqlens_q, batch, g, backward,
-                   w, st);
+                   cu_block_tokens, n_blocks, cu_seqlens_q, batch, g, flags,
+                   head_dim, w, st);
     if (rc) return rc;
     if (!dry.ok()) return LSRM_ERR_WORKSPACE;
   }
@@ -220,31 +274,45 @@ int attn_setup(const void* q, const void* k, const void* v, int dtype,
   a.rev = w.rev;
   a.qrev = w.qrev;
   a.items = w.items;
+  a.kc = w.kc;
   return LSRM_OK;
 }
 
 }  // namespace
 
-extern "C" int lsrm_sel_attn_plan(
+extern "C" int lsrm_sel_attn_plan2(
     const int32_t* topk_idx, int64_t n_q, int64_t n_k, int64_t hq, int64_t hkv,
-    int64_t topk, const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
-    int64_t n_blocks, const int32_t* cu_seqlens_q, int64_t batch, int backward,
-    void* workspace, size_t workspace_bytes, void* stream) {
-  int rc = check_attn_args(LSRM_BF16, n_q, n_k, hq, hkv, 64, topk, n_blocks,
-                           batch);
+    int64_t head_dim, int64_t topk, const int32_t* cu_seqblocks,
+    const int32_t* cu_block_tokens, int64_t n_blocks, const int32_t* cu_seqlens_q,
+    int64_t batch, int flags, void* workspace, size_t workspace_bytes, void* stream) {
+  const bool kc = (flags & LSRM_PLAN_KEY_CENTRIC) != 0;
+  int rc = check_attn_args(LSRM_BF16, n_q, n_k, hq, hkv, kc ? head_dim : 64, topk,
+                           n_blocks, batch);
   if (rc) return rc;
   if (n_q == 0) return LSRM_OK;
   if (!topk_idx || !cu_seqblocks || !cu_block_tokens || !cu_seqlens_q)
     return LSRM_ERR_INVALID_ARG;
-  const size_t need = lsrm_sel_attn_workspace_size(n_q, n_k, hq, hkv, topk,
-                                                   n_blocks, backward ? 1 : 0);
+  const size_t need = lsrm_sel_attn_workspace_size2(n_q, n_k, hq, hkv, head_dim, topk,
+                                                    n_blocks, flags);
+  if (need == 0) return LSRM_ERR_INVALID_ARG;
   if (workspace_bytes < need || !workspace) return LSRM_ERR_WORKSPACE;
   Carver ws{reinterpret_cast<char*>(align_up((size_t)workspace, 256)), 0,
             workspace_bytes - 256};
   AttnWs w{};
   return attn_plan(ws, topk_idx, n_q, n_k, hkv, topk, cu_seqblocks,
                    cu_block_tokens, n_blocks, cu_seqlens_q, batch,
-                   (int)(hq / hkv), backward != 0, w, (hipStream_t)stream);
+                   (int)(hq / hkv), flags, head_dim, w, (hipStream_t)stream);
+}
+
+extern "C" int lsrm_sel_attn_plan(
+    const int32_t* topk_idx, int64_t n_q, int64_t n_k, int64_t hq, int64_t hkv,
+    int64_t topk, const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
+    int64_t n_blocks, const int32_t* cu_seqlens_q, int64_t batch, int backward,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  return lsrm_sel_attn_plan2(topk_idx, n_q, n_k, hq, hkv, 0, topk, cu_seqblocks,
+                             cu_block_tokens, n_blocks, cu_seqlens_q, batch,
+                             backward ? LSRM_PLAN_BACKWARD : 0, workspace, workspace_bytes,
+                             stream);
 }
 
 static int fwd_impl(const void* q, const void* k, const void* v, int dtype,
@@ -254,7 +322,7 @@ static int fwd_impl(const void* q, const void* k, const void* v, int dtype,
                     int64_t n_blocks, const int32_t* cu_seqlens_q,
                     int64_t batch, float softmax_scale, void* out, float* lse,
                     void* workspace, size_t workspace_bytes, void* stream,
-                    bool plan) {
+                    bool plan, int flags) {
   const int arc = check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk,
                                   n_blocks, batch);
   if (arc || n_q == 0) return arc;
@@ -263,7 +331,7 @@ static int fwd_impl(const void* q, const void* k, const void* v, int dtype,
   AttnArgs a;
   int rc = attn_setup(q, k, v, dtype, n_q, n_k, hq, hkv, head_dim, topk_idx,
                       topk, cu_seqblocks, cu_block_tokens, n_blocks,
-                      cu_seqlens_q, batch, softmax_scale, false, plan,
+                      cu_seqlens_q, batch, softmax_scale, flags, plan,
                       workspace, workspace_bytes, st, a);
   if (rc) return rc;
   a.out = static_cast<uint16_t*>(out);
@@ -281,7 +349,7 @@ extern "C" int lsrm_sel_attn_fwd(
   return fwd_impl(q, k, v, dtype, n_q, n_k, hq, hkv, head_dim, topk_idx, topk,
                   cu_seqblocks, cu_block_tokens, n_blocks, cu_seqlens_q, batch,
                   softmax_scale, out, lse, workspace, workspace_bytes, stream,
-                  true);
+                  true, 0);
 }
 
 extern "C" int lsrm_sel_attn_fwd_run(
@@ -294,7 +362,22 @@ extern "C" int lsrm_sel_attn_fwd_run(
   return fwd_impl(q, k, v, dtype, n_q, n_k, hq, hkv, head_dim, topk_idx, topk,
                   cu_seqblocks, cu_block_tokens, n_blocks, cu_seqlens_q, batch,
                   softmax_scale, out, lse, workspace, workspace_bytes, stream,
-                  false);
+                  false, 0);
+}
+
+extern "C" int lsrm_sel_attn_fwd_run2(
+    const void* q, const void* k, const void* v, int dtype, int64_t n_q,
+    int64_t n_k, int64_t hq, int64_t hkv, int64_t head_dim,
+    const int32_t* topk_idx, int64_t topk, const int32_t* cu_seqblocks,
+    const int32_t* cu_block_tokens, int64_t n_blocks,
+    const int32_t* cu_seqlens_q, int64_t batch, float softmax_scale, void* out,
+    float* lse, void* workspace, size_t workspace_bytes, int flags, void* stream) {
+  if ((flags & ~(LSRM_PLAN_BACKWARD | LSRM_PLAN_KEY_CENTRIC)) != 0)
+    return LSRM_ERR_INVALID_ARG;
+  return fwd_impl(q, k, v, dtype, n_q, n_k, hq, hkv, head_dim, topk_idx, topk,
+                  cu_seqblocks, cu_block_tokens, n_blocks, cu_seqlens_q, batch,
+                  softmax_scale, out, lse, workspace, workspace_bytes, stream,
+                  false, flags);
 }
 
 static int bwd_impl(const void* dout, const void* q, const void* k,
@@ -318,7 +401,7 @@ static int bwd_impl(const void* dout, const void* q, const void* k,
   AttnArgs a;
   int rc = attn_setup(q, k, v, dtype, n_q, n_k, hq, hkv, head_dim, topk_idx,
                       topk, cu_seqblocks, cu_block_tokens, n_blocks,
-                      cu_seqlens_q, batch, softmax_scale, true, plan,
+                      cu_seqlens_q, batch, softmax_scale, LSRM_PLAN_BACKWARD, plan,
                       workspace, workspace_bytes, st, a);
   if (rc) return rc;
   a.o = static_cast<const uint16_t*>(out);

@@ -50,15 +50,46 @@ int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
 // rows_are_tiles: rows are the tiles of `plan` (row r of head h reads the
 // selection of query tiles[h*nq + r].x); otherwise rows are queries, and
 // with `only` (a [hkv, nq] byte mask) only the queries it marks.
+// encode_slot (rows are queries): a listing stores q * topk_n + j, j the
+// slot of the row that lists the block (ascending order is unchanged).
 int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
                       int64_t topk_n, const int32_t* cu_q, int64_t batch,
                       const int32_t* cu_sb, int64_t nb, bool rows_are_tiles,
                       const TilePlan* plan, Carver& ws, RevMap& map,
-                      hipStream_t st, const uint8_t* only = nullptr);
+                      hipStream_t st, const uint8_t* only = nullptr,
+                      bool encode_slot = false);
 
 // flags[h, q] = 1 for the queries of the grouped tiles of `plan`, else 0.
 int mark_grouped_queries(const TilePlan& plan, int64_t hkv, int64_t nq,
                          uint8_t* flags, hipStream_t st);
+
+// Key-centric forward part of a plan (plan flag LSRM_PLAN_KEY_CENTRIC): the
+// grouped tiles whose union cannot be run in one pass (flag 1) are taken out
+// of the grouped-tile kernel; their queries are listed per block (`grev`,
+// ascending, one listing q * topk + j per slot j that names the block), and
+// each block's list is cut into gathered tiles of at most ROWS / g queries:
+// item {c, e0, n, 0} = block c, listings e0 .. e0 + n of grev's segment of
+// head h.  The forward writes one partial result per (query, slot, query
+// head) -- O normalised by its own row sum in the input type and its log2
+// LSE -- and a merge pass combines each query's partials in slot order.
+struct KcPlan {
+  uint8_t* gflag;        // [hkv, n_q] per grouped tile (index as gtiles)
+  uint8_t* qmark;        // [hkv, n_q] queries of flagged tiles
+  RevMap grev;           // block -> marked queries, cap = n_q * topk per head
+  int4* items;           // [hkv, item_cap]
+  int64_t item_cap;
+  int32_t* item_count;   // [hkv]
+  int32_t* item_off;     // [hkv + 1]
+  uint16_t* part_o;      // [hkv, n_q, topk, g, D] input type
+  float* part_lse;       // [hkv, n_q, topk, g]
+};
+// Work counters of the gathered-tile kernel inside TilePlan::counter.
+constexpr int KC_QUEUE_SLOT = 16, KC_EXIT_SLOT = 18;
+
+int build_kc_items(const RevMap& grev, int64_t hkv, int64_t nb, int tq, Carver& ws,
+                   KcPlan& kc, int32_t* counter, hipStream_t st);
+int mark_flagged_queries(const TilePlan& plan, const uint8_t* gflag, int64_t hkv,
+                         int64_t nq, uint8_t* qmark, hipStream_t st);
 
 // Key chunks of at most KEY_CHUNK tokens inside each block (head
 // independent): item i = (block, first token, length) packed in an int4

@@ -339,7 +339,7 @@ __global__ void plan_offsets_kernel(const int32_t* n_groups, int32_t* tile_count
       head_off[h + 1] = acc;
       ghead_off[h + 1] = gacc;
     }
-    for (int i = 0; i < 16; ++i) counter[i] = 0;
+    for (int i = 0; i < PLAN_BWD_SLOT; ++i) counter[i] = 0;
     counter[PLAN_BWD_SLOT] = 0;  // set again by mark_backward_plan
   }
 }
@@ -433,9 +433,12 @@ struct RowSrc {
   const int32_t* count;   // rows per head (tiles) or null
   int64_t nq;
   const uint8_t* only;    // rows are queries: [hkv, nq] mask, or null (all)
+  int enc;                // > 0: a listing stores row * enc + slot (enc = topk)
   __device__ int64_t n_rows(int h) const {
     return tiles ? (int64_t)count[h] : nq;
   }
+  // Range of the stored values (the counting sort's key range).
+  __device__ int64_t n_values(int h) const { return n_rows(h) * (enc > 0 ? enc : 1); }
   __device__ int64_t query(int h, int64_t r) const {
     return tiles ? (int64_t)tiles[(int64_t)h * nq + r].x : r;
   }
@@ -485,7 +488,7 @@ __global__ __launch_bounds__(256) void rev_scatter_kernel(
       const int64_t pos =
           cu_rev[(int64_t)h * (nb + 1) + c] +
           atomicAdd(&fill[(int64_t)h * nb + c], 1);
-      if (pos < cap) rev[(int64_t)h * cap + pos] = (int32_t)r;
+      if (pos < cap) rev[(int64_t)h * cap + pos] = (int32_t)(rows.enc > 0 ? r * rows.enc + j : r);
     }
   }
 }
@@ -551,9 +554,10 @@ __global__ __launch_bounds__(256) void rev_sort_kernel(
     for (int i = threadIdx.x; i < len; i += blockDim.x) seg[i] = s[i];
     return;
   }
-  // Windowed counting sort: values are row ids in [0, n_rows).
+  // Windowed counting sort: values are row ids in [0, n_rows) (or encoded
+  // listings in [0, n_rows * enc)).
   int32_t* out = aux + (int64_t)h * cap + s0;
-  const int64_t range = rows.n_rows(h);
+  const int64_t range = rows.n_values(h);
   __shared__ int s_base;
   if (threadIdx.x == 0) s_base = 0;
   __syncthreads();
@@ -594,7 +598,7 @@ int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
                       int64_t topk_n, const int32_t* cu_q, int64_t batch,
                       const int32_t* cu_sb, int64_t nb, bool rows_are_tiles,
                       const TilePlan* plan, Carver& ws, RevMap& map,
-                      hipStream_t st, const uint8_t* only) {
+                      hipStream_t st, const uint8_t* only, bool encode_slot) {
   int32_t* counts = ws.take<int32_t>((size_t)(hkv * (nb > 0 ? nb : 1)));
   int32_t* fill = ws.take<int32_t>((size_t)(hkv * (nb > 0 ? nb : 1)));
   int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, hkv));
@@ -607,7 +611,8 @@ int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
 
   RowSrc rows{rows_are_tiles ? plan->tiles : nullptr,
               rows_are_tiles ? plan->tile_count : nullptr, nq,
-              rows_are_tiles ? nullptr : only};
+              rows_are_tiles ? nullptr : only,
+              (!rows_are_tiles && encode_slot) ? (int)topk_n : 0};
   int rc = launch_zero_i32(counts, hkv * nb, st);
   if (rc) return rc;
   rc = launch_zero_i32(fill, hkv * nb, st);
@@ -660,6 +665,99 @@ int mark_grouped_queries(const TilePlan& plan, int64_t hkv, int64_t nq,
   // Grouped tiles hold >= 2 queries, so at most nq / 2 per head.
   hipLaunchKernelGGL(mark_grouped_kernel, dim3(ceil_div(nq / 2 + 1, 256), (unsigned)hkv),
                      dim3(256), 0, st, plan.gtiles, plan.gtile_count, nq, flags);
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
+}
+
+// -------------------------------------------------- key-centric part --
+
+__global__ __launch_bounds__(256) void mark_flagged_kernel(const int2* __restrict__ gtiles,
+                                                           const int32_t* __restrict__ gcount,
+                                                           const uint8_t* __restrict__ gflag,
+                                                           int64_t nq,
+                                                           uint8_t* __restrict__ qmark) {
+  const int h = blockIdx.y;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= gcount[h] || !gflag[(int64_t)h * nq + t]) return;
+  const int2 g = gtiles[(int64_t)h * nq + t];
+  for (int i = 0; i < g.y; ++i) qmark[(int64_t)h * nq + g.x + i] = 1;
+}
+
+int mark_flagged_queries(const TilePlan& plan, const uint8_t* gflag, int64_t hkv,
+                         int64_t nq, uint8_t* qmark, hipStream_t st) {
+  if (nq <= 0) return LSRM_OK;
+  int rc = launch_zero_i32(reinterpret_cast<int32_t*>(qmark), (hkv * nq + 3) / 4, st);
+  if (rc) return rc;
+  if (!plan.gtiles) return LSRM_OK;
+  hipLaunchKernelGGL(mark_flagged_kernel, dim3(ceil_div(nq / 2 + 1, 256), (unsigned)hkv),
+                     dim3(256), 0, st, plan.gtiles, plan.gtile_count, gflag, nq, qmark);
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
+}
+
+// Gathered tiles of block c: ceil(listings / tq) pieces of its grev segment.
+struct KcItemsF {
+  const int32_t* cu_rev;
+  int64_t nb, cap;
+  int tq;
+  __device__ int64_t limit(int, int64_t n) const { return n; }
+  __device__ int operator()(int h, int64_t c) const {
+    const int32_t* p = cu_rev + (int64_t)h * (nb + 1);
+    int64_t s = p[c], e = p[c + 1];
+    e = e < cap ? e : cap;
+    return e > s ? (int)((e - s + tq - 1) / tq) : 0;
+  }
+};
+struct KcItemsW {
+  const int32_t* cu_rev;
+  int64_t nb, cap;
+  int tq;
+  int4* items;
+  int64_t item_cap;
+  __device__ void operator()(int h, int64_t c, int ex, int v, int64_t) const {
+    const int32_t* p = cu_rev + (int64_t)h * (nb + 1);
+    const int64_t s = p[c];
+    int64_t e = p[c + 1];
+    e = e < cap ? e : cap;
+    for (int t = 0; t < v && ex + t < item_cap; ++t) {
+      const int64_t e0 = s + (int64_t)tq * t;
+      const int64_t n = e - e0 < tq ? e - e0 : tq;
+      items[(int64_t)h * item_cap + ex + t] = make_int4((int)c, (int)e0, (int)n, 0);
+    }
+  }
+};
+
+__global__ void kc_offsets_kernel(const int32_t* count, int hkv, int32_t* off,
+                                  int32_t* counter) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    int acc = 0;
+    off[0] = 0;
+    for (int h = 0; h < hkv; ++h) {
+      acc += count[h];
+      off[h + 1] = acc;
+    }
+    counter[KC_QUEUE_SLOT] = 0;
+    counter[KC_EXIT_SLOT] = 0;
+  }
+}
+
+int build_kc_items(const RevMap& grev, int64_t hkv, int64_t nb, int tq, Carver& ws,
+                   KcPlan& kc, int32_t* counter, hipStream_t st) {
+  kc.item_cap = grev.cap / (tq > 0 ? tq : 1) + nb + 1;
+  kc.items = ws.take<int4>((size_t)(hkv * kc.item_cap));
+  kc.item_count = ws.take<int32_t>((size_t)hkv);
+  kc.item_off = ws.take<int32_t>((size_t)(hkv + 1));
+  int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, hkv));
+  if (!ws.base || ws.dry) return LSRM_OK;
+  if (!ws.ok()) return LSRM_ERR_WORKSPACE;
+  int rc = launch_zero_i32(kc.item_count, hkv, st);
+  if (rc) return rc;
+  rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, tq},
+                KcItemsW{grev.cu_rev, nb, grev.cap, tq, kc.items, kc.item_cap}, nb, (int)hkv,
+                sums, kc.item_count, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(kc_offsets_kernel, dim3(1), dim3(64), 0, st, kc.item_count, (int)hkv,
+                     kc.item_off, counter);
   LSRM_CHECK_LAUNCH();
   return LSRM_OK;
 }

@@ -17,6 +17,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "liblsrm_hip.so"
 
 F32, F16, BF16 = 0, 1, 2
+PLAN_BACKWARD, PLAN_KEY_CENTRIC = 1, 2  # lsrm_sel_attn_plan2 flags
 _DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 # lsrm_meta_error bits (include/lsrm_hip.h)
@@ -78,6 +79,16 @@ _SIGNATURES = {
         _I,
         [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P,
          _I64, _F, _P, _P, _P, _SZ, _P],
+    ),
+    "lsrm_sel_attn_workspace_size2": (
+        _SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I]),
+    "lsrm_sel_attn_plan2": (
+        _I, [_P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I, _P, _SZ,
+             _P]),
+    "lsrm_sel_attn_fwd_run2": (
+        _I,
+        [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P,
+         _I64, _F, _P, _P, _P, _SZ, _I, _P],
     ),
     "lsrm_sel_attn_bwd_run": (
         _I,
@@ -316,8 +327,12 @@ def describe_meta_error(bits: int) -> str:
 
 
 def sel_attn_fwd(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
-                 softmax_scale: float):
-    """Selected-block attention forward -> (out [Nq, Hq, D], lse [Hq, Nq] log2)."""
+                 softmax_scale: float, key_centric: bool = False):
+    """Selected-block attention forward -> (out [Nq, Hq, D], lse [Hq, Nq] log2).
+
+    key_centric: plan with LSRM_PLAN_KEY_CENTRIC (per-token rows without
+    locality run as per-block gathered tiles plus a merge; the workspace
+    then holds up to Hq * Nq * topk * (2 * D + 4) bytes of partial results)."""
     dev = _dev_check(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q)
     nq, hq, d = q.shape
     nk, hkv, _ = k.shape
@@ -328,6 +343,10 @@ def sel_attn_fwd(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
     lse = torch.empty(hq, nq, dtype=torch.float32, device=dev)
     if nq == 0:
         return out, lse
+    if key_centric:
+        plan = SelAttnPlan(q.shape, k.shape, topk_idx, cu_seqblocks, cu_block_tokens,
+                           cu_seqlens_q, key_centric=True)
+        return plan.fwd(q, k, v, softmax_scale, out, lse)
     with torch.cuda.device(dev):
         ws_n = lib().lsrm_sel_attn_workspace_size(nq, nk, hq, hkv, topk, nb, 0)
         ws = _workspace(ws_n, dev)
@@ -372,7 +391,7 @@ class SelAttnPlan:
     here must stay alive and unchanged while the plan is used."""
 
     def __init__(self, q_shape, k_shape, topk_idx, cu_seqblocks, cu_block_tokens,
-                 cu_seqlens_q, backward: bool = False):
+                 cu_seqlens_q, backward: bool = False, key_centric: bool = False):
         dev = _dev_check(topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q)
         self.dev = dev
         self.nq, self.hq, self.d = q_shape
@@ -385,27 +404,30 @@ class SelAttnPlan:
         self.nb = cu_block_tokens.numel() - 1
         self.batch = cu_seqlens_q.numel() - 1
         self.backward = backward
+        self.flags = (PLAN_BACKWARD if backward else 0) | (PLAN_KEY_CENTRIC if key_centric else 0)
         with torch.cuda.device(dev):
-            n = lib().lsrm_sel_attn_workspace_size(self.nq, self.nk, self.hq, self.hkv,
-                                                   self.topk, self.nb, int(backward))
+            n = lib().lsrm_sel_attn_workspace_size2(self.nq, self.nk, self.hq, self.hkv,
+                                                    self.d, self.topk, self.nb, self.flags)
+            if n == 0:
+                raise ValueError("unsupported attention plan sizes or flags")
             self.ws = _workspace(n, dev)
-            _check(lib().lsrm_sel_attn_plan(
-                _ptr(topk_idx), self.nq, self.nk, self.hq, self.hkv, self.topk,
+            _check(lib().lsrm_sel_attn_plan2(
+                _ptr(topk_idx), self.nq, self.nk, self.hq, self.hkv, self.d, self.topk,
                 _ptr(cu_seqblocks), _ptr(cu_block_tokens), self.nb, _ptr(cu_seqlens_q),
-                self.batch, int(backward), _ptr(self.ws), self.ws.numel(), _stream(dev)),
-                "lsrm_sel_attn_plan")
+                self.batch, self.flags, _ptr(self.ws), self.ws.numel(), _stream(dev)),
+                "lsrm_sel_attn_plan2")
 
     def fwd(self, q, k, v, softmax_scale: float, out=None, lse=None):
         out = torch.empty_like(q) if out is None else out
         lse = torch.empty(self.hq, self.nq, dtype=torch.float32, device=self.dev) \
             if lse is None else lse
         with torch.cuda.device(self.dev):
-            _check(lib().lsrm_sel_attn_fwd_run(
+            _check(lib().lsrm_sel_attn_fwd_run2(
                 _ptr(q), _ptr(k), _ptr(v), _DTYPE_CODE[q.dtype], self.nq, self.nk, self.hq,
                 self.hkv, self.d, _ptr(self.topk_idx), self.topk, _ptr(self.cu_seqblocks),
                 _ptr(self.cu_block_tokens), self.nb, _ptr(self.cu_seqlens_q), self.batch,
                 float(softmax_scale), _ptr(out), _ptr(lse), _ptr(self.ws), self.ws.numel(),
-                _stream(self.dev)), "lsrm_sel_attn_fwd_run")
+                self.flags, _stream(self.dev)), "lsrm_sel_attn_fwd_run2")
         return out, lse
 
     def bwd(self, do, q, k, v, o, lse, softmax_scale: float):

@@ -46,15 +46,17 @@ NS = "lsrm_hip"
 @torch.library.custom_op(f"{NS}::sel_attn_fwd", mutates_args=())
 def sel_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, topk_idx: torch.Tensor,
                  cu_seqblocks: torch.Tensor, cu_block_tokens: torch.Tensor,
-                 cu_seqlens_q: torch.Tensor, softmax_scale: float
+                 cu_seqlens_q: torch.Tensor, softmax_scale: float, key_centric: bool = False
                  ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """out [Nq, Hq, D] (q's dtype), lse [Hq, Nq] fp32 in log2 units."""
+    """out [Nq, Hq, D] (q's dtype), lse [Hq, Nq] fp32 in log2 units
+    (key_centric: the key-centric plan for per-token rows without locality)."""
     return _sel_attn_fwd(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
-                         softmax_scale)
+                         softmax_scale, key_centric)
 
 
 @sel_attn_fwd.register_fake
-def _(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q, softmax_scale):
+def _(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q, softmax_scale,
+      key_centric=False):
     return torch.empty_like(q), q.new_empty((q.shape[1], q.shape[0]), dtype=torch.float32)
 
 
@@ -77,7 +79,7 @@ def _(do, q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q
 
 
 def _fwd_setup(ctx, inputs, output):
-    q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q, scale = inputs
+    q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q, scale = inputs[:8]
     o, lse = output
     ctx.save_for_backward(q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens,
                           cu_seqlens_q)
@@ -89,7 +91,7 @@ def _fwd_backward(ctx, do, _dlse):
     dq, dk, dv, _ = torch.ops.lsrm_hip.sel_attn_bwd(
         do.contiguous().to(q.dtype), q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens,
         cu_seqlens_q, ctx.scale)
-    return dq, dk, dv, None, None, None, None, None
+    return dq, dk, dv, None, None, None, None, None, None
 
 
 sel_attn_fwd.register_autograd(_fwd_backward, setup_context=_fwd_setup)

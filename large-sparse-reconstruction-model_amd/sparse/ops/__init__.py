@@ -12,6 +12,7 @@ from .gate_merge import GateMerge, gate_merge
 from .native_sparse_attention import (
     NSA,
     native_sparse_attend,
+    set_key_centric,
     set_validation,
     set_variant,
     spatial_selection_attention,
@@ -27,6 +28,7 @@ __all__ = [
     "get_block_score",
     "native_sparse_attend",
     "select_blocks",
+    "set_key_centric",
     "set_validation",
     "set_variant",
     "sparse3d_compression",

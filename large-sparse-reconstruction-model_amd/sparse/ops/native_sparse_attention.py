@@ -20,6 +20,7 @@ import lsrm_hip as _hip
 
 _default_variant = "a"
 _validate = True
+_key_centric = False
 
 
 def set_variant(variant: str) -> None:
@@ -35,6 +36,16 @@ def set_validation(enabled: bool) -> None:
     forward call).  On by default; turn off for graph capture or timing."""
     global _validate
     _validate = bool(enabled)
+
+
+def set_key_centric(enabled: bool) -> None:
+    """Plans the forward with the key-centric pass for per-token rows without
+    locality (learned selections): each block's selecting queries are
+    gathered into full tiles and the per-block partial results merged in row
+    order.  Off by default: the workspace then holds up to
+    Hq * N * topk * (2 * D + 4) bytes of partial results."""
+    global _key_centric
+    _key_centric = bool(enabled)
 
 
 def _check_meta(q, k, topk_idx, cu_seqblocks, cu_block_include_tokens, cu_seqlens_q,
@@ -84,7 +95,7 @@ class NSA(torch.autograd.Function):
                     cu_seqlens_k)
         o, lse = torch.ops.lsrm_hip.sel_attn_fwd(q, k, v, topk_idx, cu_seqblocks,
                                                  cu_block_include_tokens, cu_seqlens_q,
-                                                 float(softmax_scale))
+                                                 float(softmax_scale), _key_centric)
         ctx.save_for_backward(q, k, v, o, lse, cu_seqlens_q, cu_seqlens_k, topk_idx,
                               cu_seqblocks, cu_block_include_tokens)
         ctx.softmax_scale = softmax_scale

@@ -1,0 +1,191 @@
+"""GPU parity of the key-centric forward (plan flag LSRM_PLAN_KEY_CENTRIC):
+per-token rows without locality (learned selections) run as per-block
+gathered tiles whose partial results are merged in row order.  Checked
+against the fp32 oracle at the attention tolerance (output and LSE), against
+the grouped-tile path, for run-to-run bitwise repeatability, and together
+with the backward on the same plan."""
+
+import numpy as np
+import pytest
+import torch
+
+import lsrm_hip as H
+import sparse.ops as ops
+from helpers import assert_attn_close
+from lsrm_hip import workloads as W
+from oracle.attention import sel_attn_ref
+from oracle.select3d import nearest_blocks_ref, volume_points_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _random_rows(n=6000, hq=2, hkv=2, topk=12, seed=4, d=64, dtype=torch.bfloat16):
+    """Blocks of 4..16 tokens (about n / 10 of them) with unrelated random rows
+    per token, as learned selections on unstructured data: 96 consecutive
+    queries list several hundred distinct blocks, more than one masked union
+    pass takes, so the grouped tiles go to the key-centric pass.  -1 padding,
+    out-of-range ids and empty rows included."""
+    rng = np.random.default_rng(seed)
+    sizes = rng.integers(4, 17, size=n // 4)
+    cu = np.concatenate([[0], np.cumsum(sizes)])
+    cu = cu[cu <= n]
+    cu[-1] = n
+    nb = len(cu) - 1
+    g = torch.Generator().manual_seed(seed)
+    q = (0.5 * torch.randn(n, hq, d, generator=g)).to(dtype)
+    k = (0.5 * torch.randn(n, hkv, d, generator=g)).to(dtype)
+    v = (0.5 * torch.randn(n, hkv, d, generator=g)).to(dtype)
+    rows = torch.randint(0, nb, (hkv, n, topk), generator=g, dtype=torch.int32)
+    rows[:, ::5, topk - 3:] = -1
+    rows[:, 1::7, 3] = nb + 5
+    rows[:, 2::11, :] = -1
+    return (q, k, v, rows, torch.tensor([0, nb], dtype=torch.int32),
+            torch.from_numpy(cu.astype(np.int32)), torch.tensor([0, n], dtype=torch.int32))
+
+
+def _fwd(args, key_centric, scale=0.125):
+    dev_args = [t.to(DEV) for t in args]
+    return H.sel_attn_fwd(*dev_args, scale, key_centric=key_centric)
+
+
+def _check_oracle(args, o, lse, scale=0.125):
+    q, k, v, rows, cu_sb, cu_blk, cu_q = args
+    o_ref, lse_ref = sel_attn_ref(q.float(), k.float(), v.float(), rows, cu_sb, cu_blk, cu_q,
+                                  scale)
+    assert_attn_close(o, o_ref, "out")
+    lse_c = lse.cpu()
+    fin = torch.isfinite(lse_ref)
+    assert torch.equal(torch.isfinite(lse_c), fin)
+    if fin.any():
+        assert float((lse_c[fin] - lse_ref[fin]).abs().max()) <= 2e-2
+
+
+def test_random_rows_match_oracle_and_grouped_path():
+    args = _random_rows()
+    o, lse = _fwd(args, True)
+    _check_oracle(args, o, lse)
+    o2, lse2 = _fwd(args, False)
+    assert_attn_close(o, o2.float().cpu(), "out vs grouped tiles")
+    # the two paths round differently: equal bits would mean no tile was
+    # gathered
+    assert not torch.equal(o, o2)
+
+
+def test_random_rows_bitwise_repeatable():
+    args = _random_rows(seed=5)
+    a = _fwd(args, True)
+    b = _fwd(args, True)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_duplicate_ids_count_twice():
+    q, k, v, rows, cu_sb, cu_blk, cu_q = _random_rows(seed=6)
+    rows = rows.clone()
+    rows[:, ::3, 1] = rows[:, ::3, 0]      # the same block listed twice
+    rows[:, 1::4, 2] = rows[:, 1::4, 0]
+    rows[:, 1::4, 5] = rows[:, 1::4, 0]    # three times
+    args = (q, k, v, rows, cu_sb, cu_blk, cu_q)
+    o, lse = _fwd(args, True)
+    _check_oracle(args, o, lse)
+
+
+@pytest.mark.parametrize("hq,hkv,d,topk", [(8, 2, 64, 8), (32, 2, 32, 4), (2, 2, 128, 8)])
+def test_gqa_and_head_dims(hq, hkv, d, topk):
+    args = _random_rows(n=3000, hq=hq, hkv=hkv, d=d, topk=topk, seed=7)
+    o, lse = _fwd(args, True)
+    _check_oracle(args, o, lse)
+
+
+def test_fp16_and_empty_blocks():
+    q, k, v, rows, cu_sb, cu_blk, cu_q = _random_rows(n=3000, seed=8, dtype=torch.float16)
+    # blocks 3 and 4 hold no tokens (block 5 takes theirs): their listings
+    # contribute nothing
+    cu = cu_blk.clone()
+    cu[4] = cu[3]
+    cu[5] = cu[3]
+    rows = rows.clone()
+    rows[:, ::2, 0] = 3
+    rows[:, ::4, 1] = 4
+    args = (q, k, v, rows, cu_sb, cu, cu_q)
+    o, lse = _fwd(args, True)
+    _check_oracle(args, o, lse)
+
+
+def test_two_batch_elements():
+    q, k, v, rows, cu_sb, cu_blk, cu_q = _random_rows(n=3000, seed=9)
+    n = q.shape[0]
+    nb = cu_blk.numel() - 1
+    args = (torch.cat([q, q]), torch.cat([k, k]), torch.cat([v, v]),
+            torch.cat([rows, rows.flip(1)], dim=1).contiguous(),
+            torch.tensor([0, nb, 2 * nb], dtype=torch.int32),
+            torch.cat([cu_blk, cu_blk[1:] + n]),
+            torch.tensor([0, n, 2 * n], dtype=torch.int32))
+    o, lse = _fwd(args, True)
+    _check_oracle(args, o, lse)
+
+
+def test_local_rows_unchanged_by_the_flag():
+    # Rows with locality (every tile is a run or a valid union): no tile is
+    # flagged, the gathered pass has no work and the result is the same bits.
+    # 3D-aware rows of cfg3-style voxel tokens: nearest block centroids.
+    w = W.config(3, n=16384, heads=2)
+    nv = w.voxel_coords.shape[0]
+    cu_all = w.cu_block_tokens.numpy().astype(np.int64)
+    cu_v = (cu_all[w.n_image_blocks:] - cu_all[w.n_image_blocks]).astype(np.int32)
+    coords = np.concatenate([np.zeros((nv, 1), np.int64), w.voxel_coords], axis=1)
+    pts = volume_points_ref(coords, 64, 1.0)
+    sel = nearest_blocks_ref(pts, cu_v, np.array([0, len(cu_v) - 1]), np.array([0, nv]), 16)
+    rows = torch.from_numpy(np.broadcast_to(sel, (2, nv, 16)).copy())
+    g = torch.Generator().manual_seed(12)
+    q, k, v = ((0.5 * torch.randn(nv, 2, 64, generator=g)).to(torch.bfloat16) for _ in range(3))
+    args = (q, k, v, rows, torch.tensor([0, len(cu_v) - 1], dtype=torch.int32),
+            torch.from_numpy(cu_v), torch.tensor([0, nv], dtype=torch.int32))
+    a = _fwd(args, True)
+    b = _fwd(args, False)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_plan_with_backward_and_key_centric():
+    # One plan carrying both parts: the key-centric forward, then the
+    # backward on the same workspace.
+    q, k, v, rows, cu_sb, cu_blk, cu_q = _random_rows(n=3000, topk=6, seed=10)
+    dev = [t.to(DEV) for t in (q, k, v, rows, cu_sb, cu_blk, cu_q)]
+    plan = H.SelAttnPlan(dev[0].shape, dev[1].shape, dev[3], dev[4], dev[5], dev[6],
+                         backward=True, key_centric=True)
+    o, lse = plan.fwd(dev[0], dev[1], dev[2], 0.125)
+    _check_oracle((q, k, v, rows, cu_sb, cu_blk, cu_q), o, lse)
+    g = torch.Generator().manual_seed(110)
+    do = (0.5 * torch.randn(q.shape, generator=g)).to(q.dtype)
+    dq, dk, dv, _ = plan.bwd(do.to(DEV), dev[0], dev[1], dev[2], o, lse, 0.125)
+    qf, kf, vf = (t.float().requires_grad_() for t in (q, k, v))
+    o_ref, _ = sel_attn_ref(qf, kf, vf, rows, cu_sb, cu_blk, cu_q, 0.125)
+    o_ref.backward(do.float())
+    assert_attn_close(dq, qf.grad, "dq")
+    assert_attn_close(dk, kf.grad, "dk")
+    assert_attn_close(dv, vf.grad, "dv")
+
+
+def test_sparse_ops_knob_with_autograd():
+    q, k, v, rows, cu_sb, cu_blk, cu_q = _random_rows(n=2000, topk=6, seed=11)
+    # sparse.ops validates the rows: -1 only as trailing padding
+    rows = torch.where(rows >= cu_blk.numel() - 1, rows[..., :1], rows)
+    rows = torch.where(rows[..., :1] < 0, torch.full_like(rows, -1), rows)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    ops.set_key_centric(True)
+    try:
+        out = ops.native_sparse_attend(qd, kd, vd, rows.to(DEV), cu_sb.to(DEV),
+                                       cu_blk.to(DEV), cu_q.to(DEV), cu_q.to(DEV), 0.125)
+    finally:
+        ops.set_key_centric(False)
+    qf, kf, vf = (t.float().requires_grad_() for t in (q, k, v))
+    o_ref, _ = sel_attn_ref(qf, kf, vf, rows, cu_sb, cu_blk, cu_q, 0.125)
+    assert_attn_close(out, o_ref, "out")
+    g = torch.Generator().manual_seed(111)
+    do = (0.5 * torch.randn(q.shape, generator=g)).to(q.dtype)
+    out.backward(do.to(DEV))
+    o_ref.backward(do.float())
+    assert_attn_close(qd.grad, qf.grad, "dq")
+    assert_attn_close(kd.grad, kf.grad, "dk")
+    assert_attn_close(vd.grad, vf.grad, "dv")
+    assert np.isfinite(out.detach().float().cpu().numpy()).all()
