@@ -152,6 +152,26 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
     ms_ca = event_time_ms(lambda: ops.compressed_attention(q, ck, cv, cu_q, cu_sb), 5)
     ms_bs = event_time_ms(lambda: ops.get_block_score(q, ck, lse, 16, cu_q, cu_sb, None, None), 5)
     ops.set_validation(True)
+    # Selected attention on the learned rows (per-token, no locality on this
+    # synthetic data): the key-centric plan; the plan is timed apart (it is
+    # built once per selection and shared by forward and backward).
+    rows_l = ops.get_block_score(q, ck, lse, 16, cu_q, cu_sb, None, None)
+    lens = (cu_blk[1:] - cu_blk[:-1]).long()
+    flops_l = 4.0 * w.d * (w.hq // w.hkv) * float(
+        torch.where(rows_l >= 0, lens[rows_l.clamp(min=0).long()], 0).sum())
+    plan_l = H.SelAttnPlan(q.shape, k.shape, rows_l, cu_sb, cu_blk, cu_q, backward=True,
+                           key_centric=True)
+    out_l = torch.empty_like(q)
+    lse_l = torch.empty(w.hq, w.n, dtype=torch.float32, device=dev)
+    ms_l = event_time_ms(lambda: plan_l.fwd(q, k, v, w.scale, out_l, lse_l), 3)
+    do_l = torch.randn(q.shape, generator=torch.Generator(device=dev).manual_seed(8),
+                       device=dev).to(q.dtype)
+    ms_lb = event_time_ms(lambda: plan_l.bwd(do_l, q, k, v, out_l, lse_l, w.scale), 2)
+    del plan_l, do_l
+    ms_lp = event_time_ms(
+        lambda: H.SelAttnPlan(q.shape, k.shape, rows_l, cu_sb, cu_blk, cu_q, backward=True,
+                              key_centric=True), 2)
+    del out_l, lse_l
 
     # gated merge of the three branch outputs at the layer shape (streams
     # gate [N, 3*hidden] and three [N, hidden] inputs, writes [N, hidden])
@@ -171,6 +191,13 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
             "ms": round(ms3b, 4), "tflops": round(2.5 * flops3 / (ms3b * 1e-3) / 1e12, 2)},
         "learned_selection": {"compressed_attn_ms": round(ms_ca, 4),
                               "get_block_score_ms": round(ms_bs, 4), "topk": 16},
+        "attn_fwd_learned_rows_key_centric": {
+            "ms": round(ms_l, 4), "tflops": round(flops_l / (ms_l * 1e-3) / 1e12, 2),
+            "plan_ms": round(ms_lp, 4),
+            "bwd_ms": round(ms_lb, 4),
+            "bwd_tflops": round(2.5 * flops_l / (ms_lb * 1e-3) / 1e12, 2),
+            "workload": f"get_block_score rows (top-16 of {w.n_blocks} blocks per token), "
+                        f"H={w.hq}"},
         "gate_merge": {"ms": round(ms_gm, 4), "bytes": gm_bytes,
                        "gbs": round(gm_bytes / (ms_gm * 1e-3) / 1e9, 1),
                        "frac_hbm_peak": round(gm_bytes / (ms_gm * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
@@ -218,6 +245,8 @@ def main() -> int:
     n, hq, hkv, d = w.n, w.hq, w.hkv, w.d
     k2 = k.view(n, hkv * d)
     v2 = v.view(n, hkv * d)
+    # forced block ids resident on the device (no host copy inside a step)
+    forced = torch.tensor(w.forced_blocks, dtype=torch.int32, device=dev)
 
     # Keys and values are pooled in one launch pair (keys in fp32: the
     # selection takes those means and the compressed keys are their rounding
@@ -227,7 +256,7 @@ def main() -> int:
     def layer():
         pk, cv = H.block_mean_pool2(k2, v2, cu_blk, torch.float32, None)
         ck = pk.to(k2.dtype)
-        topk_idx, compact = H.select_blocks(q, k, cu_sb, cu_blk, w.topk, w.forced_blocks, True,
+        topk_idx, compact = H.select_blocks(q, k, cu_sb, cu_blk, w.topk, forced, True,
                                             pooled_k=pk)
         o, lse = H.sel_attn_fwd(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, w.scale)
         return ck, cv, topk_idx, compact, o, lse
@@ -268,7 +297,7 @@ def main() -> int:
     ms_pool_kv = event_time_ms(lambda: H.block_mean_pool2(k2, v2, cu_blk, torch.float32, None),
                                reps)
     ms_select = event_time_ms(
-        lambda: H.select_blocks(q, k, cu_sb, cu_blk, w.topk, w.forced_blocks, True), reps)
+        lambda: H.select_blocks(q, k, cu_sb, cu_blk, w.topk, forced, True), reps)
     # Backward (training path) on the same selection: dQ, reverse map, dK/dV.
     bplan = H.SelAttnPlan(q.shape, k.shape, topk_idx, cu_sb, cu_blk, cu_q, backward=True)
     do = torch.randn_like(q)

@@ -303,6 +303,23 @@ int lsrm_sel_attn_fwd_run2(const void* q, const void* k, const void* v,
                            float softmax_scale, void* out, float* lse,
                            void* workspace, size_t workspace_bytes, int flags,
                            void* stream);
+/* Backward on a plan built with LSRM_PLAN_BACKWARD (and optionally
+ * LSRM_PLAN_KEY_CENTRIC): with the key-centric part, dQ of the gathered
+ * queries is computed per (query, slot) by the gathered tiles (the block's
+ * share, in the input type, in the partial buffer of the forward) and added
+ * in slot order; dK/dV are unchanged (they are already key-centric).
+ * Replaces: ..._impl_kvcentric.py:1018-1263 for per-token rows. */
+int lsrm_sel_attn_bwd_run2(const void* dout, const void* q, const void* k,
+                           const void* v, const void* out, const float* lse,
+                           int dtype, int64_t n_q, int64_t n_k, int64_t hq,
+                           int64_t hkv, int64_t head_dim,
+                           const int32_t* topk_idx, int64_t topk,
+                           const int32_t* cu_seqblocks,
+                           const int32_t* cu_block_tokens, int64_t n_blocks,
+                           const int32_t* cu_seqlens_q, int64_t batch,
+                           float softmax_scale, void* dq, void* dk, void* dv,
+                           float* delta, void* workspace,
+                           size_t workspace_bytes, int flags, void* stream);
 
 /* ------------------------------------------------------------------------
  * Selected-block attention, backward.  Inputs as for the forward plus

@@ -32,14 +32,22 @@ namespace lsrm {
 
 // ------------------------------------------------------------------- dQ --
 
-// UNION false: the run tiles of the plan.  UNION true: the grouped tiles,
-// run once over the union of their rows' blocks with per-row key masks, or
-// once per run of identical rows with the other rows' P forced to zero (the
-// passes of the forward's grouped tiles; no softmax state is carried, so
-// either way each row's dQ is a plain sum over the keys it attends).
-template <int DT, int D, bool UNION>
+// MODE 0 (DQ_RUN): the run tiles of the plan.  MODE 1 (DQ_UNION): the
+// grouped tiles, run once over the union of their rows' blocks with per-row
+// key masks, or once per run of identical rows with the other rows' P forced
+// to zero (the passes of the forward's grouped tiles; no softmax state is
+// carried, so either way each row's dQ is a plain sum over the keys it
+// attends); in a key-centric plan the flagged tiles are left to mode 2.
+// MODE 2 (DQ_GATHER): the gathered tiles of a key-centric plan, each row
+// writing the block's share of its dQ (one slot of its row, in the input
+// type) for kc_dq_merge_kernel.
+constexpr int DQ_RUN = 0, DQ_UNION = 1, DQ_GATHER = 2;
+
+template <int DT, int D, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 sel_attn_dq_kernel(AttnArgs a) {
+  constexpr bool UNION = MODE == DQ_UNION;
+  constexpr bool GATHER = MODE == DQ_GATHER;
   using G = KvTile<D>;
   constexpr int NS = D / 16;  // MFMA k-steps over the head dim
   constexpr int ND = D / 32;  // 32-wide output blocks over the head dim
@@ -51,9 +59,10 @@ sel_attn_dq_kernel(AttnArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
-  const int32_t* head_off = UNION ? a.plan.ghead_off : a.plan.head_off;
+  const int32_t* head_off =
+      GATHER ? a.kc.item_off : (UNION ? a.plan.ghead_off : a.plan.head_off);
   const int2* tiles = UNION ? a.plan.gtiles : a.plan.tiles;
-  int32_t* queue = a.plan.counter + (UNION ? 4 : 0);
+  int32_t* queue = a.plan.counter + (GATHER ? KC_QUEUE_SLOT : (UNION ? 4 : 0));
   // A plan built without its backward part: nothing here is valid to read.
   if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC) return;
   const int total = head_off[a.hkv];
@@ -70,15 +79,35 @@ sel_attn_dq_kernel(AttnArgs a) {
     const int w = uniform(fetch_work(queue, &s_slot));
     if (w >= total) break;
     const int h = head_of(head_off, a.hkv, w);
-    const int2 tile = tiles[(int64_t)h * a.nq + (w - head_off[h])];
-    const int q0 = tile.x, qn = tile.y, rows = qn * a.g;
-    // umode 0: a run tile; 1: a grouped tile over the union of its blocks,
-    // rows masked to their own; 2: a grouped tile run by run.
+    int q0, qn, gblk = 0, ge0 = 0;
+    if constexpr (GATHER) {
+      const int4 it = a.kc.items[(int64_t)h * a.kc.item_cap + (w - head_off[h])];
+      gblk = it.x;
+      ge0 = it.y;
+      q0 = 0;
+      qn = it.z;
+    } else {
+      if constexpr (UNION) {
+        if (a.kc.gflag && a.kc.gflag[(int64_t)h * a.nq + (w - head_off[h])]) {
+          __syncthreads();  // every wave has read s_slot before it is reused
+          continue;
+        }
+      }
+      const int2 tile = tiles[(int64_t)h * a.nq + (w - head_off[h])];
+      q0 = tile.x;
+      qn = tile.y;
+    }
+    const int rows = qn * a.g;
+    // umode 0: a run tile (or a gathered tile); 1: a grouped tile over the
+    // union of its blocks, rows masked to their own; 2: a grouped tile run
+    // by run.
     int umode = 0, n_pass = 1;
     if constexpr (UNION) {
       build_union(a, h, q0, qn, sel, ul);
       umode = ul.ok ? 1 : 2;
       n_pass = ul.ok ? 1 : ul.n_runs;
+    } else if constexpr (GATHER) {
+      load_block(a, gblk, sel);
     } else {
       load_selection(a, h, q0, sel);
     }
@@ -100,7 +129,15 @@ sel_attn_dq_kernel(AttnArgs a) {
     const int qr = row_ok ? r / a.g : 0;  // the row's query within the tile
     const bool row_in_pass = row_ok && qr >= q_lo && qr < q_hi;
     const bool wave_on = wv * 32 < q_hi * a.g && wv * 32 + 32 > q_lo * a.g;
-    const int64_t qi = q0 + qr;
+    // Gathered tiles: row r is listing ge0 + r / g (query * topk + slot).
+    int64_t qi, gslot = 0;
+    if constexpr (GATHER) {
+      const int64_t lv = a.kc.grev.rev[(int64_t)h * a.kc.grev.cap + ge0 + qr];
+      qi = lv / a.topk_n;
+      gslot = lv - qi * a.topk_n;
+    } else {
+      qi = q0 + qr;
+    }
     const int hh = h * a.g + (row_ok ? r % a.g : 0);
     u32x4 qb[NS], dob[NS];
     float dpart = 0.0f;
@@ -425,7 +462,11 @@ sel_attn_dq_kernel(AttnArgs a) {
     }
 
     if (row_in_pass) {
-      uint16_t* drow = a.out + (qi * a.hq + hh) * D;
+      // gathered rows: the slot's share of dQ, summed by kc_dq_merge_kernel
+      uint16_t* drow =
+          GATHER ? a.kc.part_o + ((((int64_t)h * a.nq + qi) * a.topk_n + gslot) * a.g +
+                                  (r % a.g)) * D
+                 : a.out + (qi * a.hq + hh) * D;
 #pragma unroll
       for (int db = 0; db < ND; ++db)
 #pragma unroll
@@ -900,22 +941,81 @@ sel_attn_dkdv_kernel(AttnArgs a) {
   leave_queue_xcd(a.plan.counter + 8, a.plan.counter + 3);
 }
 
+// Key-centric dQ merge: one thread per (kv head, query, query head, 4
+// channels) of the marked queries; the slot shares of dQ written by the
+// gathered tiles are added in slot order in fp32 and rounded once.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void kc_dq_merge_kernel(AttnArgs a) {
+  constexpr int CPT = 4;
+  const int64_t per_q = (int64_t)a.g * (D / CPT);
+  const int64_t n_items = (int64_t)a.hkv * a.nq * per_q;
+  for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
+       it += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t hq_idx = it / per_q;  // h * nq + q
+    if (!a.kc.qmark[hq_idx]) continue;
+    const int sub = (int)(it - hq_idx * per_q);
+    const int gi = sub / (D / CPT), d0 = (sub % (D / CPT)) * CPT;
+    const int h = (int)(hq_idx / a.nq);
+    const int64_t q = hq_idx - (int64_t)h * a.nq;
+    int b, bs, nbb;
+    bool st;
+    query_batch(a.cu_q, a.batch, a.cu_sb, q, &b, &bs, &nbb, &st);
+    const int32_t* row = a.topk + hq_idx * a.topk_n;
+    float acc[CPT] = {0.0f, 0.0f, 0.0f, 0.0f};
+    bool any = false;
+    for (int j = 0; j < a.topk_n; ++j) {
+      const int v = row[j];
+      if (!(v >= 0 && v < nbb && (int64_t)bs + v < a.nb)) continue;
+      any = true;
+      const int64_t pidx = (hq_idx * a.topk_n + j) * a.g + gi;
+      const u32x2 pv = *reinterpret_cast<const u32x2*>(a.kc.part_o + pidx * D + d0);
+      acc[0] += to_f32<DT>((uint16_t)(pv[0] & 0xffffu));
+      acc[1] += to_f32<DT>((uint16_t)(pv[0] >> 16));
+      acc[2] += to_f32<DT>((uint16_t)(pv[1] & 0xffffu));
+      acc[3] += to_f32<DT>((uint16_t)(pv[1] >> 16));
+    }
+    const int hh = h * a.g + gi;
+    *reinterpret_cast<u32x2*>(a.out + (q * a.hq + hh) * D + d0) =
+        u32x2{pack2<DT>(acc[0], acc[1]), pack2<DT>(acc[2], acc[3])};
+    if (!any && d0 == 0) {
+      // No slot names a block: no gathered row wrote this row's Delta.
+      const uint16_t* orow = a.o + (q * a.hq + hh) * D;
+      const uint16_t* drow = a.dout + (q * a.hq + hh) * D;
+      float dl = 0.0f;
+      for (int d = 0; d < D; ++d) dl += to_f32<DT>(orow[d]) * to_f32<DT>(drow[d]);
+      a.lse[(int64_t)hh * a.nq + q] = dl;
+    }
+  }
+}
+
 template <int DT, int D>
 int launch_bwd_t(const AttnArgs& a, hipStream_t st) {
   {
-    const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D, false>);
+    const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D, DQ_RUN>);
     const int grid = persistent_grid(fn, 256, 0);
     if (grid <= 0) return LSRM_ERR_LAUNCH;
-    hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D, false>), dim3(grid), dim3(256), 0,
+    hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D, DQ_RUN>), dim3(grid), dim3(256), 0,
                        st, a);
     LSRM_CHECK_LAUNCH();
   }
   if (a.plan.gtiles) {  // the grouped tiles (often none)
-    const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D, true>);
+    const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D, DQ_UNION>);
     const int grid = persistent_grid(fn, 256, 0);
     if (grid <= 0) return LSRM_ERR_LAUNCH;
-    hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D, true>), dim3(grid), dim3(256), 0,
+    hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D, DQ_UNION>), dim3(grid), dim3(256), 0,
                        st, a);
+    LSRM_CHECK_LAUNCH();
+  }
+  if (a.kc.items) {  // key-centric plans: gathered dQ tiles, then the merge
+    const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D, DQ_GATHER>);
+    const int grid = persistent_grid(fn, 256, 0);
+    if (grid <= 0) return LSRM_ERR_LAUNCH;
+    hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D, DQ_GATHER>), dim3(grid), dim3(256), 0,
+                       st, a);
+    LSRM_CHECK_LAUNCH();
+    const int gm = device_cu_count() * 16;
+    if (gm <= 0) return LSRM_ERR_LAUNCH;
+    hipLaunchKernelGGL((kc_dq_merge_kernel<DT, D>), dim3(gm), dim3(256), 0, st, a);
     LSRM_CHECK_LAUNCH();
   }
   {

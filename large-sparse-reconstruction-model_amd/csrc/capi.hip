@@ -389,7 +389,7 @@ static int bwd_impl(const void* dout, const void* q, const void* k,
                     const int32_t* cu_seqlens_q, int64_t batch,
                     float softmax_scale, void* dq, void* dk, void* dv,
                     float* delta, void* workspace, size_t workspace_bytes,
-                    void* stream, bool plan) {
+                    void* stream, bool plan, int flags = LSRM_PLAN_BACKWARD) {
   const int arc = check_attn_args(dtype, n_q, n_k, hq, hkv, head_dim, topk,
                                   n_blocks, batch);
   if (arc || n_q == 0) return arc;
@@ -401,7 +401,7 @@ static int bwd_impl(const void* dout, const void* q, const void* k,
   AttnArgs a;
   int rc = attn_setup(q, k, v, dtype, n_q, n_k, hq, hkv, head_dim, topk_idx,
                       topk, cu_seqblocks, cu_block_tokens, n_blocks,
-                      cu_seqlens_q, batch, softmax_scale, LSRM_PLAN_BACKWARD, plan,
+                      cu_seqlens_q, batch, softmax_scale, flags | LSRM_PLAN_BACKWARD, plan,
                       workspace, workspace_bytes, st, a);
   if (rc) return rc;
   a.o = static_cast<const uint16_t*>(out);
@@ -440,4 +440,21 @@ extern "C" int lsrm_sel_attn_bwd_run(
                   topk_idx, topk, cu_seqblocks, cu_block_tokens, n_blocks,
                   cu_seqlens_q, batch, softmax_scale, dq, dk, dv, delta,
                   workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int lsrm_sel_attn_bwd_run2(
+    const void* dout, const void* q, const void* k, const void* v,
+    const void* out, const float* lse, int dtype, int64_t n_q, int64_t n_k,
+    int64_t hq, int64_t hkv, int64_t head_dim, const int32_t* topk_idx,
+    int64_t topk, const int32_t* cu_seqblocks, const int32_t* cu_block_tokens,
+    int64_t n_blocks, const int32_t* cu_seqlens_q, int64_t batch,
+    float softmax_scale, void* dq, void* dk, void* dv, float* delta,
+    void* workspace, size_t workspace_bytes, int flags, void* stream) {
+  if ((flags & ~(LSRM_PLAN_BACKWARD | LSRM_PLAN_KEY_CENTRIC)) != 0 ||
+      !(flags & LSRM_PLAN_BACKWARD))
+    return LSRM_ERR_INVALID_ARG;
+  return bwd_impl(dout, q, k, v, out, lse, dtype, n_q, n_k, hq, hkv, head_dim,
+                  topk_idx, topk, cu_seqblocks, cu_block_tokens, n_blocks,
+                  cu_seqlens_q, batch, softmax_scale, dq, dk, dv, delta,
+                  workspace, workspace_bytes, stream, false, flags);
 }

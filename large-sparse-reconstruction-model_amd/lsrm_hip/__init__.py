@@ -90,6 +90,11 @@ _SIGNATURES = {
         [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P,
          _I64, _F, _P, _P, _P, _SZ, _I, _P],
     ),
+    "lsrm_sel_attn_bwd_run2": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P,
+         _I64, _P, _I64, _F, _P, _P, _P, _P, _P, _SZ, _I, _P],
+    ),
     "lsrm_sel_attn_bwd_run": (
         _I,
         [_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P,
@@ -249,7 +254,7 @@ def block_mean_pool2(x_a: torch.Tensor, x_b: torch.Tensor, cu_block_tokens: torc
 
 def select_blocks(q: torch.Tensor, k: torch.Tensor, cu_seqblocks: torch.Tensor,
                   cu_block_tokens: torch.Tensor, topk: int,
-                  forced_blocks: Optional[Sequence[int]] = None,
+                  forced_blocks=None,  # sequence of ints, or a device int32 tensor
                   force_self: bool = True,
                   pooled_k: Optional[torch.Tensor] = None):
     """Per-query-block top-k selection (self attention).
@@ -278,7 +283,11 @@ def select_blocks(q: torch.Tensor, k: torch.Tensor, cu_seqblocks: torch.Tensor,
     nb = cu.numel() - 1
     batch = cu_sb.numel() - 1
     forced = None
-    if forced_blocks is not None and len(forced_blocks) > 0:
+    if isinstance(forced_blocks, torch.Tensor):
+        # a device int32 tensor is used as is (no host-to-device copy per call)
+        if forced_blocks.numel() > 0:
+            forced = forced_blocks.to(device=dev, dtype=torch.int32).contiguous()
+    elif forced_blocks is not None and len(forced_blocks) > 0:
         forced = torch.as_tensor(list(forced_blocks), dtype=torch.int32, device=dev)
     if nb == 0 or n == 0:
         return (torch.full((hkv, n, topk), -1, dtype=torch.int32, device=dev),
@@ -359,8 +368,13 @@ def sel_attn_fwd(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
 
 
 def sel_attn_bwd(do, q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens,
-                 cu_seqlens_q, softmax_scale: float):
-    """Selected-block attention backward -> (dq, dk, dv, delta)."""
+                 cu_seqlens_q, softmax_scale: float, key_centric: bool = False):
+    """Selected-block attention backward -> (dq, dk, dv, delta)
+    (key_centric: dQ of per-token rows without locality on gathered tiles)."""
+    if key_centric and q.shape[0] > 0:
+        plan = SelAttnPlan(q.shape, k.shape, topk_idx, cu_seqblocks, cu_block_tokens,
+                           cu_seqlens_q, backward=True, key_centric=True)
+        return plan.bwd(do, q, k, v, o, lse, softmax_scale)
     dev = _dev_check(do, q, k, v, o, lse, topk_idx)
     nq, hq, d = q.shape
     nk, hkv, _ = k.shape
@@ -438,13 +452,13 @@ class SelAttnPlan:
         dv = torch.zeros_like(v)
         delta = torch.empty(self.hq, self.nq, dtype=torch.float32, device=self.dev)
         with torch.cuda.device(self.dev):
-            _check(lib().lsrm_sel_attn_bwd_run(
+            _check(lib().lsrm_sel_attn_bwd_run2(
                 _ptr(do), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _DTYPE_CODE[q.dtype],
                 self.nq, self.nk, self.hq, self.hkv, self.d, _ptr(self.topk_idx), self.topk,
                 _ptr(self.cu_seqblocks), _ptr(self.cu_block_tokens), self.nb,
                 _ptr(self.cu_seqlens_q), self.batch, float(softmax_scale), _ptr(dq), _ptr(dk),
-                _ptr(dv), _ptr(delta), _ptr(self.ws), self.ws.numel(), _stream(self.dev)),
-                "lsrm_sel_attn_bwd_run")
+                _ptr(dv), _ptr(delta), _ptr(self.ws), self.ws.numel(), self.flags,
+                _stream(self.dev)), "lsrm_sel_attn_bwd_run2")
         return dq, dk, dv, delta
 
 

@@ -64,16 +64,16 @@ def _(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q, softmax_sc
 def sel_attn_bwd(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                  o: torch.Tensor, lse: torch.Tensor, topk_idx: torch.Tensor,
                  cu_seqblocks: torch.Tensor, cu_block_tokens: torch.Tensor,
-                 cu_seqlens_q: torch.Tensor, softmax_scale: float
+                 cu_seqlens_q: torch.Tensor, softmax_scale: float, key_centric: bool = False
                  ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """(dq, dk, dv, delta [Hq, Nq] fp32 = rowsum(o * do))."""
     return _sel_attn_bwd(do, q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens,
-                         cu_seqlens_q, softmax_scale)
+                         cu_seqlens_q, softmax_scale, key_centric)
 
 
 @sel_attn_bwd.register_fake
 def _(do, q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
-      softmax_scale):
+      softmax_scale, key_centric=False):
     return (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
             q.new_empty((q.shape[1], q.shape[0]), dtype=torch.float32))
 
@@ -84,13 +84,14 @@ def _fwd_setup(ctx, inputs, output):
     ctx.save_for_backward(q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens,
                           cu_seqlens_q)
     ctx.scale = scale
+    ctx.key_centric = bool(inputs[8]) if len(inputs) > 8 else False
 
 
 def _fwd_backward(ctx, do, _dlse):
     q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q = ctx.saved_tensors
     dq, dk, dv, _ = torch.ops.lsrm_hip.sel_attn_bwd(
         do.contiguous().to(q.dtype), q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens,
-        cu_seqlens_q, ctx.scale)
+        cu_seqlens_q, ctx.scale, ctx.key_centric)
     return dq, dk, dv, None, None, None, None, None, None
 
 

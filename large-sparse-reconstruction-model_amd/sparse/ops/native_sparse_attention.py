@@ -99,6 +99,7 @@ class NSA(torch.autograd.Function):
         ctx.save_for_backward(q, k, v, o, lse, cu_seqlens_q, cu_seqlens_k, topk_idx,
                               cu_seqblocks, cu_block_include_tokens)
         ctx.softmax_scale = softmax_scale
+        ctx.key_centric = _key_centric
         ctx.mark_non_differentiable(lse)
         return o, lse
 
@@ -111,7 +112,7 @@ class NSA(torch.autograd.Function):
             do = do.to(q.dtype)
         dq, dk, dv, _delta = torch.ops.lsrm_hip.sel_attn_bwd(
             do, q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_include_tokens,
-            cu_seqlens_q, float(ctx.softmax_scale))
+            cu_seqlens_q, float(ctx.softmax_scale), ctx.key_centric)
         return dq, dk, dv, None, None, None, None, None, None
 
 

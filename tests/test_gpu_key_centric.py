@@ -189,3 +189,32 @@ def test_sparse_ops_knob_with_autograd():
     assert_attn_close(kd.grad, kf.grad, "dk")
     assert_attn_close(vd.grad, vf.grad, "dv")
     assert np.isfinite(out.detach().float().cpu().numpy()).all()
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(2, 2, 64), (32, 2, 32)])
+def test_backward_gathered_dq_duplicates_empty_rows(hq, hkv, d):
+    # dQ of the flagged queries on gathered tiles (slot shares added in row
+    # order); repeated ids, rows without any block (dQ = 0, Delta still
+    # rowsum(O dO)), GQA 16 at head dim 32.
+    q, k, v, rows, cu_sb, cu_blk, cu_q = _random_rows(n=2400, hq=hq, hkv=hkv, d=d, topk=6,
+                                                      seed=12)
+    rows = rows.clone()
+    rows[:, ::3, 1] = rows[:, ::3, 0]
+    args = (q, k, v, rows, cu_sb, cu_blk, cu_q)
+    o, lse = _fwd(args, True)
+    g = torch.Generator().manual_seed(112)
+    do = (0.5 * torch.randn(q.shape, generator=g)).to(q.dtype)
+    dev = [t.to(DEV) for t in args]
+    dq, dk, dv, delta = H.sel_attn_bwd(do.to(DEV), dev[0], dev[1], dev[2], o, lse, *dev[3:],
+                                       0.125, key_centric=True)
+    qf, kf, vf = (t.float().requires_grad_() for t in (q, k, v))
+    o_ref, _ = sel_attn_ref(qf, kf, vf, rows, cu_sb, cu_blk, cu_q, 0.125)
+    o_ref.backward(do.float())
+    assert_attn_close(dq, qf.grad, "dq")
+    assert_attn_close(dk, kf.grad, "dk")
+    assert_attn_close(dv, vf.grad, "dv")
+    delta_ref = (o.float().cpu() * do.float()).sum(-1).transpose(0, 1)
+    torch.testing.assert_close(delta.cpu(), delta_ref, rtol=1e-4, atol=1e-4)
+    again = H.sel_attn_bwd(do.to(DEV), dev[0], dev[1], dev[2], o, lse, *dev[3:], 0.125,
+                           key_centric=True)
+    assert all(torch.equal(x, y) for x, y in zip((dq, dk, dv, delta), again))
