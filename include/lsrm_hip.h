@@ -21,6 +21,8 @@
  *                             plus the metadata contract the kernels assume
  *   lsrm_sel_attn_fwd         ..._impl_kvcentric.py:931-1010 (native_sparse_attn_forward)
  *   lsrm_sel_attn_bwd         ..._impl_kvcentric.py:1018-1263 (native_sparse_attn_backward)
+ *   lsrm_sel_attn_*2          the same with plan flags (LSRM_PLAN_KEY_CENTRIC: the
+ *                             key-centric forward and dQ for per-token rows)
  *   lsrm_reverse_query_map    ..._impl_kvcentric.py:575-684 (_build_reverse_query_mapping)
  *   lsrm_block_ids            builds the self-block selection that turns the
  *                             selected-attention kernels into
