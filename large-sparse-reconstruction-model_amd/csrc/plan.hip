@@ -4,9 +4,13 @@
 //
 // The reverse map replaces the reference's _count_queries_kernel /
 // _scatter_queries_kernel / host-looped segmented sort
-// (sparse/ops/triton_native_sparse_attention_impl_kvcentric.py:494-684) with
-// count -> scan -> atomic scatter -> per-segment sort, all on the device and
-// without host synchronisation.
+// (sparse/ops/triton_native_sparse_attention_impl_kvcentric.py:494-684),
+// all on the device and without host synchronisation: for rows that are
+// queries, one stable radix sort of (head * n_blocks + block, listing) pairs
+// generated in (head, query, slot) order; for rows that are run tiles,
+// count -> scan -> atomic scatter -> per-segment sort.
+#include <rocprim/device/device_radix_sort.hpp>
+
 #include "plan.h"
 
 namespace lsrm {
@@ -594,11 +598,135 @@ __global__ __launch_bounds__(256) void rev_sort_kernel(
   for (int64_t i = threadIdx.x; i < len; i += blockDim.x) seg[i] = out[i];
 }
 
+// ------------------------------------- query rows: one stable radix sort --
+
+// Pair i = (h * nq + q) * k + j: key h * nb + block for a valid slot of a
+// marked query, else the sentinel hkv * nb; value the listing (q, or
+// q * k + j when encoding the slot).  Generated in (h, q, j) order, so the
+// stable sort leaves each block's listings ascending.
+__global__ __launch_bounds__(256) void rev_pairs_kernel(
+    const int32_t* __restrict__ topk, int64_t hkv, int64_t nq, int k,
+    const int32_t* __restrict__ cu_q, int64_t batch, const int32_t* __restrict__ cu_sb,
+    int64_t nb, const uint8_t* __restrict__ only, bool encode, uint32_t* __restrict__ keys,
+    int32_t* __restrict__ vals) {
+  const int64_t hq = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // h * nq + q
+  if (hq >= hkv * nq) return;
+  const int h = (int)(hq / nq);
+  const int64_t q = hq - (int64_t)h * nq;
+  const uint32_t none = (uint32_t)(hkv * nb);
+  const bool on = !only || only[hq];
+  int b, bs, nbb;
+  bool start;
+  query_batch(cu_q, batch, cu_sb, q, &b, &bs, &nbb, &start);
+  const int32_t* row = topk + hq * k;
+  for (int j = 0; j < k; ++j) {
+    const int v = row[j];
+    const bool ok = on && v >= 0 && v < nbb && (int64_t)bs + v < nb;
+    keys[hq * k + j] = ok ? (uint32_t)(h * nb + bs + v) : none;
+    vals[hq * k + j] = encode ? (int32_t)(q * k + j) : (int32_t)q;
+  }
+}
+
+// seg[s] = first sorted position whose key is >= s, for s = 0 .. hkv * nb.
+__global__ __launch_bounds__(256) void rev_bounds_kernel(const uint32_t* __restrict__ keys,
+                                                         int64_t n, int64_t n_seg,
+                                                         int32_t* __restrict__ seg) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i > n) return;
+  const int64_t kp = i > 0 ? (int64_t)keys[i - 1] : -1;
+  const int64_t kc = i < n ? (int64_t)keys[i] : n_seg;
+  for (int64_t s = kp + 1; s <= kc && s <= n_seg; ++s) seg[s] = (int32_t)i;
+}
+
+// Per-head CSR offsets and totals from the segment starts.
+__global__ __launch_bounds__(256) void rev_offsets_kernel(const int32_t* __restrict__ seg,
+                                                          int64_t hkv, int64_t nb,
+                                                          int32_t* __restrict__ cu_rev,
+                                                          int32_t* __restrict__ totals) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= hkv * (nb + 1)) return;
+  const int64_t h = t / (nb + 1), c = t - h * (nb + 1);
+  const int32_t base = seg[h * nb];
+  cu_rev[t] = seg[h * nb + c] - base;
+  if (c == nb) totals[h] = seg[h * nb + nb] - base;
+}
+
+// rev[h * cap + pos] = the sorted listings of head h (the first seg[n_seg]
+// sorted pairs are the valid ones).
+__global__ __launch_bounds__(256) void rev_place_kernel(const uint32_t* __restrict__ keys,
+                                                        const int32_t* __restrict__ vals,
+                                                        const int32_t* __restrict__ seg,
+                                                        int64_t nb, int64_t n_seg, int64_t cap,
+                                                        int32_t* __restrict__ rev) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)seg[n_seg]) return;
+  const int64_t h = keys[i] / nb;
+  rev[h * cap + (i - seg[h * nb])] = vals[i];
+}
+
+size_t rev_sort_temp_bytes(int64_t n, unsigned bits) {
+  size_t bytes = 0;
+  (void)rocprim::radix_sort_pairs(nullptr, bytes, (const uint32_t*)nullptr,
+                                  (uint32_t*)nullptr, (const int32_t*)nullptr,
+                                  (int32_t*)nullptr, (unsigned)(n > 0 ? n : 1), 0, bits,
+                                  (hipStream_t)0);
+  return bytes;
+}
+
+int build_query_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq, int64_t topk_n,
+                            const int32_t* cu_q, int64_t batch, const int32_t* cu_sb,
+                            int64_t nb, Carver& ws, RevMap& map, hipStream_t st,
+                            const uint8_t* only, bool encode_slot) {
+  const int64_t n = hkv * nq * topk_n;
+  const int64_t n_seg = hkv * nb;
+  uint32_t* keys = ws.take<uint32_t>((size_t)(n > 0 ? n : 1));
+  uint32_t* keys_out = ws.take<uint32_t>((size_t)(n > 0 ? n : 1));
+  int32_t* vals = ws.take<int32_t>((size_t)(n > 0 ? n : 1));
+  int32_t* vals_out = ws.take<int32_t>((size_t)(n > 0 ? n : 1));
+  int32_t* seg = ws.take<int32_t>((size_t)(n_seg + 1));
+  unsigned bits = 1;  // key bits: keys are <= n_seg
+  while (bits < 32 && (1ull << bits) <= (unsigned long long)n_seg) ++bits;
+  const size_t tb = rev_sort_temp_bytes(n, bits);
+  char* temp = ws.take<char>(tb);
+  if (!map.cu_rev) map.cu_rev = ws.take<int32_t>((size_t)(hkv * (nb + 1)));
+  if (!map.rev) map.rev = ws.take<int32_t>((size_t)(hkv * (map.cap > 0 ? map.cap : 1)));
+  if (!map.totals) map.totals = ws.take<int32_t>((size_t)hkv);
+  if (!ws.base || ws.dry) return LSRM_OK;
+  if (!ws.ok()) return LSRM_ERR_WORKSPACE;
+  if (nb == 0 || n == 0) {
+    int rc = launch_zero_i32(map.cu_rev, hkv * (nb + 1), st);
+    if (rc) return rc;
+    return launch_zero_i32(map.totals, hkv, st);
+  }
+  hipLaunchKernelGGL(rev_pairs_kernel, dim3(ceil_div(hkv * nq, 256)), dim3(256), 0, st, topk,
+                     hkv, nq, (int)topk_n, cu_q, batch, cu_sb, nb, only, encode_slot, keys,
+                     vals);
+  LSRM_CHECK_LAUNCH();
+  size_t tbv = tb;
+  if (rocprim::radix_sort_pairs(temp, tbv, keys, keys_out, vals, vals_out, (unsigned)n, 0,
+                                bits, st) != hipSuccess)
+    return LSRM_ERR_LAUNCH;
+  hipLaunchKernelGGL(rev_bounds_kernel, dim3(ceil_div(n + 1, 256)), dim3(256), 0, st, keys_out,
+                     n, n_seg, seg);
+  LSRM_CHECK_LAUNCH();
+  hipLaunchKernelGGL(rev_offsets_kernel, dim3(ceil_div(hkv * (nb + 1), 256)), dim3(256), 0, st,
+                     seg, hkv, nb, map.cu_rev, map.totals);
+  LSRM_CHECK_LAUNCH();
+  hipLaunchKernelGGL(rev_place_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, st, keys_out,
+                     vals_out, seg, nb, n_seg, map.cap, map.rev);
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
+}
+
 int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
                       int64_t topk_n, const int32_t* cu_q, int64_t batch,
                       const int32_t* cu_sb, int64_t nb, bool rows_are_tiles,
                       const TilePlan* plan, Carver& ws, RevMap& map,
                       hipStream_t st, const uint8_t* only, bool encode_slot) {
+  if (!rows_are_tiles && hkv * nq * topk_n < (int64_t{1} << 31) &&
+      hkv * nb < (int64_t{1} << 31))
+    return build_query_reverse_map(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, nb, ws, map, st,
+                                   only, encode_slot);
   int32_t* counts = ws.take<int32_t>((size_t)(hkv * (nb > 0 ? nb : 1)));
   int32_t* fill = ws.take<int32_t>((size_t)(hkv * (nb > 0 ? nb : 1)));
   int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, hkv));
