@@ -963,16 +963,28 @@ __global__ __launch_bounds__(256) void kc_dq_merge_kernel(AttnArgs a) {
     const int32_t* row = a.topk + hq_idx * a.topk_n;
     float acc[CPT] = {0.0f, 0.0f, 0.0f, 0.0f};
     bool any = false;
-    for (int j = 0; j < a.topk_n; ++j) {
-      const int v = row[j];
-      if (!(v >= 0 && v < nbb && (int64_t)bs + v < a.nb)) continue;
-      any = true;
-      const int64_t pidx = (hq_idx * a.topk_n + j) * a.g + gi;
-      const u32x2 pv = *reinterpret_cast<const u32x2*>(a.kc.part_o + pidx * D + d0);
-      acc[0] += to_f32<DT>((uint16_t)(pv[0] & 0xffffu));
-      acc[1] += to_f32<DT>((uint16_t)(pv[0] >> 16));
-      acc[2] += to_f32<DT>((uint16_t)(pv[1] & 0xffffu));
-      acc[3] += to_f32<DT>((uint16_t)(pv[1] >> 16));
+    constexpr int U = 8;  // slots whose shares are loaded together
+    for (int j0 = 0; j0 < a.topk_n; j0 += U) {
+      u32x2 pv[U];
+      bool ok[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int j = j0 + u;
+        const int v = j < a.topk_n ? row[j] : -1;
+        ok[u] = v >= 0 && v < nbb && (int64_t)bs + v < a.nb;
+        const int64_t pidx = (hq_idx * a.topk_n + (ok[u] ? j : 0)) * a.g + gi;
+        pv[u] = ok[u] ? *reinterpret_cast<const u32x2*>(a.kc.part_o + pidx * D + d0)
+                      : u32x2{0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (!ok[u]) continue;
+        any = true;
+        acc[0] += to_f32<DT>((uint16_t)(pv[u][0] & 0xffffu));
+        acc[1] += to_f32<DT>((uint16_t)(pv[u][0] >> 16));
+        acc[2] += to_f32<DT>((uint16_t)(pv[u][1] & 0xffffu));
+        acc[3] += to_f32<DT>((uint16_t)(pv[u][1] >> 16));
+      }
     }
     const int hh = h * a.g + gi;
     *reinterpret_cast<u32x2*>(a.out + (q * a.hq + hh) * D + d0) =

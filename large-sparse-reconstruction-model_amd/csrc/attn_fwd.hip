@@ -124,6 +124,14 @@ sel_attn_fwd_kernel(AttnArgs a) {
       ge0 = it.y;
       q0 = 0;
       qn = it.z;
+      // blocks of 1..KC_RES_KEYS keys belong to kc_resident_fwd_kernel
+      int64_t bs0 = a.cu_blk[gblk], bs1 = a.cu_blk[gblk + 1];
+      bs0 = bs0 < 0 ? 0 : (bs0 > a.nk ? a.nk : bs0);
+      bs1 = bs1 < bs0 ? bs0 : (bs1 > a.nk ? a.nk : bs1);
+      if (bs1 > bs0 && bs1 - bs0 <= KC_RES_KEYS) {
+        __syncthreads();  // every wave has read s_slot before it is reused
+        continue;
+      }
     } else {
       // Key-centric plans: flagged grouped tiles belong to the gathered pass.
       if constexpr (UNION) {
@@ -642,6 +650,182 @@ int launch_kc_flags(const AttnArgs& a, uint8_t* gflag, hipStream_t st) {
   return LSRM_OK;
 }
 
+// Key-centric forward of blocks with 1..KC_RES_KEYS keys: the block's K and
+// V (at most four 64-key tiles) are copied into LDS once per item and stay
+// resident while the item's query chunks (up to KC_RES_CHUNKS x 128 rows of
+// gathered listings) run over them: S^T = K Q^T and O^T += V^T P^T as in the
+// streaming kernel, an online softmax with lazy rescaling (the reference
+// moves when a tile's row maximum exceeds it by more than RESCALE_LOG2), and
+// the row's partial result (O / l in the input type and its log2 LSE)
+// written at [head, query, slot] for kc_merge_kernel.
+template <int DT, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+kc_resident_fwd_kernel(AttnArgs a) {
+  using G = KvTile<D>;
+  constexpr int NS = D / 16;
+  constexpr int ND = D / 32;
+  constexpr int NT = KC_RES_KEYS / KT;
+  __shared__ __align__(1024) char sK[NT][G::BYTES];
+  __shared__ __align__(1024) char sV[NT][G::BYTES];
+  __shared__ int s_slot;
+  const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
+  const int hb = lane >> 5, l32 = lane & 31;
+  const int32_t* head_off = a.kc.ritem_off;
+  int32_t* queue = a.plan.counter + KC_RQUEUE_SLOT;
+  const int total = head_off[a.hkv];
+  const uint32_t row_bytes = (uint32_t)a.hkv * D * 2;
+  const int tq = ROWS / a.g;
+  const int64_t cap = a.kc.grev.cap;
+
+  for (;;) {
+    const int w = uniform(fetch_work(queue, &s_slot));
+    if (w >= total) break;
+    const int h = head_of(head_off, a.hkv, w);
+    const int4 it = a.kc.ritems[(int64_t)h * a.kc.ritem_cap + (w - head_off[h])];
+    const int c = it.x, e0 = it.y, n = it.z;
+    int64_t s0 = a.cu_blk[c], s1 = a.cu_blk[c + 1];
+    s0 = s0 < 0 ? 0 : (s0 > a.nk ? a.nk : s0);
+    s1 = s1 < s0 ? s0 : (s1 > a.nk ? a.nk : s1);
+    const int len = uniform((int)(s1 - s0));  // 1..KC_RES_KEYS (plan)
+    const int ntiles = (len + KT - 1) / KT;
+    const char* kbase = reinterpret_cast<const char*>(a.k + (int64_t)h * D);
+    const char* vbase = reinterpret_cast<const char*>(a.v + (int64_t)h * D);
+    // The block into LDS: tile t, load j of this wave covers rows
+    // (wv * LPW + j) * KPL + lane / CH; keys past the block load its first
+    // token (in bounds; masked below).
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (t < ntiles) {
+#pragma unroll
+        for (int j = 0; j < G::LPW; ++j) {
+          const int row = (wv * G::LPW + j) * G::KPL + lane / G::CH;
+          const int key = t * KT + row;
+          const uint32_t tok = (uint32_t)(key < len ? s0 + key : s0);
+          const uint32_t voff = tok * row_bytes + (((lane % G::CH) ^ G::swz(row)) << 4);
+          const uint32_t dst = (uint32_t)(wv * G::LPW + j) * 1024;
+          copy16_to_lds(kbase, voff, lds_addr(sK[t]) + dst);
+          copy16_to_lds(vbase, voff, lds_addr(sV[t]) + dst);
+        }
+      }
+    }
+    wait_copies();
+    __syncthreads();
+
+    for (int cb = 0; cb < n; cb += tq) {
+      const int rows = (n - cb < tq ? n - cb : tq) * a.g;
+      const int r = wv * 32 + l32;
+      const bool row_ok = r < rows;
+      if (wv * 32 >= rows) continue;  // wave-uniform: no row of this chunk
+      const int64_t lv = a.kc.grev.rev[(int64_t)h * cap + e0 + cb + (row_ok ? r / a.g : 0)];
+      const int64_t qi = lv / a.topk_n;
+      const int64_t slot = lv - qi * a.topk_n;
+      const int hh = h * a.g + (row_ok ? r % a.g : 0);
+      u32x4 qb[NS];
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        qb[s] = row_ok ? *reinterpret_cast<const u32x4*>(a.q + (qi * a.hq + hh) * D + s * 16 +
+                                                         hb * 8)
+                       : u32x4{0u, 0u, 0u, 0u};
+      f32x16 oacc[ND];
+#pragma unroll
+      for (int i = 0; i < ND; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
+      float m_run = 0.0f, l_run = 0.0f;
+      for (int kt = 0; kt < ntiles; ++kt) {
+        f32x16 sc[2];
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) sc[blk][v] = 0.0f;
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            const u32x4 ka =
+                *reinterpret_cast<const u32x4*>(sK[kt] + G::off(blk * 32 + l32, 2 * s + hb));
+            sc[blk] = mfma32<DT>(ka, qb[s], sc[blk]);
+          }
+        }
+        if (kt * KT + KT > len) {
+#pragma unroll
+          for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              if (kt * KT + blk * 32 + acc_row(v, hb) >= len) sc[blk][v] = -__builtin_inf();
+        }
+        const float m_tile = row_max(sc) * a.scale_log2;  // tile 0 holds a key: finite
+        if (kt == 0) {
+          m_run = m_tile;
+        } else if (__builtin_amdgcn_ballot_w64(m_tile > m_run + RESCALE_LOG2) != 0) {
+          const float m_new = __builtin_elementwise_maximum(m_run, m_tile);
+          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+          m_run = m_new;
+          l_run *= alpha;
+#pragma unroll
+          for (int db = 0; db < ND; ++db)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) oacc[db][v] *= alpha;
+        }
+        u32x4 pb[2][2];
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+          float p[16];
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v], a.scale_log2, -m_run));
+#pragma unroll
+          for (int cc = 0; cc < 2; ++cc) {
+            pb[blk][cc] = u32x4{pack2<DT>(p[cc * 8 + 0], p[cc * 8 + 1]),
+                                pack2<DT>(p[cc * 8 + 2], p[cc * 8 + 3]),
+                                pack2<DT>(p[cc * 8 + 4], p[cc * 8 + 5]),
+                                pack2<DT>(p[cc * 8 + 6], p[cc * 8 + 7])};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) l_run = sum2<DT>(pb[blk][cc][e], l_run);
+          }
+        }
+        const int gi = lane & 15, dh = (lane >> 4) & 1;
+#pragma unroll
+        for (int db = 0; db < ND; ++db) {
+          const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+#pragma unroll
+          for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+              const int k0 = blk * 32 + cc * 16 + hb * 4 + (gi >> 2);
+              const int cbk = dcol >> 3, half = (dcol & 4) * 2;
+              const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_s16x4*)(sV[kt] + G::off(k0, cbk) + half));
+              const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_s16x4*)(sV[kt] + G::off(k0 + 8, cbk) + half));
+              const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+              const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+              oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]}, pb[blk][cc], oacc[db]);
+            }
+        }
+      }
+      const float l_tot = l_run + __shfl_xor(l_run, 32);
+      if (row_ok) {
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        const int64_t pidx = (((int64_t)h * a.nq + qi) * a.topk_n + slot) * a.g + (r % a.g);
+        uint16_t* orow = a.kc.part_o + pidx * D;
+#pragma unroll
+        for (int db = 0; db < ND; ++db)
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi) {
+            const int v = gi * 4;
+            *reinterpret_cast<u32x2*>(orow + db * 32 + gi * 8 + hb * 4) =
+                u32x2{pack2<DT>(oacc[db][v] * inv, oacc[db][v + 1] * inv),
+                      pack2<DT>(oacc[db][v + 2] * inv, oacc[db][v + 3] * inv)};
+          }
+        if (hb == 0)
+          a.kc.part_lse[pidx] = l_tot > 0.0f ? m_run + log2f(l_tot) : -__builtin_inf();
+      }
+    }
+    __syncthreads();  // the item's reads of sK / sV end before the next copies
+  }
+  wait_copies();
+  leave_queue(queue, queue + 2);
+}
+
 // Key-centric merge: one thread per (kv head, query, query head, 4 output
 // channels) of the marked queries.  The partials of the row's valid slots
 // (the gathered tiles wrote one per slot naming a block) are combined in
@@ -651,6 +835,7 @@ int launch_kc_flags(const AttnArgs& a, uint8_t* gflag, hipStream_t st) {
 template <int DT, int D>
 __global__ __launch_bounds__(256) void kc_merge_kernel(AttnArgs a) {
   constexpr int CPT = 4;  // output channels per thread
+  constexpr int U = 8;    // slots whose partials are loaded together
   const int64_t per_q = (int64_t)a.g * (D / CPT);
   const int64_t n_items = (int64_t)a.hkv * a.nq * per_q;
   for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
@@ -667,25 +852,42 @@ __global__ __launch_bounds__(256) void kc_merge_kernel(AttnArgs a) {
     const int32_t* row = a.topk + hq_idx * a.topk_n;
     const int64_t pbase = hq_idx * a.topk_n;  // partial (q, slot 0)
     float mx = -__builtin_inf();
-    for (int j = 0; j < a.topk_n; ++j) {
-      const int v = row[j];
-      if (v >= 0 && v < nbb && (int64_t)bs + v < a.nb)
-        mx = __builtin_elementwise_maximum(mx, a.kc.part_lse[(pbase + j) * a.g + gi]);
-    }
     float acc[CPT] = {0.0f, 0.0f, 0.0f, 0.0f};
     float wsum = 0.0f;
-    if (mx > -__builtin_inf()) {
-      for (int j = 0; j < a.topk_n; ++j) {
-        const int v = row[j];
-        if (!(v >= 0 && v < nbb && (int64_t)bs + v < a.nb)) continue;
-        const int64_t pidx = (pbase + j) * a.g + gi;
-        const float wj = __builtin_amdgcn_exp2f(a.kc.part_lse[pidx] - mx);
-        const u32x2 ov = *reinterpret_cast<const u32x2*>(a.kc.part_o + pidx * D + d0);
-        wsum += wj;
-        acc[0] += wj * to_f32<DT>((uint16_t)(ov[0] & 0xffffu));
-        acc[1] += wj * to_f32<DT>((uint16_t)(ov[0] >> 16));
-        acc[2] += wj * to_f32<DT>((uint16_t)(ov[1] & 0xffffu));
-        acc[3] += wj * to_f32<DT>((uint16_t)(ov[1] >> 16));
+    // Pass 1: the maximum LSE; pass 2: weights and weighted outputs, slot by
+    // slot in row order.  Slots are taken U at a time so that their loads
+    // are in flight together (a slot without a block loads nothing).
+    for (int pass = 0; pass < 2; ++pass) {
+      if (pass == 1 && !(mx > -__builtin_inf())) break;
+      for (int j0 = 0; j0 < a.topk_n; j0 += U) {
+        float l[U];
+        u32x2 ov[U];
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int j = j0 + u;
+          const int v = j < a.topk_n ? row[j] : -1;
+          ok[u] = v >= 0 && v < nbb && (int64_t)bs + v < a.nb;
+          const int64_t pidx = (pbase + (ok[u] ? j : 0)) * a.g + gi;
+          l[u] = ok[u] ? a.kc.part_lse[pidx] : -__builtin_inf();
+          if (pass == 1)
+            ov[u] = ok[u] ? *reinterpret_cast<const u32x2*>(a.kc.part_o + pidx * D + d0)
+                          : u32x2{0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (!ok[u]) continue;
+          if (pass == 0) {
+            mx = __builtin_elementwise_maximum(mx, l[u]);
+          } else {
+            const float wj = __builtin_amdgcn_exp2f(l[u] - mx);
+            wsum += wj;
+            acc[0] += wj * to_f32<DT>((uint16_t)(ov[u][0] & 0xffffu));
+            acc[1] += wj * to_f32<DT>((uint16_t)(ov[u][0] >> 16));
+            acc[2] += wj * to_f32<DT>((uint16_t)(ov[u][1] & 0xffffu));
+            acc[3] += wj * to_f32<DT>((uint16_t)(ov[u][1] >> 16));
+          }
+        }
       }
     }
     const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
@@ -719,6 +921,11 @@ int launch_fwd_t(const AttnArgs& a, hipStream_t st) {
     if (gg <= 0) return LSRM_ERR_LAUNCH;
     hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, FWD_GATHER>), dim3(gg), dim3(256), 0, st,
                        a);
+    LSRM_CHECK_LAUNCH();
+    const void* fr = reinterpret_cast<const void*>(&kc_resident_fwd_kernel<DT, D>);
+    const int gr = persistent_grid(fr, 256, 0);
+    if (gr <= 0) return LSRM_ERR_LAUNCH;
+    hipLaunchKernelGGL((kc_resident_fwd_kernel<DT, D>), dim3(gr), dim3(256), 0, st, a);
     LSRM_CHECK_LAUNCH();
     const int gm = device_cu_count() * 16;
     if (gm <= 0) return LSRM_ERR_LAUNCH;

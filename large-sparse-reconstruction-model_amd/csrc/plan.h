@@ -82,12 +82,24 @@ struct KcPlan {
   int32_t* item_off;     // [hkv + 1]
   uint16_t* part_o;      // [hkv, n_q, topk, g, D] input type
   float* part_lse;       // [hkv, n_q, topk, g]
+  // Forward items of blocks with at most KC_RES_KEYS keys, which the
+  // forward runs with the block resident in LDS: {c, e0, n, 0} with up to
+  // KC_RES_CHUNKS * tq listings (the streaming gathered forward skips these
+  // blocks; dQ takes every block from `items`).
+  int4* ritems;
+  int64_t ritem_cap;
+  int32_t* ritem_count;  // [hkv]
+  int32_t* ritem_off;    // [hkv + 1]
 };
-// Work counters of the gathered-tile kernel inside TilePlan::counter.
+// Work counters of the gathered-tile kernels inside TilePlan::counter.
 constexpr int KC_QUEUE_SLOT = 16, KC_EXIT_SLOT = 18;
+constexpr int KC_RQUEUE_SLOT = 20, KC_REXIT_SLOT = 22;
+constexpr int KC_RES_KEYS = 256;   // 4 key tiles of K and V resident in LDS
+constexpr int KC_RES_CHUNKS = 8;   // query chunks of tq listings per resident item
 
-int build_kc_items(const RevMap& grev, int64_t hkv, int64_t nb, int tq, Carver& ws,
-                   KcPlan& kc, int32_t* counter, hipStream_t st);
+int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
+                   int64_t nb, int tq, Carver& ws, KcPlan& kc, int32_t* counter,
+                   hipStream_t st);
 int mark_flagged_queries(const TilePlan& plan, const uint8_t* gflag, int64_t hkv,
                          int64_t nq, uint8_t* qmark, hipStream_t st);
 

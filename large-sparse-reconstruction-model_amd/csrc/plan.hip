@@ -823,13 +823,29 @@ int mark_flagged_queries(const TilePlan& plan, const uint8_t* gflag, int64_t hkv
   return LSRM_OK;
 }
 
+// Token count of block c, clamped as the attention kernels clamp it.
+__device__ inline int64_t kc_block_len(const int32_t* cu_blk, int64_t nk, int64_t c) {
+  int64_t s0 = cu_blk[c], s1 = cu_blk[c + 1];
+  s0 = s0 < 0 ? 0 : (s0 > nk ? nk : s0);
+  s1 = s1 < s0 ? s0 : (s1 > nk ? nk : s1);
+  return s1 - s0;
+}
+
 // Gathered tiles of block c: ceil(listings / tq) pieces of its grev segment.
+// With `res` set, only blocks of 1..KC_RES_KEYS keys count (the resident
+// forward's items); with cu_blk null, every block counts.
 struct KcItemsF {
   const int32_t* cu_rev;
   int64_t nb, cap;
   int tq;
+  const int32_t* cu_blk;
+  int64_t nk;
   __device__ int64_t limit(int, int64_t n) const { return n; }
   __device__ int operator()(int h, int64_t c) const {
+    if (cu_blk) {
+      const int64_t len = kc_block_len(cu_blk, nk, c);
+      if (len <= 0 || len > KC_RES_KEYS) return 0;
+    }
     const int32_t* p = cu_rev + (int64_t)h * (nb + 1);
     int64_t s = p[c], e = p[c + 1];
     e = e < cap ? e : cap;
@@ -843,6 +859,7 @@ struct KcItemsW {
   int4* items;
   int64_t item_cap;
   __device__ void operator()(int h, int64_t c, int ex, int v, int64_t) const {
+    if (v == 0) return;
     const int32_t* p = cu_rev + (int64_t)h * (nb + 1);
     const int64_t s = p[c];
     int64_t e = p[c + 1];
@@ -855,37 +872,54 @@ struct KcItemsW {
   }
 };
 
-__global__ void kc_offsets_kernel(const int32_t* count, int hkv, int32_t* off,
-                                  int32_t* counter) {
+__global__ void kc_offsets_kernel(const int32_t* count, const int32_t* rcount, int hkv,
+                                  int32_t* off, int32_t* roff, int32_t* counter) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
-    int acc = 0;
+    int acc = 0, racc = 0;
     off[0] = 0;
+    roff[0] = 0;
     for (int h = 0; h < hkv; ++h) {
       acc += count[h];
+      racc += rcount[h];
       off[h + 1] = acc;
+      roff[h + 1] = racc;
     }
     counter[KC_QUEUE_SLOT] = 0;
     counter[KC_EXIT_SLOT] = 0;
+    counter[KC_RQUEUE_SLOT] = 0;
+    counter[KC_REXIT_SLOT] = 0;
   }
 }
 
-int build_kc_items(const RevMap& grev, int64_t hkv, int64_t nb, int tq, Carver& ws,
-                   KcPlan& kc, int32_t* counter, hipStream_t st) {
+int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
+                   int64_t nb, int tq, Carver& ws, KcPlan& kc, int32_t* counter,
+                   hipStream_t st) {
+  const int rq = tq * KC_RES_CHUNKS;
   kc.item_cap = grev.cap / (tq > 0 ? tq : 1) + nb + 1;
   kc.items = ws.take<int4>((size_t)(hkv * kc.item_cap));
   kc.item_count = ws.take<int32_t>((size_t)hkv);
   kc.item_off = ws.take<int32_t>((size_t)(hkv + 1));
+  kc.ritem_cap = grev.cap / (rq > 0 ? rq : 1) + nb + 1;
+  kc.ritems = ws.take<int4>((size_t)(hkv * kc.ritem_cap));
+  kc.ritem_count = ws.take<int32_t>((size_t)hkv);
+  kc.ritem_off = ws.take<int32_t>((size_t)(hkv + 1));
   int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, hkv));
   if (!ws.base || ws.dry) return LSRM_OK;
   if (!ws.ok()) return LSRM_ERR_WORKSPACE;
   int rc = launch_zero_i32(kc.item_count, hkv, st);
   if (rc) return rc;
-  rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, tq},
+  rc = launch_zero_i32(kc.ritem_count, hkv, st);
+  if (rc) return rc;
+  rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, tq, nullptr, nk},
                 KcItemsW{grev.cu_rev, nb, grev.cap, tq, kc.items, kc.item_cap}, nb, (int)hkv,
                 sums, kc.item_count, st);
   if (rc) return rc;
-  hipLaunchKernelGGL(kc_offsets_kernel, dim3(1), dim3(64), 0, st, kc.item_count, (int)hkv,
-                     kc.item_off, counter);
+  rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, rq, cu_blk, nk},
+                KcItemsW{grev.cu_rev, nb, grev.cap, rq, kc.ritems, kc.ritem_cap}, nb,
+                (int)hkv, sums, kc.ritem_count, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(kc_offsets_kernel, dim3(1), dim3(64), 0, st, kc.item_count,
+                     kc.ritem_count, (int)hkv, kc.item_off, kc.ritem_off, counter);
   LSRM_CHECK_LAUNCH();
   return LSRM_OK;
 }

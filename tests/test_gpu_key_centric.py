@@ -20,14 +20,15 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def _random_rows(n=6000, hq=2, hkv=2, topk=12, seed=4, d=64, dtype=torch.bfloat16):
+def _random_rows(n=6000, hq=2, hkv=2, topk=12, seed=4, d=64, dtype=torch.bfloat16,
+                 sizes=(4, 17)):
     """Blocks of 4..16 tokens (about n / 10 of them) with unrelated random rows
     per token, as learned selections on unstructured data: 96 consecutive
     queries list several hundred distinct blocks, more than one masked union
     pass takes, so the grouped tiles go to the key-centric pass.  -1 padding,
     out-of-range ids and empty rows included."""
     rng = np.random.default_rng(seed)
-    sizes = rng.integers(4, 17, size=n // 4)
+    sizes = rng.integers(sizes[0], sizes[1], size=n // sizes[0])
     cu = np.concatenate([[0], np.cumsum(sizes)])
     cu = cu[cu <= n]
     cu[-1] = n
@@ -218,3 +219,14 @@ def test_backward_gathered_dq_duplicates_empty_rows(hq, hkv, d):
     again = H.sel_attn_bwd(do.to(DEV), dev[0], dev[1], dev[2], o, lse, *dev[3:], 0.125,
                            key_centric=True)
     assert all(torch.equal(x, y) for x, y in zip((dq, dk, dv, delta), again))
+
+
+def test_large_and_small_blocks_both_gathered_kernels():
+    # Blocks of 4..600 keys: those of at most 256 keys run with the block
+    # resident in LDS, the larger ones through the streaming gathered tiles.
+    args = _random_rows(n=20000, topk=8, seed=13, sizes=(4, 600))
+    cu = args[5]
+    lens = cu[1:] - cu[:-1]
+    assert (lens > 256).any() and (lens <= 256).any()
+    o, lse = _fwd(args, True)
+    _check_oracle(args, o, lse)
