@@ -27,12 +27,16 @@ constexpr int SEL_MAX_CAND = 65536;     // bitmap capacity (blocks per batch)
 constexpr int SEL_MAXK = 256;
 
 // scores[h, b, c] for b, c in [0, nb): 64x64 tile per workgroup, 4x4 per
-// thread, fp64 accumulation over (g, d) in order.
+// thread, fp64 accumulation over (g, d) in order.  The pooled rows are staged
+// in LDS as doubles, SCORE_DC head-dim columns at a time (converted once per
+// element instead of at every use; the values and the order of the fused
+// multiply-adds are unchanged).
+constexpr int SCORE_DC = 32;
 __global__ __launch_bounds__(256) void score_kernel(
     const float* __restrict__ pq, const float* __restrict__ pk, int64_t nb,
     int hq, int hkv, int d, double* __restrict__ scores) {
-  __shared__ float sq[SCORE_TILE][SEL_MAXD + 1];
-  __shared__ float sk[SCORE_TILE][SEL_MAXD + 1];
+  __shared__ double sq[SCORE_TILE][SCORE_DC + 1];
+  __shared__ double sk[SCORE_TILE][SCORE_DC + 1];
   const int h = blockIdx.z;
   const int64_t b0 = (int64_t)blockIdx.y * SCORE_TILE;
   const int64_t c0 = (int64_t)blockIdx.x * SCORE_TILE;
@@ -44,29 +48,34 @@ __global__ __launch_bounds__(256) void score_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
 
-  for (int i = threadIdx.x; i < SCORE_TILE * d; i += 256) {
-    const int r = i / d, dd = i - r * d;
-    sk[r][dd] = (c0 + r < nb) ? pk[(c0 + r) * (int64_t)hkv * d + (int64_t)h * d + dd] : 0.0f;
-  }
   for (int g = 0; g < g_n; ++g) {
     const int hh = h * g_n + g;
-    for (int i = threadIdx.x; i < SCORE_TILE * d; i += 256) {
-      const int r = i / d, dd = i - r * d;
-      sq[r][dd] = (b0 + r < nb) ? pq[(b0 + r) * (int64_t)hq * d + (int64_t)hh * d + dd] : 0.0f;
+    for (int dc = 0; dc < d; dc += SCORE_DC) {
+      const int dn = d - dc < SCORE_DC ? d - dc : SCORE_DC;
+      for (int i = threadIdx.x; i < SCORE_TILE * SCORE_DC; i += 256) {
+        const int r = i / SCORE_DC, dd = i - r * SCORE_DC;
+        const bool in_d = dd < dn;
+        sq[r][dd] = (in_d && b0 + r < nb)
+                        ? (double)pq[(b0 + r) * (int64_t)hq * d + (int64_t)hh * d + dc + dd]
+                        : 0.0;
+        sk[r][dd] = (in_d && c0 + r < nb)
+                        ? (double)pk[(c0 + r) * (int64_t)hkv * d + (int64_t)h * d + dc + dd]
+                        : 0.0;
+      }
+      __syncthreads();
+      for (int dd = 0; dd < dn; ++dd) {
+        double a[4], bv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = sq[ty * 4 + i][dd];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bv[j] = sk[tx * 4 + j][dd];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fma(a[i], bv[j], acc[i][j]);
+      }
+      __syncthreads();
     }
-    __syncthreads();
-    for (int dd = 0; dd < d; ++dd) {
-      double a[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = (double)sq[ty * 4 + i][dd];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = (double)sk[tx * 4 + j][dd];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fma(a[i], bv[j], acc[i][j]);
-    }
-    __syncthreads();
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
