@@ -66,6 +66,8 @@ sel_attn_dq_kernel(AttnArgs a) {
   // A plan built without its backward part: nothing here is valid to read.
   if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC) return;
   const int total = head_off[a.hkv];
+  // An empty queue: leave it untouched (no fetch, so nothing to reset).
+  if (total == 0) return;
 
   int ld_key[G::LPW], ld_byte[G::LPW];
 #pragma unroll

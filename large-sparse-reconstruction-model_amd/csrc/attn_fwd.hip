@@ -97,6 +97,8 @@ sel_attn_fwd_kernel(AttnArgs a) {
   const int2* tiles = UNION ? a.plan.gtiles : a.plan.tiles;
   int32_t* queue = a.plan.counter + (GATHER ? KC_QUEUE_SLOT : (UNION ? 4 : 0));
   const int total = head_off[a.hkv];
+  // An empty queue: leave it untouched (no fetch, so nothing to reset).
+  if (total == 0) return;
 
   // Loader geometry: load j of this wave covers keys (wv*LPW + j)*KPL + ...
   int ld_key[G::LPW], ld_byte[G::LPW];
@@ -673,6 +675,8 @@ kc_resident_fwd_kernel(AttnArgs a) {
   const int32_t* head_off = a.kc.ritem_off;
   int32_t* queue = a.plan.counter + KC_RQUEUE_SLOT;
   const int total = head_off[a.hkv];
+  // An empty queue: leave it untouched (no fetch, so nothing to reset).
+  if (total == 0) return;
   const uint32_t row_bytes = (uint32_t)a.hkv * D * 2;
   const int tq = ROWS / a.g;
   const int64_t cap = a.kc.grev.cap;
