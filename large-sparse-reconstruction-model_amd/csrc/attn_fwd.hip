@@ -656,10 +656,11 @@ int launch_kc_flags(const AttnArgs& a, uint8_t* gflag, hipStream_t st) {
 // V (at most four 64-key tiles) are copied into LDS once per item and stay
 // resident while the item's query chunks (up to KC_RES_CHUNKS x 128 rows of
 // gathered listings) run over them: S^T = K Q^T and O^T += V^T P^T as in the
-// streaming kernel, an online softmax with lazy rescaling (the reference
-// moves when a tile's row maximum exceeds it by more than RESCALE_LOG2), and
-// the row's partial result (O / l in the input type and its log2 LSE)
-// written at [head, query, slot] for kc_merge_kernel.
+// streaming kernel.  With at most four key tiles, a chunk first computes all
+// of its scores and the exact row maximum (the softmax reference), then the
+// exponentials, row sums and P.V tile by tile; the row's partial result
+// (O / l in the input type and its log2 LSE) is written at [head, query,
+// slot] for kc_merge_kernel.
 template <int DT, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 kc_resident_fwd_kernel(AttnArgs a) {
@@ -715,95 +716,131 @@ kc_resident_fwd_kernel(AttnArgs a) {
     wait_copies();
     __syncthreads();
 
-    for (int cb = 0; cb < n; cb += tq) {
-      const int rows = (n - cb < tq ? n - cb : tq) * a.g;
-      const int r = wv * 32 + l32;
-      const bool row_ok = r < rows;
-      if (wv * 32 >= rows) continue;  // wave-uniform: no row of this chunk
-      const int64_t lv = a.kc.grev.rev[(int64_t)h * cap + e0 + cb + (row_ok ? r / a.g : 0)];
-      const int64_t qi = lv / a.topk_n;
-      const int64_t slot = lv - qi * a.topk_n;
-      const int hh = h * a.g + (row_ok ? r % a.g : 0);
-      u32x4 qb[NS];
+    // The gathered rows of chunk cb: listing -> (query, slot) -> Q row.  The
+    // listings are loaded two chunks ahead and the Q rows one chunk ahead,
+    // so a chunk's dependent gathers are in flight during the chunk before.
+    const int r = wv * 32 + l32;
+    auto chunk_ok = [&](int cbx) { return r < (n - cbx < tq ? n - cbx : tq) * a.g; };
+    auto load_listing = [&](int cbx) -> int32_t {
+      return cbx < n ? a.kc.grev.rev[(int64_t)h * cap + e0 + cbx + (chunk_ok(cbx) ? r / a.g : 0)]
+                     : 0;
+    };
+    auto load_q = [&](int cbx, int32_t lv, u32x4* dst) {
+      const int64_t qx = lv / a.topk_n;
+      const int hx = h * a.g + (chunk_ok(cbx) ? r % a.g : 0);
 #pragma unroll
       for (int s = 0; s < NS; ++s)
-        qb[s] = row_ok ? *reinterpret_cast<const u32x4*>(a.q + (qi * a.hq + hh) * D + s * 16 +
-                                                         hb * 8)
-                       : u32x4{0u, 0u, 0u, 0u};
+        dst[s] = (cbx < n && chunk_ok(cbx))
+                     ? *reinterpret_cast<const u32x4*>(a.q + (qx * a.hq + hx) * D + s * 16 + hb * 8)
+                     : u32x4{0u, 0u, 0u, 0u};
+    };
+    int32_t lv_cur = load_listing(0);
+    u32x4 q_next[NS];
+    load_q(0, lv_cur, q_next);
+    int32_t lv_next = load_listing(tq);
+    for (int cb = 0; cb < n; cb += tq) {
+      const int rows = (n - cb < tq ? n - cb : tq) * a.g;
+      const bool row_ok = r < rows;
+      u32x4 qb[NS];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) qb[s] = q_next[s];
+      const int64_t qi = lv_cur / a.topk_n;
+      const int64_t slot = lv_cur - qi * a.topk_n;
+      // next chunk: its Q rows from the listing loaded one chunk ago; the
+      // listing after it
+      load_q(cb + tq, lv_next, q_next);
+      lv_cur = lv_next;
+      lv_next = load_listing(cb + 2 * tq);
+      if (wv * 32 >= rows) continue;  // wave-uniform: no row of this chunk
       f32x16 oacc[ND];
 #pragma unroll
       for (int i = 0; i < ND; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
-      float m_run = 0.0f, l_run = 0.0f;
-      for (int kt = 0; kt < ntiles; ++kt) {
-        f32x16 sc[2];
+      // Phase 1: the scores of every tile of the block (at most NT), keys
+      // past the block masked, and the exact row maximum.
+      f32x16 sc[NT][2];
+      float mx = -__builtin_inf();
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
+      for (int kt = 0; kt < NT; ++kt) {
+        if (kt < ntiles) {
 #pragma unroll
-          for (int v = 0; v < 16; ++v) sc[blk][v] = 0.0f;
+          for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const u32x4 ka =
-                *reinterpret_cast<const u32x4*>(sK[kt] + G::off(blk * 32 + l32, 2 * s + hb));
-            sc[blk] = mfma32<DT>(ka, qb[s], sc[blk]);
+            for (int v = 0; v < 16; ++v) sc[kt][blk][v] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+              const u32x4 ka = *reinterpret_cast<const u32x4*>(
+                  sK[kt] + G::off(blk * 32 + l32, 2 * s + hb));
+              sc[kt][blk] = mfma32<DT>(ka, qb[s], sc[kt][blk]);
+            }
           }
-        }
-        if (kt * KT + KT > len) {
+          if (kt * KT + KT > len) {
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+              for (int v = 0; v < 16; ++v)
+                if (kt * KT + blk * 32 + acc_row(v, hb) >= len) sc[kt][blk][v] = -__builtin_inf();
+          }
 #pragma unroll
           for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+            for (int v = 0; v < 16; v += 4)
+              mx = __builtin_elementwise_maximum(
+                  mx, max3f(sc[kt][blk][v], sc[kt][blk][v + 1],
+                            __builtin_elementwise_maximum(sc[kt][blk][v + 2], sc[kt][blk][v + 3])));
+        }
+      }
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
+                                                         __builtin_bit_cast(unsigned, mx),
+                                                         false, false);
+        mx = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)sw[0]),
+                                           __builtin_bit_cast(float, (unsigned)sw[1]));
+      }
+      const float m_run = mx * a.scale_log2;  // tile 0 holds a key: finite
+      float l_run = 0.0f;
+      // Phase 2: P = exp2(s * scale * log2(e) - m) rounded to the input type,
+      // row sums, O^T += V^T P^T, tile by tile.
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+        if (kt < ntiles) {
+          u32x4 pb[2][2];
+#pragma unroll
+          for (int blk = 0; blk < 2; ++blk) {
+            float p[16];
 #pragma unroll
             for (int v = 0; v < 16; ++v)
-              if (kt * KT + blk * 32 + acc_row(v, hb) >= len) sc[blk][v] = -__builtin_inf();
-        }
-        const float m_tile = row_max(sc) * a.scale_log2;  // tile 0 holds a key: finite
-        if (kt == 0) {
-          m_run = m_tile;
-        } else if (__builtin_amdgcn_ballot_w64(m_tile > m_run + RESCALE_LOG2) != 0) {
-          const float m_new = __builtin_elementwise_maximum(m_run, m_tile);
-          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-          m_run = m_new;
-          l_run *= alpha;
-#pragma unroll
-          for (int db = 0; db < ND; ++db)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) oacc[db][v] *= alpha;
-        }
-        u32x4 pb[2][2];
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-          float p[16];
-#pragma unroll
-          for (int v = 0; v < 16; ++v)
-            p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v], a.scale_log2, -m_run));
-#pragma unroll
-          for (int cc = 0; cc < 2; ++cc) {
-            pb[blk][cc] = u32x4{pack2<DT>(p[cc * 8 + 0], p[cc * 8 + 1]),
-                                pack2<DT>(p[cc * 8 + 2], p[cc * 8 + 3]),
-                                pack2<DT>(p[cc * 8 + 4], p[cc * 8 + 5]),
-                                pack2<DT>(p[cc * 8 + 6], p[cc * 8 + 7])};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) l_run = sum2<DT>(pb[blk][cc][e], l_run);
-          }
-        }
-        const int gi = lane & 15, dh = (lane >> 4) & 1;
-#pragma unroll
-        for (int db = 0; db < ND; ++db) {
-          const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
-#pragma unroll
-          for (int blk = 0; blk < 2; ++blk)
+              p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][blk][v], a.scale_log2, -m_run));
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
-              const int k0 = blk * 32 + cc * 16 + hb * 4 + (gi >> 2);
-              const int cbk = dcol >> 3, half = (dcol & 4) * 2;
-              const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                  (lds_s16x4*)(sV[kt] + G::off(k0, cbk) + half));
-              const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                  (lds_s16x4*)(sV[kt] + G::off(k0 + 8, cbk) + half));
-              const u32x2 lw = __builtin_bit_cast(u32x2, lo);
-              const u32x2 hw = __builtin_bit_cast(u32x2, hi);
-              oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]}, pb[blk][cc], oacc[db]);
+              pb[blk][cc] = u32x4{pack2<DT>(p[cc * 8 + 0], p[cc * 8 + 1]),
+                                  pack2<DT>(p[cc * 8 + 2], p[cc * 8 + 3]),
+                                  pack2<DT>(p[cc * 8 + 4], p[cc * 8 + 5]),
+                                  pack2<DT>(p[cc * 8 + 6], p[cc * 8 + 7])};
+#pragma unroll
+              for (int e = 0; e < 4; ++e) l_run = sum2<DT>(pb[blk][cc][e], l_run);
             }
+          }
+          const int gi = lane & 15, dh = (lane >> 4) & 1;
+#pragma unroll
+          for (int db = 0; db < ND; ++db) {
+            const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+              for (int cc = 0; cc < 2; ++cc) {
+                const int k0 = blk * 32 + cc * 16 + hb * 4 + (gi >> 2);
+                const int cbk = dcol >> 3, half = (dcol & 4) * 2;
+                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(sV[kt] + G::off(k0, cbk) + half));
+                const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(sV[kt] + G::off(k0 + 8, cbk) + half));
+                const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+                const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+                oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]}, pb[blk][cc], oacc[db]);
+              }
+          }
         }
       }
       const float l_tot = l_run + __shfl_xor(l_run, 32);
