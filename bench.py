@@ -135,15 +135,27 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
     lens = (cu_v[1:] - cu_v[:-1]).long()
     flops3 = 4.0 * w.d * w.hq * float(lens[rows[0].long().clamp(min=0)].masked_fill(
         rows[0] < 0, 0).sum())
-    plan3 = H.SelAttnPlan(qv.shape, kv.shape, rows, cu_sb_v, cu_v, cu_q_v)
-    out3 = torch.empty_like(qv)
-    lse3 = torch.empty(w.hq, nv, dtype=torch.float32, device=dev)
-    ms3 = event_time_ms(lambda: plan3.fwd(qv, kv, vv, w.scale, out3, lse3), 5)
-    bplan3 = H.SelAttnPlan(qv.shape, kv.shape, rows, cu_sb_v, cu_v, cu_q_v, backward=True)
+    # The key-centric plan: grouped tiles whose masked union pass would cost
+    # more than per-block gathered tiles go to the gathered pass (most of
+    # them on these rows); forward, backward and the plan (built once per
+    # selection, shared by both) timed apart.  The grouped-tile plan alone
+    # is timed beside it.
     do3 = torch.randn(qv.shape, generator=torch.Generator(device=dev).manual_seed(7),
                       device=dev).to(qv.dtype)
-    ms3b = event_time_ms(lambda: bplan3.bwd(do3, qv, kv, vv, out3, lse3, w.scale), 3)
-    del bplan3
+    out3 = torch.empty_like(qv)
+    lse3 = torch.empty(w.hq, nv, dtype=torch.float32, device=dev)
+    times3 = {}
+    for kc in (True, False):
+        plan3 = H.SelAttnPlan(qv.shape, kv.shape, rows, cu_sb_v, cu_v, cu_q_v, backward=True,
+                              key_centric=kc)
+        ms_f = event_time_ms(lambda: plan3.fwd(qv, kv, vv, w.scale, out3, lse3), 5)
+        ms_b = event_time_ms(lambda: plan3.bwd(do3, qv, kv, vv, out3, lse3, w.scale), 3)
+        del plan3
+        ms_p = event_time_ms(lambda: H.SelAttnPlan(qv.shape, kv.shape, rows, cu_sb_v, cu_v,
+                                                   cu_q_v, backward=True, key_centric=kc), 2)
+        times3[kc] = (ms_f, ms_b, ms_p)
+    ms3, ms3b, ms3p = times3[True]
+    del do3, out3, lse3
 
     ops.set_validation(False)
     ck = H.block_mean_pool(k.view(w.n, -1), cu_blk).view(-1, w.hkv, w.d)
@@ -185,10 +197,16 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
     return {
         "attn_fwd_3d_aware_rows": {
             "ms": round(ms3, 4), "tflops": round(flops3 / (ms3 * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(flops3 / (ms3 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "plan": "key-centric", "plan_ms": round(ms3p, 4),
+            "grouped_tiles_ms": round(times3[False][0], 4),
+            "grouped_tiles_plan_ms": round(times3[False][2], 4),
             "workload": f"{nv} voxel tokens, {cu_v.numel() - 1} blocks, per-token nearest 16 "
                         f"block centroids, H={w.hq}"},
         "attn_bwd_3d_aware_rows": {
-            "ms": round(ms3b, 4), "tflops": round(2.5 * flops3 / (ms3b * 1e-3) / 1e12, 2)},
+            "ms": round(ms3b, 4), "tflops": round(2.5 * flops3 / (ms3b * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(2.5 * flops3 / (ms3b * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "plan": "key-centric", "grouped_tiles_ms": round(times3[False][1], 4)},
         "learned_selection": {"compressed_attn_ms": round(ms_ca, 4),
                               "get_block_score_ms": round(ms_bs, 4), "topk": 16},
         "attn_fwd_learned_rows_key_centric": {

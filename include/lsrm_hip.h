@@ -278,8 +278,10 @@ int lsrm_sel_attn_fwd_run(const void* q, const void* k, const void* v,
  * part is carved after the others, so lsrm_sel_attn_fwd_run and
  * lsrm_sel_attn_bwd_run accept such a workspace (the former then runs the
  * flagged tiles in the grouped-tile pass); lsrm_sel_attn_fwd_run2 with the
- * plan's flags runs the key-centric pass.  head_dim sizes the partials
- * (ignored without LSRM_PLAN_KEY_CENTRIC).
+ * plan's flags runs the key-centric pass.  head_dim sizes the partials and
+ * sets which blocks the forward keeps whole in LDS (up to 512 keys at
+ * head_dim <= 64, 256 above), so the runs pass the plan's head_dim like its
+ * other inputs (ignored without LSRM_PLAN_KEY_CENTRIC).
  * Replaces: ..._impl_kvcentric.py:931-1010 for per-token rows (the
  * reference has no key-centric forward; the queries of a block are the
  * reverse map of 575-684, which its backward builds).

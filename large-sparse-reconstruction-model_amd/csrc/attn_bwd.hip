@@ -943,12 +943,15 @@ sel_attn_dkdv_kernel(AttnArgs a) {
   leave_queue_xcd(a.plan.counter + 8, a.plan.counter + 3);
 }
 
-// Key-centric dQ merge: one thread per (kv head, query, query head, 4
+// Key-centric dQ merge: one thread per (kv head, query, query head, 8
 // channels) of the marked queries; the slot shares of dQ written by the
-// gathered tiles are added in slot order in fp32 and rounded once.
+// gathered tiles are added in slot order in fp32 and rounded once.  Slots
+// are taken 16 at a time with their ids and shares loaded together (a slot
+// without a block is loaded and ignored: the buffer covers every slot).
 template <int DT, int D>
 __global__ __launch_bounds__(256) void kc_dq_merge_kernel(AttnArgs a) {
-  constexpr int CPT = 4;
+  constexpr int CPT = 8;  // output channels per thread: one 16-byte load per slot
+  constexpr int U = 16;   // slots whose shares are loaded together
   const int64_t per_q = (int64_t)a.g * (D / CPT);
   const int64_t n_items = (int64_t)a.hkv * a.nq * per_q;
   for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
@@ -963,34 +966,36 @@ __global__ __launch_bounds__(256) void kc_dq_merge_kernel(AttnArgs a) {
     bool st;
     query_batch(a.cu_q, a.batch, a.cu_sb, q, &b, &bs, &nbb, &st);
     const int32_t* row = a.topk + hq_idx * a.topk_n;
-    float acc[CPT] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) acc[c] = 0.0f;
     bool any = false;
-    constexpr int U = 8;  // slots whose shares are loaded together
     for (int j0 = 0; j0 < a.topk_n; j0 += U) {
-      u32x2 pv[U];
-      bool ok[U];
+      int v[U];
+      u32x4 pv[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int j = j0 + u;
-        const int v = j < a.topk_n ? row[j] : -1;
-        ok[u] = v >= 0 && v < nbb && (int64_t)bs + v < a.nb;
-        const int64_t pidx = (hq_idx * a.topk_n + (ok[u] ? j : 0)) * a.g + gi;
-        pv[u] = ok[u] ? *reinterpret_cast<const u32x2*>(a.kc.part_o + pidx * D + d0)
-                      : u32x2{0u, 0u};
+        const bool in = j < a.topk_n;
+        v[u] = in ? row[j] : -1;
+        const int64_t pidx = (hq_idx * a.topk_n + (in ? j : 0)) * a.g + gi;
+        pv[u] = *reinterpret_cast<const u32x4*>(a.kc.part_o + pidx * D + d0);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        if (!ok[u]) continue;
+        if (!(v[u] >= 0 && v[u] < nbb && (int64_t)bs + v[u] < a.nb)) continue;
         any = true;
-        acc[0] += to_f32<DT>((uint16_t)(pv[u][0] & 0xffffu));
-        acc[1] += to_f32<DT>((uint16_t)(pv[u][0] >> 16));
-        acc[2] += to_f32<DT>((uint16_t)(pv[u][1] & 0xffffu));
-        acc[3] += to_f32<DT>((uint16_t)(pv[u][1] >> 16));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[2 * e] += to_f32<DT>((uint16_t)(pv[u][e] & 0xffffu));
+          acc[2 * e + 1] += to_f32<DT>((uint16_t)(pv[u][e] >> 16));
+        }
       }
     }
     const int hh = h * a.g + gi;
-    *reinterpret_cast<u32x2*>(a.out + (q * a.hq + hh) * D + d0) =
-        u32x2{pack2<DT>(acc[0], acc[1]), pack2<DT>(acc[2], acc[3])};
+    *reinterpret_cast<u32x4*>(a.out + (q * a.hq + hh) * D + d0) =
+        u32x4{pack2<DT>(acc[0], acc[1]), pack2<DT>(acc[2], acc[3]), pack2<DT>(acc[4], acc[5]),
+              pack2<DT>(acc[6], acc[7])};
     if (!any && d0 == 0) {
       // No slot names a block: no gathered row wrote this row's Delta.
       const uint16_t* orow = a.o + (q * a.hq + hh) * D;

@@ -93,7 +93,7 @@ sel_attn_fwd_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
   const int32_t* head_off =
-      GATHER ? a.kc.item_off : (UNION ? a.plan.ghead_off : a.plan.head_off);
+      GATHER ? a.kc.fitem_off : (UNION ? a.plan.ghead_off : a.plan.head_off);
   const int2* tiles = UNION ? a.plan.gtiles : a.plan.tiles;
   int32_t* queue = a.plan.counter + (GATHER ? KC_QUEUE_SLOT : (UNION ? 4 : 0));
   const int total = head_off[a.hkv];
@@ -121,19 +121,11 @@ sel_attn_fwd_kernel(AttnArgs a) {
     const int h = head_of(head_off, a.hkv, w);
     int q0, qn, gblk = 0, ge0 = 0;
     if constexpr (GATHER) {
-      const int4 it = a.kc.items[(int64_t)h * a.kc.item_cap + (w - head_off[h])];
+      const int4 it = a.kc.fitems[(int64_t)h * a.kc.fitem_cap + (w - head_off[h])];
       gblk = it.x;
       ge0 = it.y;
       q0 = 0;
       qn = it.z;
-      // blocks of 1..KC_RES_KEYS keys belong to kc_resident_fwd_kernel
-      int64_t bs0 = a.cu_blk[gblk], bs1 = a.cu_blk[gblk + 1];
-      bs0 = bs0 < 0 ? 0 : (bs0 > a.nk ? a.nk : bs0);
-      bs1 = bs1 < bs0 ? bs0 : (bs1 > a.nk ? a.nk : bs1);
-      if (bs1 > bs0 && bs1 - bs0 <= KC_RES_KEYS) {
-        __syncthreads();  // every wave has read s_slot before it is reused
-        continue;
-      }
     } else {
       // Key-centric plans: flagged grouped tiles belong to the gathered pass.
       if constexpr (UNION) {
@@ -629,20 +621,52 @@ sel_attn_fwd_kernel(AttnArgs a) {
 }
 
 // Plan step of key-centric plans: gflag[h, t] = 1 for the grouped tiles
-// whose union cannot run in one masked pass (build_union's ok is false:
-// more than MAXSEL union blocks, a row listing a block twice, or a union
-// longer than the runs' own streams together).  One workgroup per tile.
+// that go to the gathered pass: those whose union cannot run in one masked
+// pass (build_union's ok is false: more than MAXSEL union blocks, a row
+// listing a block twice, or a union longer than the runs' own streams
+// together), and those whose masked pass computes more key-rows than their
+// rows' own keys (every key of the union for every row of its busy waves,
+// against each row's own keys in the gathered tiles).  Measured on 3D-aware
+// rows, the gathered tiles with their partial results and merge run at
+// about the masked pass's rate per computed key-row, so any such waste
+// favours them.  One workgroup per tile.
 __global__ __launch_bounds__(256) void kc_flag_kernel(AttnArgs a, uint8_t* gflag) {
   __shared__ SelLds sel;
   __shared__ UnionLds ul;
+  __shared__ unsigned long long own;
   const int total = a.plan.ghead_off[a.hkv];
   for (int w = blockIdx.x; w < total; w += gridDim.x) {
     const int h = head_of(a.plan.ghead_off, a.hkv, w);
     const int t = w - a.plan.ghead_off[h];
     const int2 tile = a.plan.gtiles[(int64_t)h * a.nq + t];
+    if (threadIdx.x == 0) own = 0ull;
     build_union(a, h, tile.x, tile.y, sel, ul);
-    if (threadIdx.x == 0) gflag[(int64_t)h * a.nq + t] = ul.ok ? 0 : 1;
-    __syncthreads();  // ul.ok read before the next tile rebuilds the LDS
+    if (ul.ok) {
+      // the rows' own keys: every slot naming a block, repeats included
+      int b, bs, nbb;
+      bool st;
+      query_batch(a.cu_q, a.batch, a.cu_sb, tile.x, &b, &bs, &nbb, &st);
+      const int32_t* rows = a.topk + ((int64_t)h * a.nq + tile.x) * a.topk_n;
+      unsigned long long mine = 0ull;
+      for (int e = threadIdx.x; e < tile.y * a.topk_n; e += blockDim.x) {
+        int t0, len;
+        block_span(a, bs, nbb, rows[e], t0, len);
+        mine += (unsigned long long)len;
+      }
+      atomicAdd(&own, mine);
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+      bool flag = !ul.ok;
+      if (!flag) {
+        const int waves = (tile.y * a.g + 31) / 32;
+        const unsigned long long masked =
+            (unsigned long long)sel.cum[sel.n] * (unsigned long long)(waves * 32);
+        flag = masked > own * (unsigned long long)a.g;
+      }
+      gflag[(int64_t)h * a.nq + t] = flag ? 1 : 0;
+    }
+    __syncthreads();  // ul / own read before the next tile rebuilds the LDS
   }
 }
 
@@ -652,29 +676,37 @@ int launch_kc_flags(const AttnArgs& a, uint8_t* gflag, hipStream_t st) {
   return LSRM_OK;
 }
 
-// Key-centric forward of blocks with 1..KC_RES_KEYS keys: the block's K and
-// V (at most four 64-key tiles) are copied into LDS once per item and stay
-// resident while the item's query chunks (up to KC_RES_CHUNKS x 128 rows of
-// gathered listings) run over them: S^T = K Q^T and O^T += V^T P^T as in the
-// streaming kernel.  With at most four key tiles, a chunk first computes all
-// of its scores and the exact row maximum (the softmax reference), then the
+// Key-centric forward of blocks held whole in LDS: the block's K and V (at
+// most NT 64-key tiles) are copied into LDS once per item and stay resident
+// while the item's query chunks (up to KC_RES_CHUNKS x 128 rows of gathered
+// listings) run over them: S^T = K Q^T and O^T += V^T P^T as in the
+// streaming kernel.  BIG = 0: four waves, blocks of 1..KC_RES_KEYS keys;
+// BIG = 1 (head dim <= 64): eight waves in two groups of four, each group
+// running its own chunks, blocks of KC_RES_KEYS+1..KC_RES2_KEYS keys.  The
+// tiles are taken four at a time: a group of four first computes all of its
+// scores and their exact row maximum (the softmax reference, raised from
+// the previous group's with O and the row sum rescaled), then the
 // exponentials, row sums and P.V tile by tile; the row's partial result
 // (O / l in the input type and its log2 LSE) is written at [head, query,
 // slot] for kc_merge_kernel.
-template <int DT, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+template <int DT, int D, int BIG>
+__global__ __launch_bounds__(BIG ? 512 : 256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 kc_resident_fwd_kernel(AttnArgs a) {
   using G = KvTile<D>;
   constexpr int NS = D / 16;
   constexpr int ND = D / 32;
-  constexpr int NT = KC_RES_KEYS / KT;
+  constexpr int NT = (BIG ? KC_RES2_KEYS : KC_RES_KEYS) / KT;
+  constexpr int NWG = BIG ? 2 : 1;  // groups of four waves
   __shared__ __align__(1024) char sK[NT][G::BYTES];
   __shared__ __align__(1024) char sV[NT][G::BYTES];
   __shared__ int s_slot;
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
+  const int wg = wv >> 2, wl = wv & 3;  // wave group, wave inside the group
   const int hb = lane >> 5, l32 = lane & 31;
-  const int32_t* head_off = a.kc.ritem_off;
-  int32_t* queue = a.plan.counter + KC_RQUEUE_SLOT;
+  const int32_t* head_off = BIG ? a.kc.r2item_off : a.kc.ritem_off;
+  const int4* items = BIG ? a.kc.r2items : a.kc.ritems;
+  const int64_t item_cap = BIG ? a.kc.r2item_cap : a.kc.ritem_cap;
+  int32_t* queue = a.plan.counter + (BIG ? KC_R2QUEUE_SLOT : KC_RQUEUE_SLOT);
   const int total = head_off[a.hkv];
   // An empty queue: leave it untouched (no fetch, so nothing to reset).
   if (total == 0) return;
@@ -686,28 +718,28 @@ kc_resident_fwd_kernel(AttnArgs a) {
     const int w = uniform(fetch_work(queue, &s_slot));
     if (w >= total) break;
     const int h = head_of(head_off, a.hkv, w);
-    const int4 it = a.kc.ritems[(int64_t)h * a.kc.ritem_cap + (w - head_off[h])];
+    const int4 it = items[(int64_t)h * item_cap + (w - head_off[h])];
     const int c = it.x, e0 = it.y, n = it.z;
     int64_t s0 = a.cu_blk[c], s1 = a.cu_blk[c + 1];
     s0 = s0 < 0 ? 0 : (s0 > a.nk ? a.nk : s0);
     s1 = s1 < s0 ? s0 : (s1 > a.nk ? a.nk : s1);
-    const int len = uniform((int)(s1 - s0));  // 1..KC_RES_KEYS (plan)
+    const int len = uniform((int)(s1 - s0));  // 1..NT * KT (plan)
     const int ntiles = (len + KT - 1) / KT;
     const char* kbase = reinterpret_cast<const char*>(a.k + (int64_t)h * D);
     const char* vbase = reinterpret_cast<const char*>(a.v + (int64_t)h * D);
-    // The block into LDS: tile t, load j of this wave covers rows
-    // (wv * LPW + j) * KPL + lane / CH; keys past the block load its first
-    // token (in bounds; masked below).
+    // The block into LDS: wave group t % NWG copies tile t; load j of its
+    // wave wl covers rows (wl * LPW + j) * KPL + lane / CH; keys past the
+    // block load its first token (in bounds; masked below).
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      if (t < ntiles) {
+      if (t < ntiles && t % NWG == wg) {
 #pragma unroll
         for (int j = 0; j < G::LPW; ++j) {
-          const int row = (wv * G::LPW + j) * G::KPL + lane / G::CH;
+          const int row = (wl * G::LPW + j) * G::KPL + lane / G::CH;
           const int key = t * KT + row;
           const uint32_t tok = (uint32_t)(key < len ? s0 + key : s0);
           const uint32_t voff = tok * row_bytes + (((lane % G::CH) ^ G::swz(row)) << 4);
-          const uint32_t dst = (uint32_t)(wv * G::LPW + j) * 1024;
+          const uint32_t dst = (uint32_t)(wl * G::LPW + j) * 1024;
           copy16_to_lds(kbase, voff, lds_addr(sK[t]) + dst);
           copy16_to_lds(vbase, voff, lds_addr(sV[t]) + dst);
         }
@@ -716,10 +748,12 @@ kc_resident_fwd_kernel(AttnArgs a) {
     wait_copies();
     __syncthreads();
 
-    // The gathered rows of chunk cb: listing -> (query, slot) -> Q row.  The
-    // listings are loaded two chunks ahead and the Q rows one chunk ahead,
-    // so a chunk's dependent gathers are in flight during the chunk before.
-    const int r = wv * 32 + l32;
+    // The gathered rows of chunk cb: listing -> (query, slot) -> Q row.  A
+    // wave group runs chunks wg * tq, wg * tq + step, ...  The listings are
+    // loaded two chunks ahead and the Q rows one chunk ahead, so a chunk's
+    // dependent gathers are in flight during the chunk before.
+    const int r = wl * 32 + l32;
+    const int step = NWG * tq;
     auto chunk_ok = [&](int cbx) { return r < (n - cbx < tq ? n - cbx : tq) * a.g; };
     auto load_listing = [&](int cbx) -> int32_t {
       return cbx < n ? a.kc.grev.rev[(int64_t)h * cap + e0 + cbx + (chunk_ok(cbx) ? r / a.g : 0)]
@@ -734,11 +768,12 @@ kc_resident_fwd_kernel(AttnArgs a) {
                      ? *reinterpret_cast<const u32x4*>(a.q + (qx * a.hq + hx) * D + s * 16 + hb * 8)
                      : u32x4{0u, 0u, 0u, 0u};
     };
-    int32_t lv_cur = load_listing(0);
+    const int cb0 = wg * tq;
+    int32_t lv_cur = load_listing(cb0);
     u32x4 q_next[NS];
-    load_q(0, lv_cur, q_next);
-    int32_t lv_next = load_listing(tq);
-    for (int cb = 0; cb < n; cb += tq) {
+    load_q(cb0, lv_cur, q_next);
+    int32_t lv_next = load_listing(cb0 + step);
+    for (int cb = cb0; cb < n; cb += step) {
       const int rows = (n - cb < tq ? n - cb : tq) * a.g;
       const bool row_ok = r < rows;
       u32x4 qb[NS];
@@ -748,98 +783,115 @@ kc_resident_fwd_kernel(AttnArgs a) {
       const int64_t slot = lv_cur - qi * a.topk_n;
       // next chunk: its Q rows from the listing loaded one chunk ago; the
       // listing after it
-      load_q(cb + tq, lv_next, q_next);
+      load_q(cb + step, lv_next, q_next);
       lv_cur = lv_next;
-      lv_next = load_listing(cb + 2 * tq);
-      if (wv * 32 >= rows) continue;  // wave-uniform: no row of this chunk
+      lv_next = load_listing(cb + 2 * step);
+      if (wl * 32 >= rows) continue;  // wave-uniform: no row of this chunk
       f32x16 oacc[ND];
 #pragma unroll
       for (int i = 0; i < ND; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
-      // Phase 1: the scores of every tile of the block (at most NT), keys
-      // past the block masked, and the exact row maximum.
-      f32x16 sc[NT][2];
-      float mx = -__builtin_inf();
+      float m_run = -__builtin_inf();
+      float l_run = 0.0f;
 #pragma unroll
-      for (int kt = 0; kt < NT; ++kt) {
-        if (kt < ntiles) {
+      for (int kb = 0; kb < NT; kb += 4) {
+        if (kb >= ntiles) break;  // uniform
+        // Phase 1: the scores of the group's tiles, keys past the block
+        // masked, and the exact row maximum.
+        f32x16 sc[4][2];
+        float mx = -__builtin_inf();
 #pragma unroll
-          for (int blk = 0; blk < 2; ++blk) {
+        for (int t4 = 0; t4 < 4; ++t4) {
+          const int kt = kb + t4;
+          if (kt < ntiles) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) sc[kt][blk][v] = 0.0f;
+            for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
-            for (int s = 0; s < NS; ++s) {
-              const u32x4 ka = *reinterpret_cast<const u32x4*>(
-                  sK[kt] + G::off(blk * 32 + l32, 2 * s + hb));
-              sc[kt][blk] = mfma32<DT>(ka, qb[s], sc[kt][blk]);
+              for (int v = 0; v < 16; ++v) sc[t4][blk][v] = 0.0f;
+#pragma unroll
+              for (int s = 0; s < NS; ++s) {
+                const u32x4 ka = *reinterpret_cast<const u32x4*>(
+                    sK[kt] + G::off(blk * 32 + l32, 2 * s + hb));
+                sc[t4][blk] = mfma32<DT>(ka, qb[s], sc[t4][blk]);
+              }
             }
-          }
-          if (kt * KT + KT > len) {
+            if (kt * KT + KT > len) {
+#pragma unroll
+              for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                  if (kt * KT + blk * 32 + acc_row(v, hb) >= len) sc[t4][blk][v] = -__builtin_inf();
+            }
 #pragma unroll
             for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+              for (int v = 0; v < 16; v += 4)
+                mx = __builtin_elementwise_maximum(
+                    mx, max3f(sc[t4][blk][v], sc[t4][blk][v + 1],
+                              __builtin_elementwise_maximum(sc[t4][blk][v + 2], sc[t4][blk][v + 3])));
+          }
+        }
+        {
+          const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
+                                                           __builtin_bit_cast(unsigned, mx),
+                                                           false, false);
+          mx = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)sw[0]),
+                                             __builtin_bit_cast(float, (unsigned)sw[1]));
+        }
+        // The group's first tile holds a key: mx is finite.
+        const float m_new = __builtin_elementwise_maximum(m_run, mx * a.scale_log2);
+        if (kb > 0) {
+          const float al = __builtin_amdgcn_exp2f(m_run - m_new);
+          l_run *= al;
+#pragma unroll
+          for (int i = 0; i < ND; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) oacc[i][v] *= al;
+        }
+        m_run = m_new;
+        // Phase 2: P = exp2(s * scale * log2(e) - m) rounded to the input
+        // type, row sums, O^T += V^T P^T, tile by tile.
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          const int kt = kb + t4;
+          if (kt < ntiles) {
+            u32x4 pb[2][2];
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk) {
+              float p[16];
 #pragma unroll
               for (int v = 0; v < 16; ++v)
-                if (kt * KT + blk * 32 + acc_row(v, hb) >= len) sc[kt][blk][v] = -__builtin_inf();
-          }
-#pragma unroll
-          for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-            for (int v = 0; v < 16; v += 4)
-              mx = __builtin_elementwise_maximum(
-                  mx, max3f(sc[kt][blk][v], sc[kt][blk][v + 1],
-                            __builtin_elementwise_maximum(sc[kt][blk][v + 2], sc[kt][blk][v + 3])));
-        }
-      }
-      {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
-                                                         __builtin_bit_cast(unsigned, mx),
-                                                         false, false);
-        mx = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)sw[0]),
-                                           __builtin_bit_cast(float, (unsigned)sw[1]));
-      }
-      const float m_run = mx * a.scale_log2;  // tile 0 holds a key: finite
-      float l_run = 0.0f;
-      // Phase 2: P = exp2(s * scale * log2(e) - m) rounded to the input type,
-      // row sums, O^T += V^T P^T, tile by tile.
-#pragma unroll
-      for (int kt = 0; kt < NT; ++kt) {
-        if (kt < ntiles) {
-          u32x4 pb[2][2];
-#pragma unroll
-          for (int blk = 0; blk < 2; ++blk) {
-            float p[16];
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-              p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][blk][v], a.scale_log2, -m_run));
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-              pb[blk][cc] = u32x4{pack2<DT>(p[cc * 8 + 0], p[cc * 8 + 1]),
-                                  pack2<DT>(p[cc * 8 + 2], p[cc * 8 + 3]),
-                                  pack2<DT>(p[cc * 8 + 4], p[cc * 8 + 5]),
-                                  pack2<DT>(p[cc * 8 + 6], p[cc * 8 + 7])};
-#pragma unroll
-              for (int e = 0; e < 4; ++e) l_run = sum2<DT>(pb[blk][cc][e], l_run);
-            }
-          }
-          const int gi = lane & 15, dh = (lane >> 4) & 1;
-#pragma unroll
-          for (int db = 0; db < ND; ++db) {
-            const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
-#pragma unroll
-            for (int blk = 0; blk < 2; ++blk)
+                p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t4][blk][v], a.scale_log2, -m_run));
 #pragma unroll
               for (int cc = 0; cc < 2; ++cc) {
-                const int k0 = blk * 32 + cc * 16 + hb * 4 + (gi >> 2);
-                const int cbk = dcol >> 3, half = (dcol & 4) * 2;
-                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_s16x4*)(sV[kt] + G::off(k0, cbk) + half));
-                const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_s16x4*)(sV[kt] + G::off(k0 + 8, cbk) + half));
-                const u32x2 lw = __builtin_bit_cast(u32x2, lo);
-                const u32x2 hw = __builtin_bit_cast(u32x2, hi);
-                oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]}, pb[blk][cc], oacc[db]);
+                pb[blk][cc] = u32x4{pack2<DT>(p[cc * 8 + 0], p[cc * 8 + 1]),
+                                    pack2<DT>(p[cc * 8 + 2], p[cc * 8 + 3]),
+                                    pack2<DT>(p[cc * 8 + 4], p[cc * 8 + 5]),
+                                    pack2<DT>(p[cc * 8 + 6], p[cc * 8 + 7])};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) l_run = sum2<DT>(pb[blk][cc][e], l_run);
               }
+            }
+            const int gi = lane & 15, dh = (lane >> 4) & 1;
+#pragma unroll
+            for (int db = 0; db < ND; ++db) {
+              const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+#pragma unroll
+              for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+                for (int cc = 0; cc < 2; ++cc) {
+                  const int k0 = blk * 32 + cc * 16 + hb * 4 + (gi >> 2);
+                  const int cbk = dcol >> 3, half = (dcol & 4) * 2;
+                  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                      (lds_s16x4*)(sV[kt] + G::off(k0, cbk) + half));
+                  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                      (lds_s16x4*)(sV[kt] + G::off(k0 + 8, cbk) + half));
+                  const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+                  const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+                  oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]}, pb[blk][cc], oacc[db]);
+                }
+            }
           }
         }
       }
@@ -867,16 +919,20 @@ kc_resident_fwd_kernel(AttnArgs a) {
   leave_queue(queue, queue + 2);
 }
 
-// Key-centric merge: one thread per (kv head, query, query head, 4 output
+// Key-centric merge: one thread per (kv head, query, query head, 8 output
 // channels) of the marked queries.  The partials of the row's valid slots
 // (the gathered tiles wrote one per slot naming a block) are combined in
 // slot order: M = max LSE_j, W = sum 2^(LSE_j - M), O = sum 2^(LSE_j - M)
-// O_j / W, LSE = M + log2 W.  A row without a partial that attended a key
-// gives O = 0 and LSE = -inf.
+// O_j / W, LSE = M + log2 W.  Slots are taken 16 at a time with their ids,
+// LSEs and partials loaded together (a slot without a block is loaded and
+// ignored: the buffers cover every slot); M is the maximum over the chunks
+// seen so far and earlier terms are rescaled when a chunk raises it, which
+// for rows of at most 16 slots is the single maximum above.  A row without
+// a partial that attended a key gives O = 0 and LSE = -inf.
 template <int DT, int D>
 __global__ __launch_bounds__(256) void kc_merge_kernel(AttnArgs a) {
-  constexpr int CPT = 4;  // output channels per thread
-  constexpr int U = 8;    // slots whose partials are loaded together
+  constexpr int CPT = 8;  // output channels per thread: one 16-byte load per slot
+  constexpr int U = 16;   // slots loaded together
   const int64_t per_q = (int64_t)a.g * (D / CPT);
   const int64_t n_items = (int64_t)a.hkv * a.nq * per_q;
   for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
@@ -893,48 +949,56 @@ __global__ __launch_bounds__(256) void kc_merge_kernel(AttnArgs a) {
     const int32_t* row = a.topk + hq_idx * a.topk_n;
     const int64_t pbase = hq_idx * a.topk_n;  // partial (q, slot 0)
     float mx = -__builtin_inf();
-    float acc[CPT] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) acc[c] = 0.0f;
     float wsum = 0.0f;
-    // Pass 1: the maximum LSE; pass 2: weights and weighted outputs, slot by
-    // slot in row order.  Slots are taken U at a time so that their loads
-    // are in flight together (a slot without a block loads nothing).
-    for (int pass = 0; pass < 2; ++pass) {
-      if (pass == 1 && !(mx > -__builtin_inf())) break;
-      for (int j0 = 0; j0 < a.topk_n; j0 += U) {
-        float l[U];
-        u32x2 ov[U];
-        bool ok[U];
+    for (int j0 = 0; j0 < a.topk_n; j0 += U) {
+      int v[U];
+      float l[U];
+      u32x4 ov[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int j = j0 + u;
-          const int v = j < a.topk_n ? row[j] : -1;
-          ok[u] = v >= 0 && v < nbb && (int64_t)bs + v < a.nb;
-          const int64_t pidx = (pbase + (ok[u] ? j : 0)) * a.g + gi;
-          l[u] = ok[u] ? a.kc.part_lse[pidx] : -__builtin_inf();
-          if (pass == 1)
-            ov[u] = ok[u] ? *reinterpret_cast<const u32x2*>(a.kc.part_o + pidx * D + d0)
-                          : u32x2{0u, 0u};
-        }
+      for (int u = 0; u < U; ++u) {
+        const int j = j0 + u;
+        const bool in = j < a.topk_n;
+        v[u] = in ? row[j] : -1;
+        const int64_t pidx = (pbase + (in ? j : 0)) * a.g + gi;
+        l[u] = a.kc.part_lse[pidx];
+        ov[u] = *reinterpret_cast<const u32x4*>(a.kc.part_o + pidx * D + d0);
+      }
+      bool ok[U];
+      float cm = -__builtin_inf();
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          if (!ok[u]) continue;
-          if (pass == 0) {
-            mx = __builtin_elementwise_maximum(mx, l[u]);
-          } else {
-            const float wj = __builtin_amdgcn_exp2f(l[u] - mx);
-            wsum += wj;
-            acc[0] += wj * to_f32<DT>((uint16_t)(ov[u][0] & 0xffffu));
-            acc[1] += wj * to_f32<DT>((uint16_t)(ov[u][0] >> 16));
-            acc[2] += wj * to_f32<DT>((uint16_t)(ov[u][1] & 0xffffu));
-            acc[3] += wj * to_f32<DT>((uint16_t)(ov[u][1] >> 16));
-          }
+      for (int u = 0; u < U; ++u) {
+        ok[u] = v[u] >= 0 && v[u] < nbb && (int64_t)bs + v[u] < a.nb;
+        if (ok[u]) cm = __builtin_elementwise_maximum(cm, l[u]);
+      }
+      const float m_new = __builtin_elementwise_maximum(mx, cm);
+      if (!(m_new > -__builtin_inf())) continue;  // no finite LSE yet
+      if (m_new != mx) {  // the first finite chunk (scale 0 on zeros) or a larger maximum
+        const float sc = __builtin_amdgcn_exp2f(mx - m_new);
+        wsum *= sc;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) acc[c] *= sc;
+        mx = m_new;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (!ok[u]) continue;
+        const float wj = __builtin_amdgcn_exp2f(l[u] - mx);
+        wsum += wj;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[2 * e] += wj * to_f32<DT>((uint16_t)(ov[u][e] & 0xffffu));
+          acc[2 * e + 1] += wj * to_f32<DT>((uint16_t)(ov[u][e] >> 16));
         }
       }
     }
     const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
     const int hh = h * a.g + gi;
-    *reinterpret_cast<u32x2*>(a.out + (q * a.hq + hh) * D + d0) =
-        u32x2{pack2<DT>(acc[0] * inv, acc[1] * inv), pack2<DT>(acc[2] * inv, acc[3] * inv)};
+    *reinterpret_cast<u32x4*>(a.out + (q * a.hq + hh) * D + d0) =
+        u32x4{pack2<DT>(acc[0] * inv, acc[1] * inv), pack2<DT>(acc[2] * inv, acc[3] * inv),
+              pack2<DT>(acc[4] * inv, acc[5] * inv), pack2<DT>(acc[6] * inv, acc[7] * inv)};
     if (d0 == 0)
       a.lse[(int64_t)hh * a.nq + q] = wsum > 0.0f ? mx + log2f(wsum) : -__builtin_inf();
   }
@@ -963,11 +1027,18 @@ int launch_fwd_t(const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, FWD_GATHER>), dim3(gg), dim3(256), 0, st,
                        a);
     LSRM_CHECK_LAUNCH();
-    const void* fr = reinterpret_cast<const void*>(&kc_resident_fwd_kernel<DT, D>);
+    const void* fr = reinterpret_cast<const void*>(&kc_resident_fwd_kernel<DT, D, 0>);
     const int gr = persistent_grid(fr, 256, 0);
     if (gr <= 0) return LSRM_ERR_LAUNCH;
-    hipLaunchKernelGGL((kc_resident_fwd_kernel<DT, D>), dim3(gr), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((kc_resident_fwd_kernel<DT, D, 0>), dim3(gr), dim3(256), 0, st, a);
     LSRM_CHECK_LAUNCH();
+    if constexpr (kc_res_max(D) > KC_RES_KEYS) {
+      const void* fr2 = reinterpret_cast<const void*>(&kc_resident_fwd_kernel<DT, D, 1>);
+      const int gr2 = persistent_grid(fr2, 512, 0);
+      if (gr2 <= 0) return LSRM_ERR_LAUNCH;
+      hipLaunchKernelGGL((kc_resident_fwd_kernel<DT, D, 1>), dim3(gr2), dim3(512), 0, st, a);
+      LSRM_CHECK_LAUNCH();
+    }
     const int gm = device_cu_count() * 16;
     if (gm <= 0) return LSRM_ERR_LAUNCH;
     hipLaunchKernelGGL((kc_merge_kernel<DT, D>), dim3(gm), dim3(256), 0, st, a);

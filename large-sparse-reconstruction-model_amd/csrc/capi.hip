@@ -133,7 +133,8 @@ int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
     rc = build_reverse_map(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, nb, false, nullptr,
                            ws, kc.grev, st, kc.qmark, true);
     if (rc) return rc;
-    rc = build_kc_items(kc.grev, cu_blk, nk, hkv, nb, tq, ws, kc, w.plan.counter, st);
+    rc = build_kc_items(kc.grev, cu_blk, nk, hkv, nb, tq, head_dim, ws, kc, w.plan.counter,
+                        st);
     if (rc) return rc;
     const size_t parts = (size_t)(hkv * (kc.grev.cap > 0 ? kc.grev.cap : 1) * g);
     kc.part_o = ws.take<uint16_t>(parts * (size_t)(head_dim > 0 ? head_dim : 1));

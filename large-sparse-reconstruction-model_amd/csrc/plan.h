@@ -84,22 +84,39 @@ struct KcPlan {
   float* part_lse;       // [hkv, n_q, topk, g]
   // Forward items of blocks with at most KC_RES_KEYS keys, which the
   // forward runs with the block resident in LDS: {c, e0, n, 0} with up to
-  // KC_RES_CHUNKS * tq listings (the streaming gathered forward skips these
-  // blocks; dQ takes every block from `items`).
+  // KC_RES_CHUNKS * tq listings (dQ takes every block from `items`).
   int4* ritems;
   int64_t ritem_cap;
   int32_t* ritem_count;  // [hkv]
   int32_t* ritem_off;    // [hkv + 1]
+  // The same for blocks of KC_RES_KEYS + 1 .. KC_RES2_KEYS keys (head dim
+  // <= 64; empty otherwise), run by the eight-wave resident forward.
+  int4* r2items;
+  int64_t r2item_cap;
+  int32_t* r2item_count;  // [hkv]
+  int32_t* r2item_off;    // [hkv + 1]
+  // The streaming gathered forward's items: `items` of the blocks the
+  // resident forwards do not take (no keys, or more than kc_res_max of the
+  // plan's head dim).
+  int4* fitems;
+  int64_t fitem_cap;
+  int32_t* fitem_count;  // [hkv]
+  int32_t* fitem_off;    // [hkv + 1]
 };
 // Work counters of the gathered-tile kernels inside TilePlan::counter.
 constexpr int KC_QUEUE_SLOT = 16, KC_EXIT_SLOT = 18;
 constexpr int KC_RQUEUE_SLOT = 20, KC_REXIT_SLOT = 22;
+constexpr int KC_R2QUEUE_SLOT = 24, KC_R2EXIT_SLOT = 26;
 constexpr int KC_RES_KEYS = 256;   // 4 key tiles of K and V resident in LDS
-constexpr int KC_RES_CHUNKS = 8;   // query chunks of tq listings per resident item
+constexpr int KC_RES2_KEYS = 512;  // 8 key tiles (head dim <= 64: 128 KB of LDS)
+constexpr int KC_RES_CHUNKS = 16;  // query chunks of tq listings per resident item
+// Largest block the resident forward takes at head dim d; larger blocks run
+// as streaming gathered tiles.
+__host__ __device__ constexpr int kc_res_max(int d) { return d <= 64 ? KC_RES2_KEYS : KC_RES_KEYS; }
 
 int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
-                   int64_t nb, int tq, Carver& ws, KcPlan& kc, int32_t* counter,
-                   hipStream_t st);
+                   int64_t nb, int tq, int64_t head_dim, Carver& ws, KcPlan& kc,
+                   int32_t* counter, hipStream_t st);
 int mark_flagged_queries(const TilePlan& plan, const uint8_t* gflag, int64_t hkv,
                          int64_t nq, uint8_t* qmark, hipStream_t st);
 

@@ -832,19 +832,23 @@ __device__ inline int64_t kc_block_len(const int32_t* cu_blk, int64_t nk, int64_
 }
 
 // Gathered tiles of block c: ceil(listings / tq) pieces of its grev segment.
-// With `res` set, only blocks of 1..KC_RES_KEYS keys count (the resident
-// forward's items); with cu_blk null, every block counts.
+// With cu_blk set, only blocks of lo + 1 .. hi keys count (the resident
+// forwards' items, lo >= 0), or with `outside` only the other blocks (the
+// streaming forward's); with cu_blk null, every block counts.
 struct KcItemsF {
   const int32_t* cu_rev;
   int64_t nb, cap;
   int tq;
   const int32_t* cu_blk;
   int64_t nk;
+  int lo, hi;
+  bool outside;
   __device__ int64_t limit(int, int64_t n) const { return n; }
   __device__ int operator()(int h, int64_t c) const {
     if (cu_blk) {
       const int64_t len = kc_block_len(cu_blk, nk, c);
-      if (len <= 0 || len > KC_RES_KEYS) return 0;
+      const bool in = len > lo && len <= hi;
+      if (in == outside) return 0;
     }
     const int32_t* p = cu_rev + (int64_t)h * (nb + 1);
     int64_t s = p[c], e = p[c + 1];
@@ -872,29 +876,38 @@ struct KcItemsW {
   }
 };
 
-__global__ void kc_offsets_kernel(const int32_t* count, const int32_t* rcount, int hkv,
-                                  int32_t* off, int32_t* roff, int32_t* counter) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) {
-    int acc = 0, racc = 0;
+// Per-head offsets of the item lists (all blocks, resident, eight-wave
+// resident, streaming forward) and their cleared work counters.
+struct KcCounts {
+  const int32_t* count[4];
+  int32_t* off[4];
+};
+__global__ void kc_offsets_kernel(KcCounts c, int hkv, int32_t* counter) {
+  if (threadIdx.x < 4 && blockIdx.x == 0) {
+    const int32_t* cnt = c.count[threadIdx.x];
+    int32_t* off = c.off[threadIdx.x];
+    int acc = 0;
     off[0] = 0;
-    roff[0] = 0;
     for (int h = 0; h < hkv; ++h) {
-      acc += count[h];
-      racc += rcount[h];
+      acc += cnt[h];
       off[h + 1] = acc;
-      roff[h + 1] = racc;
     }
+  }
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
     counter[KC_QUEUE_SLOT] = 0;
     counter[KC_EXIT_SLOT] = 0;
     counter[KC_RQUEUE_SLOT] = 0;
     counter[KC_REXIT_SLOT] = 0;
+    counter[KC_R2QUEUE_SLOT] = 0;
+    counter[KC_R2EXIT_SLOT] = 0;
   }
 }
 
 int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
-                   int64_t nb, int tq, Carver& ws, KcPlan& kc, int32_t* counter,
-                   hipStream_t st) {
+                   int64_t nb, int tq, int64_t head_dim, Carver& ws, KcPlan& kc,
+                   int32_t* counter, hipStream_t st) {
   const int rq = tq * KC_RES_CHUNKS;
+  const int res_max = kc_res_max((int)(head_dim > 0 ? head_dim : 1));
   kc.item_cap = grev.cap / (tq > 0 ? tq : 1) + nb + 1;
   kc.items = ws.take<int4>((size_t)(hkv * kc.item_cap));
   kc.item_count = ws.take<int32_t>((size_t)hkv);
@@ -903,23 +916,43 @@ int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_
   kc.ritems = ws.take<int4>((size_t)(hkv * kc.ritem_cap));
   kc.ritem_count = ws.take<int32_t>((size_t)hkv);
   kc.ritem_off = ws.take<int32_t>((size_t)(hkv + 1));
+  kc.r2item_cap = kc.ritem_cap;
+  kc.r2items = ws.take<int4>((size_t)(hkv * kc.r2item_cap));
+  kc.r2item_count = ws.take<int32_t>((size_t)hkv);
+  kc.r2item_off = ws.take<int32_t>((size_t)(hkv + 1));
+  kc.fitem_cap = kc.item_cap;
+  kc.fitems = ws.take<int4>((size_t)(hkv * kc.fitem_cap));
+  kc.fitem_count = ws.take<int32_t>((size_t)hkv);
+  kc.fitem_off = ws.take<int32_t>((size_t)(hkv + 1));
   int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, hkv));
   if (!ws.base || ws.dry) return LSRM_OK;
   if (!ws.ok()) return LSRM_ERR_WORKSPACE;
-  int rc = launch_zero_i32(kc.item_count, hkv, st);
+  for (int32_t* cnt : {kc.item_count, kc.ritem_count, kc.r2item_count, kc.fitem_count}) {
+    const int rc = launch_zero_i32(cnt, hkv, st);
+    if (rc) return rc;
+  }
+  int rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, tq, nullptr, nk, 0, 0, false},
+                    KcItemsW{grev.cu_rev, nb, grev.cap, tq, kc.items, kc.item_cap}, nb,
+                    (int)hkv, sums, kc.item_count, st);
   if (rc) return rc;
-  rc = launch_zero_i32(kc.ritem_count, hkv, st);
-  if (rc) return rc;
-  rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, tq, nullptr, nk},
-                KcItemsW{grev.cu_rev, nb, grev.cap, tq, kc.items, kc.item_cap}, nb, (int)hkv,
-                sums, kc.item_count, st);
-  if (rc) return rc;
-  rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, rq, cu_blk, nk},
+  rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, rq, cu_blk, nk, 0, KC_RES_KEYS, false},
                 KcItemsW{grev.cu_rev, nb, grev.cap, rq, kc.ritems, kc.ritem_cap}, nb,
                 (int)hkv, sums, kc.ritem_count, st);
   if (rc) return rc;
-  hipLaunchKernelGGL(kc_offsets_kernel, dim3(1), dim3(64), 0, st, kc.item_count,
-                     kc.ritem_count, (int)hkv, kc.item_off, kc.ritem_off, counter);
+  if (res_max > KC_RES_KEYS) {
+    rc = run_scan(
+        KcItemsF{grev.cu_rev, nb, grev.cap, rq, cu_blk, nk, KC_RES_KEYS, res_max, false},
+        KcItemsW{grev.cu_rev, nb, grev.cap, rq, kc.r2items, kc.r2item_cap}, nb, (int)hkv, sums,
+        kc.r2item_count, st);
+    if (rc) return rc;
+  }
+  rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, tq, cu_blk, nk, 0, res_max, true},
+                KcItemsW{grev.cu_rev, nb, grev.cap, tq, kc.fitems, kc.fitem_cap}, nb,
+                (int)hkv, sums, kc.fitem_count, st);
+  if (rc) return rc;
+  const KcCounts c{{kc.item_count, kc.ritem_count, kc.r2item_count, kc.fitem_count},
+                   {kc.item_off, kc.ritem_off, kc.r2item_off, kc.fitem_off}};
+  hipLaunchKernelGGL(kc_offsets_kernel, dim3(1), dim3(64), 0, st, c, (int)hkv, counter);
   LSRM_CHECK_LAUNCH();
   return LSRM_OK;
 }

@@ -126,25 +126,65 @@ def test_two_batch_elements():
     _check_oracle(args, o, lse)
 
 
-def test_local_rows_unchanged_by_the_flag():
-    # Rows with locality (every tile is a run or a valid union): no tile is
-    # flagged, the gathered pass has no work and the result is the same bits.
-    # 3D-aware rows of cfg3-style voxel tokens: nearest block centroids.
-    w = W.config(3, n=16384, heads=2)
+def test_block_rows_unchanged_by_the_flag():
+    # Rows shared by the 128 queries of each block (block-level selection):
+    # every tile is a full run tile, none is grouped, so the gathered pass
+    # has no work and the result is the same bits.
+    nb, blk, topk = 40, 128, 8
+    n = nb * blk
+    g = torch.Generator().manual_seed(12)
+    per_block = torch.stack([torch.randperm(nb, generator=g)[:topk] for _ in range(nb)])
+    rows = per_block.repeat_interleave(blk, dim=0).to(torch.int32)
+    rows = torch.stack([rows, rows.flip(1)]).contiguous()
+    q, k, v = ((0.5 * torch.randn(n, 2, 64, generator=g)).to(torch.bfloat16) for _ in range(3))
+    args = (q, k, v, rows, torch.tensor([0, nb], dtype=torch.int32),
+            torch.arange(0, n + 1, blk, dtype=torch.int32), torch.tensor([0, n], dtype=torch.int32))
+    a = _fwd(args, True)
+    b = _fwd(args, False)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def _aware_rows(heads=2, seed=12):
+    # 3D-aware rows of cfg3-style voxel tokens (blocks of 32..512 Morton-
+    # ordered voxels): each token's nearest 16 block centroids.
+    w = W.config(3, n=16384, heads=heads)
     nv = w.voxel_coords.shape[0]
     cu_all = w.cu_block_tokens.numpy().astype(np.int64)
     cu_v = (cu_all[w.n_image_blocks:] - cu_all[w.n_image_blocks]).astype(np.int32)
     coords = np.concatenate([np.zeros((nv, 1), np.int64), w.voxel_coords], axis=1)
     pts = volume_points_ref(coords, 64, 1.0)
     sel = nearest_blocks_ref(pts, cu_v, np.array([0, len(cu_v) - 1]), np.array([0, nv]), 16)
-    rows = torch.from_numpy(np.broadcast_to(sel, (2, nv, 16)).copy())
-    g = torch.Generator().manual_seed(12)
-    q, k, v = ((0.5 * torch.randn(nv, 2, 64, generator=g)).to(torch.bfloat16) for _ in range(3))
-    args = (q, k, v, rows, torch.tensor([0, len(cu_v) - 1], dtype=torch.int32),
+    rows = torch.from_numpy(np.broadcast_to(sel, (heads, nv, 16)).copy())
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = ((0.5 * torch.randn(nv, heads, 64, generator=g)).to(torch.bfloat16)
+               for _ in range(3))
+    return (q, k, v, rows, torch.tensor([0, len(cu_v) - 1], dtype=torch.int32),
             torch.from_numpy(cu_v), torch.tensor([0, nv], dtype=torch.int32))
-    a = _fwd(args, True)
-    b = _fwd(args, False)
-    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_3d_aware_rows_take_the_gathered_pass():
+    # Grouped tiles whose masked union pass would compute far more key-rows
+    # than their rows' own keys go to the gathered pass (the cost rule of
+    # the plan): on 3D-aware rows most do.  Forward and backward of the
+    # key-centric plan against the oracle.
+    args = _aware_rows()
+    q, k, v, rows, cu_sb, cu_blk, cu_q = args
+    dev = [t.to(DEV) for t in args]
+    plan = H.SelAttnPlan(dev[0].shape, dev[1].shape, dev[3], dev[4], dev[5], dev[6],
+                         backward=True, key_centric=True)
+    o, lse = plan.fwd(dev[0], dev[1], dev[2], 0.125)
+    _check_oracle(args, o, lse)
+    o2, _ = _fwd(args, False)
+    assert not torch.equal(o, o2)
+    g = torch.Generator().manual_seed(113)
+    do = (0.5 * torch.randn(q.shape, generator=g)).to(q.dtype)
+    dq, dk, dv, _ = plan.bwd(do.to(DEV), dev[0], dev[1], dev[2], o, lse, 0.125)
+    qf, kf, vf = (t.float().requires_grad_() for t in (q, k, v))
+    o_ref, _ = sel_attn_ref(qf, kf, vf, rows, cu_sb, cu_blk, cu_q, 0.125)
+    o_ref.backward(do.float())
+    assert_attn_close(dq, qf.grad, "dq")
+    assert_attn_close(dk, kf.grad, "dk")
+    assert_attn_close(dv, vf.grad, "dv")
 
 
 def test_plan_with_backward_and_key_centric():
@@ -221,12 +261,19 @@ def test_backward_gathered_dq_duplicates_empty_rows(hq, hkv, d):
     assert all(torch.equal(x, y) for x, y in zip((dq, dk, dv, delta), again))
 
 
-def test_large_and_small_blocks_both_gathered_kernels():
-    # Blocks of 4..600 keys: those of at most 256 keys run with the block
-    # resident in LDS, the larger ones through the streaming gathered tiles.
-    args = _random_rows(n=20000, topk=8, seed=13, sizes=(4, 600))
+@pytest.mark.parametrize("hq,hkv,d,topk", [(2, 2, 64, 8), (8, 2, 64, 20), (2, 2, 32, 8),
+                                           (2, 2, 128, 8)])
+def test_large_and_small_blocks_all_gathered_kernels(hq, hkv, d, topk):
+    # Blocks of 4..700 keys: those of at most 256 keys run with the block
+    # resident in LDS (four waves), those of 257..512 keys too at head dim
+    # <= 64 (eight waves, two groups of four tiles with the softmax
+    # reference raised between them), the rest through the streaming
+    # gathered tiles.  topk 20: the merge takes the slots 16 at a time.
+    args = _random_rows(n=20000, hq=hq, hkv=hkv, d=d, topk=topk, seed=13, sizes=(4, 700))
     cu = args[5]
     lens = cu[1:] - cu[:-1]
-    assert (lens > 256).any() and (lens <= 256).any()
+    assert (lens <= 256).any() and ((lens > 256) & (lens <= 512)).any() and (lens > 512).any()
     o, lse = _fwd(args, True)
     _check_oracle(args, o, lse)
+    again = _fwd(args, True)
+    assert torch.equal(o, again[0]) and torch.equal(lse, again[1])
