@@ -42,7 +42,7 @@ struct AttnArgs {
   RevMap qrev;       // backward: block -> queries of grouped tiles that
                      // selected it (one entry per listing, ascending)
   KeyItems items;    // backward: key chunks of every block
-  KcPlan kc;         // forward, key-centric plans only (kc.items null otherwise)
+  KcPlan kc;         // key-centric plans only (kc.fitems null otherwise)
 };
 
 // Compile-time value tag (e.g. a ring-slot phase).

@@ -38,9 +38,10 @@ namespace lsrm {
 // to zero (the passes of the forward's grouped tiles; no softmax state is
 // carried, so either way each row's dQ is a plain sum over the keys it
 // attends); in a key-centric plan the flagged tiles are left to mode 2.
-// MODE 2 (DQ_GATHER): the gathered tiles of a key-centric plan, each row
-// writing the block's share of its dQ (one slot of its row, in the input
-// type) for kc_dq_merge_kernel.
+// MODE 2 (DQ_GATHER): the gathered tiles of a key-centric plan over blocks
+// the resident kernels do not take (no keys, or more than kc_res_max), each
+// row writing the block's share of its dQ (one slot of its row, in the
+// input type) for kc_dq_merge_kernel.
 constexpr int DQ_RUN = 0, DQ_UNION = 1, DQ_GATHER = 2;
 
 template <int DT, int D, int MODE>
@@ -60,7 +61,7 @@ sel_attn_dq_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
   const int32_t* head_off =
-      GATHER ? a.kc.item_off : (UNION ? a.plan.ghead_off : a.plan.head_off);
+      GATHER ? a.kc.fitem_off : (UNION ? a.plan.ghead_off : a.plan.head_off);
   const int2* tiles = UNION ? a.plan.gtiles : a.plan.tiles;
   int32_t* queue = a.plan.counter + (GATHER ? KC_QUEUE_SLOT : (UNION ? 4 : 0));
   // A plan built without its backward part: nothing here is valid to read.
@@ -83,7 +84,7 @@ sel_attn_dq_kernel(AttnArgs a) {
     const int h = head_of(head_off, a.hkv, w);
     int q0, qn, gblk = 0, ge0 = 0;
     if constexpr (GATHER) {
-      const int4 it = a.kc.items[(int64_t)h * a.kc.item_cap + (w - head_off[h])];
+      const int4 it = a.kc.fitems[(int64_t)h * a.kc.fitem_cap + (w - head_off[h])];
       gblk = it.x;
       ge0 = it.y;
       q0 = 0;
@@ -943,6 +944,235 @@ sel_attn_dkdv_kernel(AttnArgs a) {
   leave_queue_xcd(a.plan.counter + 8, a.plan.counter + 3);
 }
 
+// Key-centric dQ of blocks held whole in LDS (the forward's resident items:
+// BIG = 0, four waves, blocks of 1..KC_RES_KEYS keys; BIG = 1, eight waves
+// in two groups running their own chunks, blocks of KC_RES_KEYS+1 ..
+// KC_RES2_KEYS keys at head dim <= 64).  The block's K and V are copied
+// into LDS once per item; each chunk of up to 128 gathered rows loads its Q,
+// dO and O rows (one chunk ahead, listings two ahead), forms Delta =
+// rowsum(O dO), and for every key tile computes S^T = K Q^T and dP^T = V
+// dO^T, dS = P (dP - Delta) with P = 2^(S scale log2 e - LSE), and dQ^T +=
+// K^T dS^T: the arithmetic of the streaming gathered tiles, key tile by key
+// tile in the same order.  Each row writes its share of dQ at [head, query,
+// slot] for kc_dq_merge_kernel, and Delta.
+template <int DT, int D, int BIG>
+__global__ __launch_bounds__(BIG ? 512 : 256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+kc_resident_dq_kernel(AttnArgs a) {
+  using G = KvTile<D>;
+  constexpr int NS = D / 16;
+  constexpr int ND = D / 32;
+  constexpr int NT = (BIG ? KC_RES2_KEYS : KC_RES_KEYS) / KT;
+  constexpr int NWG = BIG ? 2 : 1;  // groups of four waves
+  constexpr bool PF = D <= 64;      // Q / dO / O rows loaded one chunk ahead
+  __shared__ __align__(1024) char sK[NT][G::BYTES];
+  __shared__ __align__(1024) char sV[NT][G::BYTES];
+  __shared__ int s_slot;
+  const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
+  const int wg = wv >> 2, wl = wv & 3;  // wave group, wave inside the group
+  const int hb = lane >> 5, l32 = lane & 31;
+  // A plan built without its backward part: nothing here is valid to read.
+  if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC) return;
+  const int32_t* head_off = BIG ? a.kc.r2item_off : a.kc.ritem_off;
+  const int4* items = BIG ? a.kc.r2items : a.kc.ritems;
+  const int64_t item_cap = BIG ? a.kc.r2item_cap : a.kc.ritem_cap;
+  int32_t* queue = a.plan.counter + (BIG ? KC_R2QUEUE_SLOT : KC_RQUEUE_SLOT);
+  const int total = head_off[a.hkv];
+  // An empty queue: leave it untouched (no fetch, so nothing to reset).
+  if (total == 0) return;
+  const uint32_t row_bytes = (uint32_t)a.hkv * D * 2;
+  const int tq = ROWS / a.g;
+  const int64_t cap = a.kc.grev.cap;
+
+  for (;;) {
+    const int w = uniform(fetch_work(queue, &s_slot));
+    if (w >= total) break;
+    const int h = head_of(head_off, a.hkv, w);
+    const int4 it = items[(int64_t)h * item_cap + (w - head_off[h])];
+    const int c = it.x, e0 = it.y, n = it.z;
+    int64_t s0 = a.cu_blk[c], s1 = a.cu_blk[c + 1];
+    s0 = s0 < 0 ? 0 : (s0 > a.nk ? a.nk : s0);
+    s1 = s1 < s0 ? s0 : (s1 > a.nk ? a.nk : s1);
+    const int len = uniform((int)(s1 - s0));  // 1..NT * KT (plan)
+    const int ntiles = (len + KT - 1) / KT;
+    const char* kbase = reinterpret_cast<const char*>(a.k + (int64_t)h * D);
+    const char* vbase = reinterpret_cast<const char*>(a.v + (int64_t)h * D);
+    // The block into LDS: wave group t % NWG copies tile t; load j of its
+    // wave wl covers rows (wl * LPW + j) * KPL + lane / CH; keys past the
+    // block load its first token (in bounds; masked below).
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (t < ntiles && t % NWG == wg) {
+#pragma unroll
+        for (int j = 0; j < G::LPW; ++j) {
+          const int row = (wl * G::LPW + j) * G::KPL + lane / G::CH;
+          const int key = t * KT + row;
+          const uint32_t tok = (uint32_t)(key < len ? s0 + key : s0);
+          const uint32_t voff = tok * row_bytes + (((lane % G::CH) ^ G::swz(row)) << 4);
+          const uint32_t dst = (uint32_t)(wl * G::LPW + j) * 1024;
+          copy16_to_lds(kbase, voff, lds_addr(sK[t]) + dst);
+          copy16_to_lds(vbase, voff, lds_addr(sV[t]) + dst);
+        }
+      }
+    }
+    wait_copies();
+    __syncthreads();
+
+    const int r = wl * 32 + l32;
+    const int step = NWG * tq;
+    auto chunk_ok = [&](int cbx) { return r < (n - cbx < tq ? n - cbx : tq) * a.g; };
+    auto load_listing = [&](int cbx) -> int32_t {
+      return cbx < n ? a.kc.grev.rev[(int64_t)h * cap + e0 + cbx + (chunk_ok(cbx) ? r / a.g : 0)]
+                     : 0;
+    };
+    // Q, dO and O of the row of listing lv (zeros for rows outside the chunk)
+    auto load_rows = [&](int cbx, int32_t lv, u32x4* qd, u32x4* dd, u32x4* od) {
+      const int64_t qx = lv / a.topk_n;
+      const bool ok = cbx < n && chunk_ok(cbx);
+      const int hx = h * a.g + (ok ? r % a.g : 0);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int64_t off = (qx * a.hq + hx) * D + s * 16 + hb * 8;
+        qd[s] = ok ? *reinterpret_cast<const u32x4*>(a.q + off) : u32x4{0u, 0u, 0u, 0u};
+        dd[s] = ok ? *reinterpret_cast<const u32x4*>(a.dout + off) : u32x4{0u, 0u, 0u, 0u};
+        od[s] = ok ? *reinterpret_cast<const u32x4*>(a.o + off) : u32x4{0u, 0u, 0u, 0u};
+      }
+    };
+    const int cb0 = wg * tq;
+    int32_t lv_cur = load_listing(cb0);
+    u32x4 qn_[PF ? NS : 1], dn_[PF ? NS : 1], on_[PF ? NS : 1];
+    if constexpr (PF) load_rows(cb0, lv_cur, qn_, dn_, on_);
+    int32_t lv_next = load_listing(cb0 + step);
+    for (int cb = cb0; cb < n; cb += step) {
+      const int rows = (n - cb < tq ? n - cb : tq) * a.g;
+      const bool row_ok = r < rows;
+      u32x4 qb[NS], dob[NS], ob[NS];
+      if constexpr (PF) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          qb[s] = qn_[s];
+          dob[s] = dn_[s];
+          ob[s] = on_[s];
+        }
+      } else {
+        load_rows(cb, lv_cur, qb, dob, ob);
+      }
+      const int64_t qi = lv_cur / a.topk_n;
+      const int64_t slot = lv_cur - qi * a.topk_n;
+      const int hh = h * a.g + (row_ok ? r % a.g : 0);
+      // next chunk: its rows from the listing loaded one chunk ago; the
+      // listing after it
+      if constexpr (PF) load_rows(cb + step, lv_next, qn_, dn_, on_);
+      lv_cur = lv_next;
+      lv_next = load_listing(cb + 2 * step);
+      if (wl * 32 >= rows) continue;  // wave-uniform: no row of this chunk
+      float dpart = 0.0f;
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dpart += to_f32<DT>((uint16_t)(ob[s][i] & 0xffffu)) *
+                   to_f32<DT>((uint16_t)(dob[s][i] & 0xffffu));
+          dpart += to_f32<DT>((uint16_t)(ob[s][i] >> 16)) *
+                   to_f32<DT>((uint16_t)(dob[s][i] >> 16));
+        }
+      const float delta = dpart + __shfl_xor(dpart, 32);
+      // Exponent bias -lse; -inf (P = 0) for rows outside the chunk and rows
+      // that attend nothing.
+      float bias = -__builtin_inf();
+      if (row_ok) {
+        const float l = a.lse_in[(int64_t)hh * a.nq + qi];
+        if (l > -__builtin_inf()) bias = -l;
+      }
+      f32x16 dqacc[ND];
+#pragma unroll
+      for (int i = 0; i < ND; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) dqacc[i][v] = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+        if (kt < ntiles) {
+          const char* ks = sK[kt];
+          const char* vs = sV[kt];
+          f32x16 sacc[2], dpacc[2];
+#pragma unroll
+          for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sacc[blk][v] = dpacc[blk][v] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+              const int o = G::off(blk * 32 + l32, 2 * s + hb);
+              sacc[blk] = mfma32<DT>(*reinterpret_cast<const u32x4*>(ks + o), qb[s], sacc[blk]);
+              dpacc[blk] = mfma32<DT>(*reinterpret_cast<const u32x4*>(vs + o), dob[s], dpacc[blk]);
+            }
+          }
+          if (kt * KT + KT > len) {
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+              for (int v = 0; v < 16; ++v)
+                if (kt * KT + blk * 32 + acc_row(v, hb) >= len) sacc[blk][v] = -__builtin_inf();
+          }
+          u32x4 dsb[2][2];
+#pragma unroll
+          for (int blk = 0; blk < 2; ++blk) {
+            float ds[16];
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              ds[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[blk][v], a.scale_log2, bias)) *
+                      (dpacc[blk][v] - delta);
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc)
+              dsb[blk][cc] = u32x4{pack2<DT>(ds[cc * 8 + 0], ds[cc * 8 + 1]),
+                                   pack2<DT>(ds[cc * 8 + 2], ds[cc * 8 + 3]),
+                                   pack2<DT>(ds[cc * 8 + 4], ds[cc * 8 + 5]),
+                                   pack2<DT>(ds[cc * 8 + 6], ds[cc * 8 + 7])};
+          }
+          // dQ^T += K^T dS^T: K^T by transposed reads (slot e of lane (hb,
+          // row d) = key blk*32 + cc*16 + (e/4)*8 + hb*4 + e%4, the score
+          // layout).
+          const int gi = lane & 15, dh = (lane >> 4) & 1;
+#pragma unroll
+          for (int db = 0; db < ND; ++db) {
+            const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+            const int cbk = dcol >> 3, half = (dcol & 4) * 2;
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+              for (int cc = 0; cc < 2; ++cc) {
+                const int k0 = blk * 32 + cc * 16 + hb * 4 + (gi >> 2);
+                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(ks + G::off(k0, cbk) + half));
+                const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(ks + G::off(k0 + 8, cbk) + half));
+                const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+                const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+                dqacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]}, dsb[blk][cc], dqacc[db]);
+              }
+          }
+        }
+      }
+      if (row_ok) {
+        uint16_t* drow = a.kc.part_o + ((((int64_t)h * a.nq + qi) * a.topk_n + slot) * a.g +
+                                        (r % a.g)) * D;
+#pragma unroll
+        for (int db = 0; db < ND; ++db)
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi) {
+            const int v = gi * 4;
+            // dS was kept unscaled: dQ = scale * (dS' K)
+            *reinterpret_cast<u32x2*>(drow + db * 32 + gi * 8 + hb * 4) =
+                u32x2{pack2<DT>(a.scale * dqacc[db][v], a.scale * dqacc[db][v + 1]),
+                      pack2<DT>(a.scale * dqacc[db][v + 2], a.scale * dqacc[db][v + 3])};
+          }
+        if (hb == 0) a.lse[(int64_t)hh * a.nq + qi] = delta;
+      }
+    }
+    __syncthreads();  // the item's reads of sK / sV end before the next copies
+  }
+  wait_copies();
+  leave_queue(queue, queue + 2);
+}
+
 // Key-centric dQ merge: one thread per (kv head, query, query head, 8
 // channels) of the marked queries; the slot shares of dQ written by the
 // gathered tiles are added in slot order in fp32 and rounded once.  Slots
@@ -1025,13 +1255,25 @@ int launch_bwd_t(const AttnArgs& a, hipStream_t st) {
                        st, a);
     LSRM_CHECK_LAUNCH();
   }
-  if (a.kc.items) {  // key-centric plans: gathered dQ tiles, then the merge
+  if (a.kc.fitems) {  // key-centric plans: gathered dQ tiles, then the merge
     const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D, DQ_GATHER>);
     const int grid = persistent_grid(fn, 256, 0);
     if (grid <= 0) return LSRM_ERR_LAUNCH;
     hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D, DQ_GATHER>), dim3(grid), dim3(256), 0,
                        st, a);
     LSRM_CHECK_LAUNCH();
+    const void* fr = reinterpret_cast<const void*>(&kc_resident_dq_kernel<DT, D, 0>);
+    const int gr = persistent_grid(fr, 256, 0);
+    if (gr <= 0) return LSRM_ERR_LAUNCH;
+    hipLaunchKernelGGL((kc_resident_dq_kernel<DT, D, 0>), dim3(gr), dim3(256), 0, st, a);
+    LSRM_CHECK_LAUNCH();
+    if constexpr (kc_res_max(D) > KC_RES_KEYS) {
+      const void* fr2 = reinterpret_cast<const void*>(&kc_resident_dq_kernel<DT, D, 1>);
+      const int gr2 = persistent_grid(fr2, 512, 0);
+      if (gr2 <= 0) return LSRM_ERR_LAUNCH;
+      hipLaunchKernelGGL((kc_resident_dq_kernel<DT, D, 1>), dim3(gr2), dim3(512), 0, st, a);
+      LSRM_CHECK_LAUNCH();
+    }
     const int gm = device_cu_count() * 16;
     if (gm <= 0) return LSRM_ERR_LAUNCH;
     hipLaunchKernelGGL((kc_dq_merge_kernel<DT, D>), dim3(gm), dim3(256), 0, st, a);

@@ -1020,7 +1020,7 @@ int launch_fwd_t(const AttnArgs& a, hipStream_t st) {
                        a);
     LSRM_CHECK_LAUNCH();
   }
-  if (a.kc.items) {  // key-centric plans: gathered tiles, then the merge
+  if (a.kc.fitems) {  // key-centric plans: gathered tiles, then the merge
     const void* fg = reinterpret_cast<const void*>(&sel_attn_fwd_kernel<DT, D, FWD_GATHER>);
     const int gg = persistent_grid(fg, 256, 0);
     if (gg <= 0) return LSRM_ERR_LAUNCH;

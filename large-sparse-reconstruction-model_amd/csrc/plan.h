@@ -63,41 +63,36 @@ int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
 int mark_grouped_queries(const TilePlan& plan, int64_t hkv, int64_t nq,
                          uint8_t* flags, hipStream_t st);
 
-// Key-centric forward part of a plan (plan flag LSRM_PLAN_KEY_CENTRIC): the
-// grouped tiles whose union cannot be run in one pass (flag 1) are taken out
-// of the grouped-tile kernel; their queries are listed per block (`grev`,
-// ascending, one listing q * topk + j per slot j that names the block), and
-// each block's list is cut into gathered tiles of at most ROWS / g queries:
-// item {c, e0, n, 0} = block c, listings e0 .. e0 + n of grev's segment of
-// head h.  The forward writes one partial result per (query, slot, query
-// head) -- O normalised by its own row sum in the input type and its log2
-// LSE -- and a merge pass combines each query's partials in slot order.
+// Key-centric part of a plan (plan flag LSRM_PLAN_KEY_CENTRIC): the grouped
+// tiles flagged by kc_flag_kernel (flag 1) are taken out of the grouped-tile
+// kernels; their queries are listed per block (`grev`, ascending, one
+// listing q * topk + j per slot j that names the block), and each block's
+// list is cut into items {c, e0, n, 0} = block c, listings e0 .. e0 + n of
+// grev's segment of head h.  The forward writes one partial result per
+// (query, slot, query head) -- O normalised by its own row sum in the input
+// type and its log2 LSE -- and the dQ pass the slot's share of dQ; merge
+// passes combine each query's partials in slot order.
 struct KcPlan {
   uint8_t* gflag;        // [hkv, n_q] per grouped tile (index as gtiles)
   uint8_t* qmark;        // [hkv, n_q] queries of flagged tiles
   RevMap grev;           // block -> marked queries, cap = n_q * topk per head
-  int4* items;           // [hkv, item_cap]
-  int64_t item_cap;
-  int32_t* item_count;   // [hkv]
-  int32_t* item_off;     // [hkv + 1]
   uint16_t* part_o;      // [hkv, n_q, topk, g, D] input type
   float* part_lse;       // [hkv, n_q, topk, g]
-  // Forward items of blocks with at most KC_RES_KEYS keys, which the
-  // forward runs with the block resident in LDS: {c, e0, n, 0} with up to
-  // KC_RES_CHUNKS * tq listings (dQ takes every block from `items`).
+  // Items of blocks with 1..KC_RES_KEYS keys, run with the block resident
+  // in LDS (forward and dQ): up to KC_RES_CHUNKS * tq listings each.
   int4* ritems;
   int64_t ritem_cap;
   int32_t* ritem_count;  // [hkv]
   int32_t* ritem_off;    // [hkv + 1]
   // The same for blocks of KC_RES_KEYS + 1 .. KC_RES2_KEYS keys (head dim
-  // <= 64; empty otherwise), run by the eight-wave resident forward.
+  // <= 64; empty otherwise), run by the eight-wave resident kernels.
   int4* r2items;
   int64_t r2item_cap;
   int32_t* r2item_count;  // [hkv]
   int32_t* r2item_off;    // [hkv + 1]
-  // The streaming gathered forward's items: `items` of the blocks the
-  // resident forwards do not take (no keys, or more than kc_res_max of the
-  // plan's head dim).
+  // The streaming gathered tiles' items: blocks the resident kernels do not
+  // take (no keys, or more than kc_res_max of the plan's head dim), at most
+  // tq listings each.  fitems is null in plans without this part.
   int4* fitems;
   int64_t fitem_cap;
   int32_t* fitem_count;  // [hkv]

@@ -876,14 +876,14 @@ struct KcItemsW {
   }
 };
 
-// Per-head offsets of the item lists (all blocks, resident, eight-wave
-// resident, streaming forward) and their cleared work counters.
+// Per-head offsets of the item lists (resident, eight-wave resident,
+// streaming) and their cleared work counters.
 struct KcCounts {
-  const int32_t* count[4];
-  int32_t* off[4];
+  const int32_t* count[3];
+  int32_t* off[3];
 };
 __global__ void kc_offsets_kernel(KcCounts c, int hkv, int32_t* counter) {
-  if (threadIdx.x < 4 && blockIdx.x == 0) {
+  if (threadIdx.x < 3 && blockIdx.x == 0) {
     const int32_t* cnt = c.count[threadIdx.x];
     int32_t* off = c.off[threadIdx.x];
     int acc = 0;
@@ -908,10 +908,6 @@ int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_
                    int32_t* counter, hipStream_t st) {
   const int rq = tq * KC_RES_CHUNKS;
   const int res_max = kc_res_max((int)(head_dim > 0 ? head_dim : 1));
-  kc.item_cap = grev.cap / (tq > 0 ? tq : 1) + nb + 1;
-  kc.items = ws.take<int4>((size_t)(hkv * kc.item_cap));
-  kc.item_count = ws.take<int32_t>((size_t)hkv);
-  kc.item_off = ws.take<int32_t>((size_t)(hkv + 1));
   kc.ritem_cap = grev.cap / (rq > 0 ? rq : 1) + nb + 1;
   kc.ritems = ws.take<int4>((size_t)(hkv * kc.ritem_cap));
   kc.ritem_count = ws.take<int32_t>((size_t)hkv);
@@ -920,24 +916,20 @@ int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_
   kc.r2items = ws.take<int4>((size_t)(hkv * kc.r2item_cap));
   kc.r2item_count = ws.take<int32_t>((size_t)hkv);
   kc.r2item_off = ws.take<int32_t>((size_t)(hkv + 1));
-  kc.fitem_cap = kc.item_cap;
+  kc.fitem_cap = grev.cap / (tq > 0 ? tq : 1) + nb + 1;
   kc.fitems = ws.take<int4>((size_t)(hkv * kc.fitem_cap));
   kc.fitem_count = ws.take<int32_t>((size_t)hkv);
   kc.fitem_off = ws.take<int32_t>((size_t)(hkv + 1));
   int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, hkv));
   if (!ws.base || ws.dry) return LSRM_OK;
   if (!ws.ok()) return LSRM_ERR_WORKSPACE;
-  for (int32_t* cnt : {kc.item_count, kc.ritem_count, kc.r2item_count, kc.fitem_count}) {
+  for (int32_t* cnt : {kc.ritem_count, kc.r2item_count, kc.fitem_count}) {
     const int rc = launch_zero_i32(cnt, hkv, st);
     if (rc) return rc;
   }
-  int rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, tq, nullptr, nk, 0, 0, false},
-                    KcItemsW{grev.cu_rev, nb, grev.cap, tq, kc.items, kc.item_cap}, nb,
-                    (int)hkv, sums, kc.item_count, st);
-  if (rc) return rc;
-  rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, rq, cu_blk, nk, 0, KC_RES_KEYS, false},
-                KcItemsW{grev.cu_rev, nb, grev.cap, rq, kc.ritems, kc.ritem_cap}, nb,
-                (int)hkv, sums, kc.ritem_count, st);
+  int rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, rq, cu_blk, nk, 0, KC_RES_KEYS, false},
+                    KcItemsW{grev.cu_rev, nb, grev.cap, rq, kc.ritems, kc.ritem_cap}, nb,
+                    (int)hkv, sums, kc.ritem_count, st);
   if (rc) return rc;
   if (res_max > KC_RES_KEYS) {
     rc = run_scan(
@@ -950,8 +942,8 @@ int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_
                 KcItemsW{grev.cu_rev, nb, grev.cap, tq, kc.fitems, kc.fitem_cap}, nb,
                 (int)hkv, sums, kc.fitem_count, st);
   if (rc) return rc;
-  const KcCounts c{{kc.item_count, kc.ritem_count, kc.r2item_count, kc.fitem_count},
-                   {kc.item_off, kc.ritem_off, kc.r2item_off, kc.fitem_off}};
+  const KcCounts c{{kc.ritem_count, kc.r2item_count, kc.fitem_count},
+                   {kc.ritem_off, kc.r2item_off, kc.fitem_off}};
   hipLaunchKernelGGL(kc_offsets_kernel, dim3(1), dim3(64), 0, st, c, (int)hkv, counter);
   LSRM_CHECK_LAUNCH();
   return LSRM_OK;
