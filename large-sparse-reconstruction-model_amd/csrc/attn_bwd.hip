@@ -1094,15 +1094,18 @@ kc_resident_dq_kernel(AttnArgs a) {
           const char* ks = sK[kt];
           const char* vs = sV[kt];
           f32x16 sacc[2], dpacc[2];
+          const int nblk = kt * KT + 32 < len ? 2 : 1;  // halves holding keys (dS = 0 past)
 #pragma unroll
           for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) sacc[blk][v] = dpacc[blk][v] = 0.0f;
+            if (blk < nblk) {
 #pragma unroll
-            for (int s = 0; s < NS; ++s) {
-              const int o = G::off(blk * 32 + l32, 2 * s + hb);
-              sacc[blk] = mfma32<DT>(*reinterpret_cast<const u32x4*>(ks + o), qb[s], sacc[blk]);
-              dpacc[blk] = mfma32<DT>(*reinterpret_cast<const u32x4*>(vs + o), dob[s], dpacc[blk]);
+              for (int s = 0; s < NS; ++s) {
+                const int o = G::off(blk * 32 + l32, 2 * s + hb);
+                sacc[blk] = mfma32<DT>(*reinterpret_cast<const u32x4*>(ks + o), qb[s], sacc[blk]);
+                dpacc[blk] = mfma32<DT>(*reinterpret_cast<const u32x4*>(vs + o), dob[s], dpacc[blk]);
+              }
             }
           }
           if (kt * KT + KT > len) {
@@ -1137,6 +1140,7 @@ kc_resident_dq_kernel(AttnArgs a) {
             const int cbk = dcol >> 3, half = (dcol & 4) * 2;
 #pragma unroll
             for (int blk = 0; blk < 2; ++blk)
+              if (blk < nblk)
 #pragma unroll
               for (int cc = 0; cc < 2; ++cc) {
                 const int k0 = blk * 32 + cc * 16 + hb * 4 + (gi >> 2);

@@ -809,11 +809,14 @@ kc_resident_fwd_kernel(AttnArgs a) {
             for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
               for (int v = 0; v < 16; ++v) sc[t4][blk][v] = 0.0f;
+              // a 32-key half past the block's end stays all masked
+              if (kt * KT + blk * 32 < len) {
 #pragma unroll
-              for (int s = 0; s < NS; ++s) {
-                const u32x4 ka = *reinterpret_cast<const u32x4*>(
-                    sK[kt] + G::off(blk * 32 + l32, 2 * s + hb));
-                sc[t4][blk] = mfma32<DT>(ka, qb[s], sc[t4][blk]);
+                for (int s = 0; s < NS; ++s) {
+                  const u32x4 ka = *reinterpret_cast<const u32x4*>(
+                      sK[kt] + G::off(blk * 32 + l32, 2 * s + hb));
+                  sc[t4][blk] = mfma32<DT>(ka, qb[s], sc[t4][blk]);
+                }
               }
             }
             if (kt * KT + KT > len) {
@@ -874,11 +877,13 @@ kc_resident_fwd_kernel(AttnArgs a) {
               }
             }
             const int gi = lane & 15, dh = (lane >> 4) & 1;
+            const int nblk = kt * KT + 32 < len ? 2 : 1;  // halves holding keys (P = 0 past)
 #pragma unroll
             for (int db = 0; db < ND; ++db) {
               const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
 #pragma unroll
               for (int blk = 0; blk < 2; ++blk)
+                if (blk < nblk)
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {
                   const int k0 = blk * 32 + cc * 16 + hb * 4 + (gi >> 2);
