@@ -603,14 +603,18 @@ __global__ __launch_bounds__(256) void rev_sort_kernel(
 // Pair i = (h * nq + q) * k + j: key h * nb + block for a valid slot of a
 // marked query, else the sentinel hkv * nb; value the listing (q, or
 // q * k + j when encoding the slot).  Generated in (h, q, j) order, so the
-// stable sort leaves each block's listings ascending.
+// stable sort leaves each block's listings ascending.  One thread per pair
+// (n = hkv * nq * k < 2^31, checked by the caller): the row reads and the
+// key / value writes are contiguous across the wave.
 __global__ __launch_bounds__(256) void rev_pairs_kernel(
     const int32_t* __restrict__ topk, int64_t hkv, int64_t nq, int k,
     const int32_t* __restrict__ cu_q, int64_t batch, const int32_t* __restrict__ cu_sb,
     int64_t nb, const uint8_t* __restrict__ only, bool encode, uint32_t* __restrict__ keys,
     int32_t* __restrict__ vals) {
-  const int64_t hq = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // h * nq + q
-  if (hq >= hkv * nq) return;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= hkv * nq * k) return;
+  const int64_t hq = i / k;  // h * nq + q
+  const int j = (int)(i - hq * k);
   const int h = (int)(hq / nq);
   const int64_t q = hq - (int64_t)h * nq;
   const uint32_t none = (uint32_t)(hkv * nb);
@@ -618,13 +622,10 @@ __global__ __launch_bounds__(256) void rev_pairs_kernel(
   int b, bs, nbb;
   bool start;
   query_batch(cu_q, batch, cu_sb, q, &b, &bs, &nbb, &start);
-  const int32_t* row = topk + hq * k;
-  for (int j = 0; j < k; ++j) {
-    const int v = row[j];
-    const bool ok = on && v >= 0 && v < nbb && (int64_t)bs + v < nb;
-    keys[hq * k + j] = ok ? (uint32_t)(h * nb + bs + v) : none;
-    vals[hq * k + j] = encode ? (int32_t)(q * k + j) : (int32_t)q;
-  }
+  const int v = topk[i];
+  const bool ok = on && v >= 0 && v < nbb && (int64_t)bs + v < nb;
+  keys[i] = ok ? (uint32_t)(h * nb + bs + v) : none;
+  vals[i] = encode ? (int32_t)(q * k + j) : (int32_t)q;
 }
 
 // seg[s] = first sorted position whose key is >= s, for s = 0 .. hkv * nb.
@@ -698,7 +699,7 @@ int build_query_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq, int64_
     if (rc) return rc;
     return launch_zero_i32(map.totals, hkv, st);
   }
-  hipLaunchKernelGGL(rev_pairs_kernel, dim3(ceil_div(hkv * nq, 256)), dim3(256), 0, st, topk,
+  hipLaunchKernelGGL(rev_pairs_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, st, topk,
                      hkv, nq, (int)topk_n, cu_q, batch, cu_sb, nb, only, encode_slot, keys,
                      vals);
   LSRM_CHECK_LAUNCH();
