@@ -611,12 +611,13 @@ __global__ __launch_bounds__(256) void rev_pairs_kernel(
     const int32_t* __restrict__ cu_q, int64_t batch, const int32_t* __restrict__ cu_sb,
     int64_t nb, const uint8_t* __restrict__ only, bool encode, uint32_t* __restrict__ keys,
     int32_t* __restrict__ vals) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= hkv * nq * k) return;
-  const int64_t hq = i / k;  // h * nq + q
-  const int j = (int)(i - hq * k);
-  const int h = (int)(hq / nq);
-  const int64_t q = hq - (int64_t)h * nq;
+  // 32-bit index arithmetic (every index here is below 2^31)
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if ((int64_t)i >= hkv * nq * k) return;
+  const uint32_t hq = i / (uint32_t)k;  // h * nq + q
+  const int j = (int)(i - hq * (uint32_t)k);
+  const int h = (int)(hq / (uint32_t)nq);
+  const int64_t q = (int64_t)(hq - (uint32_t)h * (uint32_t)nq);
   const uint32_t none = (uint32_t)(hkv * nb);
   const bool on = !only || only[hq];
   int b, bs, nbb;
@@ -661,7 +662,7 @@ __global__ __launch_bounds__(256) void rev_place_kernel(const uint32_t* __restri
                                                         int32_t* __restrict__ rev) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (int64_t)seg[n_seg]) return;
-  const int64_t h = keys[i] / nb;
+  const int64_t h = keys[i] / (uint32_t)nb;  // keys and nb below 2^31: 32-bit divide
   rev[h * cap + (i - seg[h * nb])] = vals[i];
 }
 
