@@ -9,6 +9,7 @@
 // queries, one stable radix sort of (head * n_blocks + block, listing) pairs
 // generated in (head, query, slot) order; for rows that are run tiles,
 // count -> scan -> atomic scatter -> per-segment sort.
+#include <algorithm>
 #include <rocprim/device/device_radix_sort.hpp>
 
 #include "plan.h"
@@ -611,33 +612,36 @@ __global__ __launch_bounds__(256) void rev_pairs_kernel(
     const int32_t* __restrict__ cu_q, int64_t batch, const int32_t* __restrict__ cu_sb,
     int64_t nb, const uint8_t* __restrict__ only, bool encode, uint32_t* __restrict__ keys,
     int32_t* __restrict__ vals) {
-  // 32-bit index arithmetic (every index here is below 2^31)
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if ((int64_t)i >= hkv * nq * k) return;
-  const uint32_t hq = i / (uint32_t)k;  // h * nq + q
-  const int j = (int)(i - hq * (uint32_t)k);
-  const int h = (int)(hq / (uint32_t)nq);
-  const int64_t q = (int64_t)(hq - (uint32_t)h * (uint32_t)nq);
+  // 32-bit index arithmetic (every index here is below 2^31); a grid-stride
+  // loop over a bounded grid
+  const uint32_t n = (uint32_t)(hkv * nq * k);
   const uint32_t none = (uint32_t)(hkv * nb);
-  const bool on = !only || only[hq];
-  int b, bs, nbb;
-  bool start;
-  query_batch(cu_q, batch, cu_sb, q, &b, &bs, &nbb, &start);
-  const int v = topk[i];
-  const bool ok = on && v >= 0 && v < nbb && (int64_t)bs + v < nb;
-  keys[i] = ok ? (uint32_t)(h * nb + bs + v) : none;
-  vals[i] = encode ? (int32_t)(q * k + j) : (int32_t)q;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const uint32_t hq = i / (uint32_t)k;  // h * nq + q
+    const int j = (int)(i - hq * (uint32_t)k);
+    const int h = (int)(hq / (uint32_t)nq);
+    const int64_t q = (int64_t)(hq - (uint32_t)h * (uint32_t)nq);
+    const bool on = !only || only[hq];
+    int b, bs, nbb;
+    bool start;
+    query_batch(cu_q, batch, cu_sb, q, &b, &bs, &nbb, &start);
+    const int v = topk[i];
+    const bool ok = on && v >= 0 && v < nbb && (int64_t)bs + v < nb;
+    keys[i] = ok ? (uint32_t)(h * nb + bs + v) : none;
+    vals[i] = encode ? (int32_t)(q * k + j) : (int32_t)q;
+  }
 }
 
 // seg[s] = first sorted position whose key is >= s, for s = 0 .. hkv * nb.
 __global__ __launch_bounds__(256) void rev_bounds_kernel(const uint32_t* __restrict__ keys,
                                                          int64_t n, int64_t n_seg,
                                                          int32_t* __restrict__ seg) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i > n) return;
-  const int64_t kp = i > 0 ? (int64_t)keys[i - 1] : -1;
-  const int64_t kc = i < n ? (int64_t)keys[i] : n_seg;
-  for (int64_t s = kp + 1; s <= kc && s <= n_seg; ++s) seg[s] = (int32_t)i;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i <= n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t kp = i > 0 ? (int64_t)keys[i - 1] : -1;
+    const int64_t kc = i < n ? (int64_t)keys[i] : n_seg;
+    for (int64_t s = kp + 1; s <= kc && s <= n_seg; ++s) seg[s] = (int32_t)i;
+  }
 }
 
 // Per-head CSR offsets and totals from the segment starts.
@@ -660,10 +664,12 @@ __global__ __launch_bounds__(256) void rev_place_kernel(const uint32_t* __restri
                                                         const int32_t* __restrict__ seg,
                                                         int64_t nb, int64_t n_seg, int64_t cap,
                                                         int32_t* __restrict__ rev) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)seg[n_seg]) return;
-  const int64_t h = keys[i] / (uint32_t)nb;  // keys and nb below 2^31: 32-bit divide
-  rev[h * cap + (i - seg[h * nb])] = vals[i];
+  const int64_t n = seg[n_seg];
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t h = keys[i] / (uint32_t)nb;  // keys and nb below 2^31: 32-bit divide
+    rev[h * cap + (i - seg[h * nb])] = vals[i];
+  }
 }
 
 size_t rev_sort_temp_bytes(int64_t n, unsigned bits) {
@@ -700,7 +706,8 @@ int build_query_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq, int64_
     if (rc) return rc;
     return launch_zero_i32(map.totals, hkv, st);
   }
-  hipLaunchKernelGGL(rev_pairs_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, st, topk,
+  const int64_t grid = std::min<int64_t>(ceil_div(n + 1, 256), 16384);
+  hipLaunchKernelGGL(rev_pairs_kernel, dim3(grid), dim3(256), 0, st, topk,
                      hkv, nq, (int)topk_n, cu_q, batch, cu_sb, nb, only, encode_slot, keys,
                      vals);
   LSRM_CHECK_LAUNCH();
@@ -708,13 +715,13 @@ int build_query_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq, int64_
   if (rocprim::radix_sort_pairs(temp, tbv, keys, keys_out, vals, vals_out, (unsigned)n, 0,
                                 bits, st) != hipSuccess)
     return LSRM_ERR_LAUNCH;
-  hipLaunchKernelGGL(rev_bounds_kernel, dim3(ceil_div(n + 1, 256)), dim3(256), 0, st, keys_out,
+  hipLaunchKernelGGL(rev_bounds_kernel, dim3(grid), dim3(256), 0, st, keys_out,
                      n, n_seg, seg);
   LSRM_CHECK_LAUNCH();
   hipLaunchKernelGGL(rev_offsets_kernel, dim3(ceil_div(hkv * (nb + 1), 256)), dim3(256), 0, st,
                      seg, hkv, nb, map.cu_rev, map.totals);
   LSRM_CHECK_LAUNCH();
-  hipLaunchKernelGGL(rev_place_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, st, keys_out,
+  hipLaunchKernelGGL(rev_place_kernel, dim3(grid), dim3(256), 0, st, keys_out,
                      vals_out, seg, nb, n_seg, map.cap, map.rev);
   LSRM_CHECK_LAUNCH();
   return LSRM_OK;
