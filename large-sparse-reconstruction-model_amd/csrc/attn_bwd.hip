@@ -509,7 +509,6 @@ sel_attn_dkdv_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
   static_assert(KEY_CHUNK == 4 * 32, "four waves of 32 keys cover a chunk");
-  const int kh = wv;  // this wave's 32 keys of the chunk; it covers all rows
   // A plan built without its backward part: no reverse maps or key chunks.
   if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC) return;
   const int n_items = a.items.n_items[0];
@@ -563,6 +562,14 @@ sel_attn_dkdv_kernel(AttnArgs a) {
     const int QC = ROWS / a.g;
     const int n_steps = QM ? n_ent + (n_qent + QC - 1) / QC : n_ent;
 
+    // This wave's 32 keys of the chunk (kh) and the row halves of every step
+    // it computes.  Chunks of at most 64 keys at head dim <= 64 split the
+    // rows too: wave w takes keys (w & 1) * 32 .. +32 and row half w >> 1,
+    // so that four waves work instead of one or two; the halves' dK / dV are
+    // added in LDS at the end (half 0 + half 1).
+    const bool rsplit = D <= 64 && nk_item <= 64;
+    const int kh = rsplit ? (wv & 1) : wv;
+    const int rh_lo = rsplit ? (wv >> 1) : 0, rh_hi = rsplit ? rh_lo + 1 : 2;
     // This wave's 32 keys as B operands (K^T, V^T columns).
     const int key = kh * 32 + l32;
     const bool key_ok = key < nk_item;
@@ -787,7 +794,7 @@ sel_attn_dkdv_kernel(AttnArgs a) {
         }
       } else if (computes) {
 #pragma unroll 1
-        for (int rh = 0; rh < 2 && rh * 64 < rows_cur; ++rh) {  // row halves
+        for (int rh = rh_lo; rh < rh_hi && rh * 64 < rows_cur; ++rh) {  // row halves
         const char* qs = sQ[slot];
         const char* os = sO[slot];
         // The step's 8 * NS MFMAs in a fixed issue order, in four phases:
@@ -913,9 +920,35 @@ sel_attn_dkdv_kernel(AttnArgs a) {
       __syncthreads();
       rows_cur = rows_next;
     }
+    if (rsplit) {
+      // Row half 1 hands its sums to half 0 through LDS.  The Q ring is
+      // free: every copy has landed and every wave has passed the last
+      // step's barrier; the next item's copies follow the barrier below.
+      float* red = reinterpret_cast<float*>(sQ[0]) + kh * (2 * ND * 16 * 64);
+      static_assert(2 * 2 * ND * 16 * 64 * 4 <= 2 * G::BYTES, "reduction fits the Q ring");
+      if (rh_lo == 1) {
+#pragma unroll
+        for (int db = 0; db < ND; ++db)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            red[((0 * ND + db) * 16 + v) * 64 + lane] = dkacc[db][v];
+            red[((1 * ND + db) * 16 + v) * 64 + lane] = dvacc[db][v];
+          }
+      }
+      __syncthreads();
+      if (rh_lo == 0) {
+#pragma unroll
+        for (int db = 0; db < ND; ++db)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            dkacc[db][v] += red[((0 * ND + db) * 16 + v) * 64 + lane];
+            dvacc[db][v] += red[((1 * ND + db) * 16 + v) * 64 + lane];
+          }
+      }
+    }
     // Each wave owns its keys: dK (scaled by the softmax scale, dS was kept
     // unscaled) and dV straight from the accumulators.
-    if (key_ok) {
+    if (key_ok && rh_lo == 0) {
       const int64_t base = ((int64_t)(t0 + key) * a.hkv + h) * D;
 #pragma unroll
       for (int db = 0; db < ND; ++db)
