@@ -135,11 +135,10 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
     lens = (cu_v[1:] - cu_v[:-1]).long()
     flops3 = 4.0 * w.d * w.hq * float(lens[rows[0].long().clamp(min=0)].masked_fill(
         rows[0] < 0, 0).sum())
-    # The key-centric plan: grouped tiles whose masked union pass would cost
-    # more than per-block gathered tiles go to the gathered pass (most of
-    # them on these rows); forward, backward and the plan (built once per
-    # selection, shared by both) timed apart.  The grouped-tile plan alone
-    # is timed beside it.
+    # The key-centric plan: the grouped tiles' queries run as per-block
+    # gathered tiles with their partials merged; forward, backward and the
+    # plan (built once per selection, shared by both) timed apart.  The
+    # grouped-tile plan alone is timed beside it.
     do3 = torch.randn(qv.shape, generator=torch.Generator(device=dev).manual_seed(7),
                       device=dev).to(qv.dtype)
     out3 = torch.empty_like(qv)

@@ -262,12 +262,13 @@ int lsrm_sel_attn_fwd_run(const void* q, const void* k, const void* v,
 
 /* ------------------------------------------------------------------------
  * Plans with flags.  LSRM_PLAN_BACKWARD is the backward != 0 of the calls
- * above.  LSRM_PLAN_KEY_CENTRIC adds the key-centric forward for per-token
- * rows without locality (for example learned selections): query tiles of
- * consecutive queries whose rows differ and whose union of blocks cannot
- * be run in one masked pass are taken out of the grouped-tile pass; for
- * every block, the queries that listed it are gathered into tiles of up to
- * 128 rows that attend that block alone, each writing a partial result
+ * above.  LSRM_PLAN_KEY_CENTRIC adds the key-centric forward and dQ for
+ * per-token rows (learned selections, 3D-aware maps): the query tiles of
+ * consecutive queries whose rows differ (the grouped tiles) are taken out of
+ * the grouped-tile pass; for every block, the queries of those tiles that
+ * listed it are gathered into tiles of up to 128 rows (blocks of up to 256
+ * keys, 512 at head_dim <= 64, held whole in LDS) that attend that block
+ * alone, each writing a partial result
  * (O over the block normalised by its own sum, in the input type, and the
  * log2 LSE); a merge combines each query's partials in the order of its
  * top-k row (M = max LSE_j, W = sum 2^(LSE_j - M), O = sum 2^(LSE_j - M)
@@ -276,8 +277,8 @@ int lsrm_sel_attn_fwd_run(const void* q, const void* k, const void* v,
  * workspace then also holds the partials: hq * n_q * topk * (head_dim * 2
  * + 4) bytes at most, which is why the part is opt-in.  The key-centric
  * part is carved after the others, so lsrm_sel_attn_fwd_run and
- * lsrm_sel_attn_bwd_run accept such a workspace (the former then runs the
- * flagged tiles in the grouped-tile pass); lsrm_sel_attn_fwd_run2 with the
+ * lsrm_sel_attn_bwd_run accept such a workspace (they then run the grouped
+ * tiles in the grouped-tile passes); lsrm_sel_attn_fwd_run2 with the
  * plan's flags runs the key-centric pass.  head_dim sizes the partials and
  * sets which blocks the forward keeps whole in LDS (up to 512 keys at
  * head_dim <= 64, 256 above), so the runs pass the plan's head_dim like its

@@ -454,8 +454,6 @@ __device__ inline int head_of(const int32_t* head_off, int hkv, int w) {
 
 // Persistent-grid size for a kernel: CUs x resident workgroups per CU.
 int persistent_grid(const void* kernel, int block, size_t dyn_lds);
-// Key-centric plans: flags the grouped tiles left to the gathered pass.
-int launch_kc_flags(const AttnArgs& a, uint8_t* gflag, hipStream_t st);
 
 // ------------------------------------------------ LDS tile streaming --
 // Shared by the forward and backward kernels: 16-byte global -> LDS copies,

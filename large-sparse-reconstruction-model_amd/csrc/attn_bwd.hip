@@ -37,7 +37,8 @@ namespace lsrm {
 // key masks, or once per run of identical rows with the other rows' P forced
 // to zero (the passes of the forward's grouped tiles; no softmax state is
 // carried, so either way each row's dQ is a plain sum over the keys it
-// attends); in a key-centric plan the flagged tiles are left to mode 2.
+// attends); a key-centric plan does not launch it (its grouped tiles' rows
+// run as gathered tiles).
 // MODE 2 (DQ_GATHER): the gathered tiles of a key-centric plan over blocks
 // the resident kernels do not take (no keys, or more than kc_res_max), each
 // row writing the block's share of its dQ (one slot of its row, in the
@@ -90,12 +91,6 @@ sel_attn_dq_kernel(AttnArgs a) {
       q0 = 0;
       qn = it.z;
     } else {
-      if constexpr (UNION) {
-        if (a.kc.gflag && a.kc.gflag[(int64_t)h * a.nq + (w - head_off[h])]) {
-          __syncthreads();  // every wave has read s_slot before it is reused
-          continue;
-        }
-      }
       const int2 tile = tiles[(int64_t)h * a.nq + (w - head_off[h])];
       q0 = tile.x;
       qn = tile.y;
@@ -1284,7 +1279,7 @@ int launch_bwd_t(const AttnArgs& a, hipStream_t st) {
                        st, a);
     LSRM_CHECK_LAUNCH();
   }
-  if (a.plan.gtiles) {  // the grouped tiles (often none)
+  if (a.plan.gtiles && !a.kc.fitems) {  // the grouped tiles (key-centric plans: gathered)
     const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D, DQ_UNION>);
     const int grid = persistent_grid(fn, 256, 0);
     if (grid <= 0) return LSRM_ERR_LAUNCH;

@@ -67,8 +67,9 @@ __device__ inline float row_max(const f32x16* sc) {
 
 // MODE 0 (FWD_RUN): the run tiles of the plan (every row of a tile shares
 // one key stream).  MODE 1 (FWD_UNION): the grouped tiles (see build_union),
-// run with per-row key masks; in a key-centric plan the flagged ones are
-// left to mode 2.  MODE 2 (FWD_GATHER): gathered tiles of a key-centric plan
+// run with per-row key masks; a key-centric plan does not launch it (its
+// grouped tiles' rows run as gathered tiles).  MODE 2 (FWD_GATHER): gathered
+// tiles of a key-centric plan
 // -- the queries that listed one block, attending that block alone, each row
 // written as a partial result (O over the block normalised by its own sum,
 // in the input type, and its log2 LSE) for kc_merge_kernel.  Separate
@@ -127,13 +128,6 @@ sel_attn_fwd_kernel(AttnArgs a) {
       q0 = 0;
       qn = it.z;
     } else {
-      // Key-centric plans: flagged grouped tiles belong to the gathered pass.
-      if constexpr (UNION) {
-        if (a.kc.gflag && a.kc.gflag[(int64_t)h * a.nq + (w - head_off[h])]) {
-          __syncthreads();  // every wave has read s_slot before it is reused
-          continue;
-        }
-      }
       const int2 tile = tiles[(int64_t)h * a.nq + (w - head_off[h])];
       q0 = tile.x;
       qn = tile.y;
@@ -620,62 +614,6 @@ sel_attn_fwd_kernel(AttnArgs a) {
   leave_queue(queue, queue + 2);
 }
 
-// Plan step of key-centric plans: gflag[h, t] = 1 for the grouped tiles
-// that go to the gathered pass: those whose union cannot run in one masked
-// pass (build_union's ok is false: more than MAXSEL union blocks, a row
-// listing a block twice, or a union longer than the runs' own streams
-// together), and those whose masked pass computes more key-rows than their
-// rows' own keys (every key of the union for every row of its busy waves,
-// against each row's own keys in the gathered tiles).  Measured on 3D-aware
-// rows, the gathered tiles with their partial results and merge run at
-// about the masked pass's rate per computed key-row, so any such waste
-// favours them.  One workgroup per tile.
-__global__ __launch_bounds__(256) void kc_flag_kernel(AttnArgs a, uint8_t* gflag) {
-  __shared__ SelLds sel;
-  __shared__ UnionLds ul;
-  __shared__ unsigned long long own;
-  const int total = a.plan.ghead_off[a.hkv];
-  for (int w = blockIdx.x; w < total; w += gridDim.x) {
-    const int h = head_of(a.plan.ghead_off, a.hkv, w);
-    const int t = w - a.plan.ghead_off[h];
-    const int2 tile = a.plan.gtiles[(int64_t)h * a.nq + t];
-    if (threadIdx.x == 0) own = 0ull;
-    build_union(a, h, tile.x, tile.y, sel, ul);
-    if (ul.ok) {
-      // the rows' own keys: every slot naming a block, repeats included
-      int b, bs, nbb;
-      bool st;
-      query_batch(a.cu_q, a.batch, a.cu_sb, tile.x, &b, &bs, &nbb, &st);
-      const int32_t* rows = a.topk + ((int64_t)h * a.nq + tile.x) * a.topk_n;
-      unsigned long long mine = 0ull;
-      for (int e = threadIdx.x; e < tile.y * a.topk_n; e += blockDim.x) {
-        int t0, len;
-        block_span(a, bs, nbb, rows[e], t0, len);
-        mine += (unsigned long long)len;
-      }
-      atomicAdd(&own, mine);
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-      bool flag = !ul.ok;
-      if (!flag) {
-        const int waves = (tile.y * a.g + 31) / 32;
-        const unsigned long long masked =
-            (unsigned long long)sel.cum[sel.n] * (unsigned long long)(waves * 32);
-        flag = masked > own * (unsigned long long)a.g;
-      }
-      gflag[(int64_t)h * a.nq + t] = flag ? 1 : 0;
-    }
-    __syncthreads();  // ul / own read before the next tile rebuilds the LDS
-  }
-}
-
-int launch_kc_flags(const AttnArgs& a, uint8_t* gflag, hipStream_t st) {
-  hipLaunchKernelGGL(kc_flag_kernel, dim3(2048), dim3(256), 0, st, a, gflag);
-  LSRM_CHECK_LAUNCH();
-  return LSRM_OK;
-}
-
 // Key-centric forward of blocks held whole in LDS: the block's K and V (at
 // most NT 64-key tiles) are copied into LDS once per item and stay resident
 // while the item's query chunks (up to KC_RES_CHUNKS x 128 rows of gathered
@@ -1017,7 +955,7 @@ int launch_fwd_t(const AttnArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, FWD_RUN>), dim3(grid), dim3(256), 0, st,
                      a);
   LSRM_CHECK_LAUNCH();
-  if (a.plan.gtiles) {  // forward plans: the grouped tiles (often none)
+  if (a.plan.gtiles && !a.kc.fitems) {  // the grouped tiles (key-centric plans: gathered)
     const void* fu = reinterpret_cast<const void*>(&sel_attn_fwd_kernel<DT, D, FWD_UNION>);
     const int gu = persistent_grid(fu, 256, 0);
     if (gu <= 0) return LSRM_ERR_LAUNCH;

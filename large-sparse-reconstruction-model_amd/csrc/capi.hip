@@ -105,27 +105,11 @@ int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
   if (flags & LSRM_PLAN_KEY_CENTRIC) {
     KcPlan& kc = w.kc;
     const size_t qwords = (size_t)((hkv * nq + 3) / 4 > 0 ? (hkv * nq + 3) / 4 : 1);
-    kc.gflag = reinterpret_cast<uint8_t*>(ws.take<int32_t>(qwords));
     kc.qmark = reinterpret_cast<uint8_t*>(ws.take<int32_t>(qwords));
     if (ws.base && !ws.dry) {
       if (!ws.ok()) return LSRM_ERR_WORKSPACE;
-      AttnArgs fa{};
-      fa.topk = topk;
-      fa.cu_sb = cu_sb;
-      fa.cu_blk = cu_blk;
-      fa.cu_q = cu_q;
-      fa.nb = nb;
-      fa.batch = batch;
-      fa.nq = nq;
-      fa.nk = nk;
-      fa.topk_n = (int)topk_n;
-      fa.hkv = (int)hkv;
-      fa.hq = (int)hkv * g;
-      fa.g = g;
-      fa.plan = w.plan;
-      rc = launch_kc_flags(fa, kc.gflag, st);
-      if (rc) return rc;
-      rc = mark_flagged_queries(w.plan, kc.gflag, hkv, nq, kc.qmark, st);
+      // every grouped tile goes to the gathered pass: its queries are marked
+      rc = mark_grouped_queries(w.plan, hkv, nq, kc.qmark, st);
       if (rc) return rc;
     }
     kc.grev = RevMap{};

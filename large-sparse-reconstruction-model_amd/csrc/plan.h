@@ -64,8 +64,8 @@ int mark_grouped_queries(const TilePlan& plan, int64_t hkv, int64_t nq,
                          uint8_t* flags, hipStream_t st);
 
 // Key-centric part of a plan (plan flag LSRM_PLAN_KEY_CENTRIC): the grouped
-// tiles flagged by kc_flag_kernel (flag 1) are taken out of the grouped-tile
-// kernels; their queries are listed per block (`grev`, ascending, one
+// tiles are taken out of the grouped-tile kernels (which a key-centric plan
+// does not launch); their queries are listed per block (`grev`, ascending, one
 // listing q * topk + j per slot j that names the block), and each block's
 // list is cut into items {c, e0, n, 0} = block c, listings e0 .. e0 + n of
 // grev's segment of head h.  The forward writes one partial result per
@@ -73,8 +73,7 @@ int mark_grouped_queries(const TilePlan& plan, int64_t hkv, int64_t nq,
 // type and its log2 LSE -- and the dQ pass the slot's share of dQ; merge
 // passes combine each query's partials in slot order.
 struct KcPlan {
-  uint8_t* gflag;        // [hkv, n_q] per grouped tile (index as gtiles)
-  uint8_t* qmark;        // [hkv, n_q] queries of flagged tiles
+  uint8_t* qmark;        // [hkv, n_q] queries of grouped tiles
   RevMap grev;           // block -> marked queries, cap = n_q * topk per head
   uint16_t* part_o;      // [hkv, n_q, topk, g, D] input type
   float* part_lse;       // [hkv, n_q, topk, g]
@@ -112,8 +111,6 @@ __host__ __device__ constexpr int kc_res_max(int d) { return d <= 64 ? KC_RES2_K
 int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
                    int64_t nb, int tq, int64_t head_dim, Carver& ws, KcPlan& kc,
                    int32_t* counter, hipStream_t st);
-int mark_flagged_queries(const TilePlan& plan, const uint8_t* gflag, int64_t hkv,
-                         int64_t nq, uint8_t* qmark, hipStream_t st);
 
 // Key chunks of at most KEY_CHUNK tokens inside each block (head
 // independent): item i = (block, first token, length) packed in an int4

@@ -808,30 +808,6 @@ int mark_grouped_queries(const TilePlan& plan, int64_t hkv, int64_t nq,
 
 // -------------------------------------------------- key-centric part --
 
-__global__ __launch_bounds__(256) void mark_flagged_kernel(const int2* __restrict__ gtiles,
-                                                           const int32_t* __restrict__ gcount,
-                                                           const uint8_t* __restrict__ gflag,
-                                                           int64_t nq,
-                                                           uint8_t* __restrict__ qmark) {
-  const int h = blockIdx.y;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= gcount[h] || !gflag[(int64_t)h * nq + t]) return;
-  const int2 g = gtiles[(int64_t)h * nq + t];
-  for (int i = 0; i < g.y; ++i) qmark[(int64_t)h * nq + g.x + i] = 1;
-}
-
-int mark_flagged_queries(const TilePlan& plan, const uint8_t* gflag, int64_t hkv,
-                         int64_t nq, uint8_t* qmark, hipStream_t st) {
-  if (nq <= 0) return LSRM_OK;
-  int rc = launch_zero_i32(reinterpret_cast<int32_t*>(qmark), (hkv * nq + 3) / 4, st);
-  if (rc) return rc;
-  if (!plan.gtiles) return LSRM_OK;
-  hipLaunchKernelGGL(mark_flagged_kernel, dim3(ceil_div(nq / 2 + 1, 256), (unsigned)hkv),
-                     dim3(256), 0, st, plan.gtiles, plan.gtile_count, gflag, nq, qmark);
-  LSRM_CHECK_LAUNCH();
-  return LSRM_OK;
-}
-
 // Token count of block c, clamped as the attention kernels clamp it.
 __device__ inline int64_t kc_block_len(const int32_t* cu_blk, int64_t nk, int64_t c) {
   int64_t s0 = cu_blk[c], s1 = cu_blk[c + 1];

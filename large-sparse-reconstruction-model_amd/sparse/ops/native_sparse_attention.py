@@ -40,8 +40,8 @@ def set_validation(enabled: bool) -> None:
 
 def set_key_centric(enabled: bool) -> None:
     """Plans the forward and dQ with the key-centric pass for per-token rows
-    (learned selections, 3D-aware maps): grouped tiles whose masked union
-    pass would compute more key-rows than their rows' own keys are taken out,
+    (learned selections, 3D-aware maps): the grouped tiles (consecutive
+    queries whose rows differ) are taken out of the grouped-tile passes,
     each block's selecting queries are gathered into full tiles and the
     per-block partial results merged in row order.  Off by default: the
     workspace then holds up to Hq * N * topk * (2 * D + 4) bytes of partial

@@ -1,6 +1,7 @@
 """GPU parity of the key-centric forward (plan flag LSRM_PLAN_KEY_CENTRIC):
-per-token rows without locality (learned selections) run as per-block
-gathered tiles whose partial results are merged in row order.  Checked
+the queries of per-token rows (learned selections, 3D-aware maps) that fall
+in grouped tiles run as per-block gathered tiles whose partial results are
+merged in row order.  Checked
 against the fp32 oracle at the attention tolerance (output and LSE), against
 the grouped-tile path, for run-to-run bitwise repeatability, and together
 with the backward on the same plan."""
@@ -24,8 +25,8 @@ def _random_rows(n=6000, hq=2, hkv=2, topk=12, seed=4, d=64, dtype=torch.bfloat1
                  sizes=(4, 17)):
     """Blocks of 4..16 tokens (about n / 10 of them) with unrelated random rows
     per token, as learned selections on unstructured data: 96 consecutive
-    queries list several hundred distinct blocks, more than one masked union
-    pass takes, so the grouped tiles go to the key-centric pass.  -1 padding,
+    queries list several hundred distinct blocks; the grouped tiles go to the
+    key-centric pass.  -1 padding,
     out-of-range ids and empty rows included."""
     rng = np.random.default_rng(seed)
     sizes = rng.integers(sizes[0], sizes[1], size=n // sizes[0])
@@ -163,9 +164,8 @@ def _aware_rows(heads=2, seed=12):
 
 
 def test_3d_aware_rows_take_the_gathered_pass():
-    # Grouped tiles whose masked union pass would compute far more key-rows
-    # than their rows' own keys go to the gathered pass (the cost rule of
-    # the plan): on 3D-aware rows most do.  Forward and backward of the
+    # The grouped tiles of 3D-aware rows (runs of identical rows average ~1.3
+    # queries) go to the gathered pass.  Forward and backward of the
     # key-centric plan against the oracle.
     args = _aware_rows()
     q, k, v, rows, cu_sb, cu_blk, cu_q = args
@@ -235,7 +235,7 @@ def test_sparse_ops_knob_with_autograd():
 
 @pytest.mark.parametrize("hq,hkv,d", [(2, 2, 64), (32, 2, 32)])
 def test_backward_gathered_dq_duplicates_empty_rows(hq, hkv, d):
-    # dQ of the flagged queries on gathered tiles (slot shares added in row
+    # dQ of the grouped queries on gathered tiles (slot shares added in row
     # order); repeated ids, rows without any block (dQ = 0, Delta still
     # rowsum(O dO)), GQA 16 at head dim 32.
     q, k, v, rows, cu_sb, cu_blk, cu_q = _random_rows(n=2400, hq=hq, hkv=hkv, d=d, topk=6,
