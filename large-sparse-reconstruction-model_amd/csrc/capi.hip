@@ -91,8 +91,18 @@ int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
     }
     w.qrev = RevMap{};
     w.qrev.cap = nq * topk_n;
-    rc = build_reverse_map(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, nb, false,
-                           nullptr, ws, w.qrev, st, grouped);
+    if (flags & LSRM_PLAN_KEY_CENTRIC) {
+      // The key-centric part lists the same queries per block (slot-encoded,
+      // in the same order): the map is carved here and derived from that one
+      // once it is built.
+      Carver carve_only{ws.base, ws.used, ws.cap, true};
+      rc = build_reverse_map(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, nb, false,
+                             nullptr, carve_only, w.qrev, st, grouped);
+      ws.used = carve_only.used;
+    } else {
+      rc = build_reverse_map(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, nb, false,
+                             nullptr, ws, w.qrev, st, grouped);
+    }
     if (rc) return rc;
     rc = build_key_items(cu_blk, nb, nk, ws, w.items, st);
     if (rc) return rc;
@@ -120,6 +130,10 @@ int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
     rc = build_kc_items(kc.grev, cu_blk, nk, hkv, nb, tq, head_dim, ws, kc, w.plan.counter,
                         st);
     if (rc) return rc;
+    if (backward && ws.base && !ws.dry) {
+      rc = derive_query_map(kc.grev, w.qrev, hkv, nb, topk_n, st);
+      if (rc) return rc;
+    }
     const size_t parts = (size_t)(hkv * (kc.grev.cap > 0 ? kc.grev.cap : 1) * g);
     kc.part_o = ws.take<uint16_t>(parts * (size_t)(head_dim > 0 ? head_dim : 1));
     kc.part_lse = ws.take<float>(parts);

@@ -108,6 +108,10 @@ constexpr int KC_RES_CHUNKS = 16;  // query chunks of tq listings per resident i
 // as streaming gathered tiles.
 __host__ __device__ constexpr int kc_res_max(int d) { return d <= 64 ? KC_RES2_KEYS : KC_RES_KEYS; }
 
+// plain = enc with every listing q * topk + slot replaced by q (the same
+// blocks, counts and order: the map of the same queries without slots).
+int derive_query_map(const RevMap& enc, const RevMap& plain, int64_t hkv, int64_t nb,
+                     int64_t topk_n, hipStream_t st);
 int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
                    int64_t nb, int tq, int64_t head_dim, Carver& ws, KcPlan& kc,
                    int32_t* counter, hipStream_t st);

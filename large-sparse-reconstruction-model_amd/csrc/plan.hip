@@ -861,6 +861,34 @@ struct KcItemsW {
   }
 };
 
+__global__ __launch_bounds__(256) void derive_offsets_kernel(RevMap enc, RevMap plain,
+                                                             int64_t hkv, int64_t nb) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < hkv * (nb + 1)) plain.cu_rev[i] = enc.cu_rev[i];
+  if (i < hkv) plain.totals[i] = enc.totals[i];
+}
+__global__ __launch_bounds__(256) void derive_rev_kernel(RevMap enc, RevMap plain, int64_t hkv,
+                                                         int k) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < hkv * enc.cap;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t h = i / enc.cap;
+    if (i - h * enc.cap < enc.totals[h]) plain.rev[i] = enc.rev[i] / k;
+  }
+}
+
+int derive_query_map(const RevMap& enc, const RevMap& plain, int64_t hkv, int64_t nb,
+                     int64_t topk_n, hipStream_t st) {
+  if (enc.cap != plain.cap || hkv <= 0 || topk_n <= 0) return LSRM_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(derive_offsets_kernel, dim3(ceil_div(hkv * (nb + 1) + hkv, 256)), dim3(256),
+                     0, st, enc, plain, hkv, nb);
+  LSRM_CHECK_LAUNCH();
+  const int64_t grid = std::min<int64_t>(ceil_div(hkv * enc.cap, 256), 16384);
+  hipLaunchKernelGGL(derive_rev_kernel, dim3(grid > 0 ? grid : 1), dim3(256), 0, st, enc, plain,
+                     hkv, (int)topk_n);
+  LSRM_CHECK_LAUNCH();
+  return LSRM_OK;
+}
+
 // Per-head offsets of the item lists (resident, eight-wave resident,
 // streaming) and their cleared work counters.
 struct KcCounts {
