@@ -24,6 +24,7 @@
 // dK^T = Q^T dS take Q^T / dO^T by transposed reads.  Chunks hold up to 128
 // keys: each wave owns 32 of them and runs every step's 128 rows as two
 // 64-row halves, so one copy of a step's Q / dO rows feeds 128 keys.
+#include <algorithm>
 #include <type_traits>
 
 #include "attn.h"
@@ -976,13 +977,13 @@ sel_attn_dkdv_kernel(AttnArgs a) {
 // BIG = 0, four waves, blocks of 1..KC_RES_KEYS keys; BIG = 1, eight waves
 // in two groups running their own chunks, blocks of KC_RES_KEYS+1 ..
 // KC_RES2_KEYS keys at head dim <= 64).  The block's K and V are copied
-// into LDS once per item; each chunk of up to 128 gathered rows loads its Q,
-// dO and O rows (one chunk ahead, listings two ahead), forms Delta =
-// rowsum(O dO), and for every key tile computes S^T = K Q^T and dP^T = V
+// into LDS once per item; each chunk of up to 128 gathered rows loads its Q
+// and dO rows (one chunk ahead, listings two ahead) and its rows' Delta
+// (written by kc_delta_kernel), and for every key tile computes S^T = K Q^T and dP^T = V
 // dO^T, dS = P (dP - Delta) with P = 2^(S scale log2 e - LSE), and dQ^T +=
 // K^T dS^T: the arithmetic of the streaming gathered tiles, key tile by key
 // tile in the same order.  Each row writes its share of dQ at [head, query,
-// slot] for kc_dq_merge_kernel, and Delta.
+// slot] for kc_dq_merge_kernel.
 template <int DT, int D, int BIG>
 __global__ __launch_bounds__(BIG ? 512 : 256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 kc_resident_dq_kernel(AttnArgs a) {
@@ -1053,7 +1054,7 @@ kc_resident_dq_kernel(AttnArgs a) {
                      : 0;
     };
     // Q, dO and O of the row of listing lv (zeros for rows outside the chunk)
-    auto load_rows = [&](int cbx, int32_t lv, u32x4* qd, u32x4* dd, u32x4* od) {
+    auto load_rows = [&](int cbx, int32_t lv, u32x4* qd, u32x4* dd) {
       const int64_t qx = lv / a.topk_n;
       const bool ok = cbx < n && chunk_ok(cbx);
       const int hx = h * a.g + (ok ? r % a.g : 0);
@@ -1062,52 +1063,41 @@ kc_resident_dq_kernel(AttnArgs a) {
         const int64_t off = (qx * a.hq + hx) * D + s * 16 + hb * 8;
         qd[s] = ok ? *reinterpret_cast<const u32x4*>(a.q + off) : u32x4{0u, 0u, 0u, 0u};
         dd[s] = ok ? *reinterpret_cast<const u32x4*>(a.dout + off) : u32x4{0u, 0u, 0u, 0u};
-        od[s] = ok ? *reinterpret_cast<const u32x4*>(a.o + off) : u32x4{0u, 0u, 0u, 0u};
       }
     };
     const int cb0 = wg * tq;
     int32_t lv_cur = load_listing(cb0);
-    u32x4 qn_[PF ? NS : 1], dn_[PF ? NS : 1], on_[PF ? NS : 1];
-    if constexpr (PF) load_rows(cb0, lv_cur, qn_, dn_, on_);
+    u32x4 qn_[PF ? NS : 1], dn_[PF ? NS : 1];
+    if constexpr (PF) load_rows(cb0, lv_cur, qn_, dn_);
     int32_t lv_next = load_listing(cb0 + step);
     for (int cb = cb0; cb < n; cb += step) {
       const int rows = (n - cb < tq ? n - cb : tq) * a.g;
       const bool row_ok = r < rows;
-      u32x4 qb[NS], dob[NS], ob[NS];
+      u32x4 qb[NS], dob[NS];
       if constexpr (PF) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
           qb[s] = qn_[s];
           dob[s] = dn_[s];
-          ob[s] = on_[s];
         }
       } else {
-        load_rows(cb, lv_cur, qb, dob, ob);
+        load_rows(cb, lv_cur, qb, dob);
       }
       const int64_t qi = lv_cur / a.topk_n;
       const int64_t slot = lv_cur - qi * a.topk_n;
       const int hh = h * a.g + (row_ok ? r % a.g : 0);
       // next chunk: its rows from the listing loaded one chunk ago; the
       // listing after it
-      if constexpr (PF) load_rows(cb + step, lv_next, qn_, dn_, on_);
+      if constexpr (PF) load_rows(cb + step, lv_next, qn_, dn_);
       lv_cur = lv_next;
       lv_next = load_listing(cb + 2 * step);
       if (wl * 32 >= rows) continue;  // wave-uniform: no row of this chunk
-      float dpart = 0.0f;
-#pragma unroll
-      for (int s = 0; s < NS; ++s)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          dpart += to_f32<DT>((uint16_t)(ob[s][i] & 0xffffu)) *
-                   to_f32<DT>((uint16_t)(dob[s][i] & 0xffffu));
-          dpart += to_f32<DT>((uint16_t)(ob[s][i] >> 16)) *
-                   to_f32<DT>((uint16_t)(dob[s][i] >> 16));
-        }
-      const float delta = dpart + __shfl_xor(dpart, 32);
-      // Exponent bias -lse; -inf (P = 0) for rows outside the chunk and rows
-      // that attend nothing.
+      // Delta of the row's query (kc_delta_kernel); exponent bias -lse, -inf
+      // (P = 0) for rows outside the chunk and rows that attend nothing.
+      float delta = 0.0f;
       float bias = -__builtin_inf();
       if (row_ok) {
+        delta = a.lse[(int64_t)hh * a.nq + qi];
         const float l = a.lse_in[(int64_t)hh * a.nq + qi];
         if (l > -__builtin_inf()) bias = -l;
       }
@@ -1196,13 +1186,44 @@ kc_resident_dq_kernel(AttnArgs a) {
                 u32x2{pack2<DT>(a.scale * dqacc[db][v], a.scale * dqacc[db][v + 1]),
                       pack2<DT>(a.scale * dqacc[db][v + 2], a.scale * dqacc[db][v + 3])};
           }
-        if (hb == 0) a.lse[(int64_t)hh * a.nq + qi] = delta;
       }
     }
     __syncthreads();  // the item's reads of sK / sV end before the next copies
   }
   wait_copies();
   leave_queue(queue, queue + 2);
+}
+
+// Delta = rowsum(O dO) of the rows of the marked queries (key-centric
+// plans), once per row, for the resident dQ kernels (which then gather only
+// the Q and dO rows of a listing): one thread per (kv head, query, query
+// head), 16-byte loads, fp32 sum in channel order.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void kc_delta_kernel(AttnArgs a) {
+  const int64_t n_items = (int64_t)a.hkv * a.nq * a.g;
+  for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
+       it += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t hq_idx = it / a.g;  // h * nq + q
+    if (!a.kc.qmark[hq_idx]) continue;
+    const int gi = (int)(it - hq_idx * a.g);
+    const int h = (int)(hq_idx / a.nq);
+    const int64_t q = hq_idx - (int64_t)h * a.nq;
+    const int hh = h * a.g + gi;
+    const uint16_t* orow = a.o + (q * a.hq + hh) * D;
+    const uint16_t* drow = a.dout + (q * a.hq + hh) * D;
+    float dl = 0.0f;
+#pragma unroll
+    for (int c = 0; c < D; c += 8) {
+      const u32x4 ov = *reinterpret_cast<const u32x4*>(orow + c);
+      const u32x4 dv = *reinterpret_cast<const u32x4*>(drow + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        dl += to_f32<DT>((uint16_t)(ov[e] & 0xffffu)) * to_f32<DT>((uint16_t)(dv[e] & 0xffffu));
+        dl += to_f32<DT>((uint16_t)(ov[e] >> 16)) * to_f32<DT>((uint16_t)(dv[e] >> 16));
+      }
+    }
+    a.lse[(int64_t)hh * a.nq + q] = dl;
+  }
 }
 
 // Key-centric dQ merge: one thread per (kv head, query, query head, 8
@@ -1287,7 +1308,14 @@ int launch_bwd_t(const AttnArgs& a, hipStream_t st) {
                        st, a);
     LSRM_CHECK_LAUNCH();
   }
-  if (a.kc.fitems) {  // key-centric plans: gathered dQ tiles, then the merge
+  if (a.kc.fitems) {  // key-centric plans: Delta, gathered dQ tiles, then the merge
+    {
+      const int64_t items = (int64_t)a.hkv * a.nq * a.g;
+      const int64_t gd = std::min<int64_t>((items + 255) / 256 > 0 ? (items + 255) / 256 : 1,
+                                           (int64_t)device_cu_count() * 64);
+      hipLaunchKernelGGL((kc_delta_kernel<DT, D>), dim3((unsigned)gd), dim3(256), 0, st, a);
+      LSRM_CHECK_LAUNCH();
+    }
     const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D, DQ_GATHER>);
     const int grid = persistent_grid(fn, 256, 0);
     if (grid <= 0) return LSRM_ERR_LAUNCH;
