@@ -146,20 +146,28 @@ sel_attn_dq_kernel(AttnArgs a) {
         const int64_t off = (qi * a.hq + hh) * D + s * 16 + hb * 8;
         qb[s] = *reinterpret_cast<const u32x4*>(a.q + off);
         dob[s] = *reinterpret_cast<const u32x4*>(a.dout + off);
-        const u32x4 ob = *reinterpret_cast<const u32x4*>(a.o + off);
+        if constexpr (!GATHER) {
+          const u32x4 ob = *reinterpret_cast<const u32x4*>(a.o + off);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          dpart += to_f32<DT>((uint16_t)(ob[i] & 0xffffu)) *
-                   to_f32<DT>((uint16_t)(dob[s][i] & 0xffffu));
-          dpart += to_f32<DT>((uint16_t)(ob[i] >> 16)) *
-                   to_f32<DT>((uint16_t)(dob[s][i] >> 16));
+          for (int i = 0; i < 4; ++i) {
+            dpart += to_f32<DT>((uint16_t)(ob[i] & 0xffffu)) *
+                     to_f32<DT>((uint16_t)(dob[s][i] & 0xffffu));
+            dpart += to_f32<DT>((uint16_t)(ob[i] >> 16)) *
+                     to_f32<DT>((uint16_t)(dob[s][i] >> 16));
+          }
         }
       } else {
         qb[s] = u32x4{0u, 0u, 0u, 0u};
         dob[s] = u32x4{0u, 0u, 0u, 0u};
       }
     }
-    const float delta = dpart + __shfl_xor(dpart, 32);
+    // Delta: fused here for run and grouped tiles; gathered rows read the
+    // value kc_delta_kernel wrote for their query.
+    float delta;
+    if constexpr (GATHER)
+      delta = row_ok ? a.lse[(int64_t)hh * a.nq + qi] : 0.0f;
+    else
+      delta = dpart + __shfl_xor(dpart, 32);
     // Exponent bias -lse.  Rows outside the tile or the pass get -inf (P =
     // 0), and so does a row that attends nothing (lse = -inf; in a grouped
     // tile its masked scores would otherwise give -inf + inf).
@@ -168,7 +176,7 @@ sel_attn_dq_kernel(AttnArgs a) {
       const float l = a.lse_in[(int64_t)hh * a.nq + qi];
       if (l > -__builtin_inf()) bias = -l;
     }
-    if (row_in_pass && hb == 0) a.lse[(int64_t)hh * a.nq + qi] = delta;
+    if (!GATHER && row_in_pass && hb == 0) a.lse[(int64_t)hh * a.nq + qi] = delta;
 
     const char* kbase = reinterpret_cast<const char*>(a.k + (int64_t)h * D);
     const char* vbase = reinterpret_cast<const char*>(a.v + (int64_t)h * D);
