@@ -43,7 +43,14 @@ struct AttnArgs {
                      // selected it (one entry per listing, ascending)
   KeyItems items;    // backward: key chunks of every block
   KcPlan kc;         // key-centric plans only (kc.fitems null otherwise)
+  int32_t kc_marker; // kc_plan_marker of the flags and head dim of this run
 };
+
+// A key-centric kernel runs only on a plan whose key-centric part was built
+// for this run's flags and head dim (see PLAN_KC_SLOT).
+__device__ inline bool kc_plan_ok(const AttnArgs& a) {
+  return a.plan.counter[PLAN_KC_SLOT] == a.kc_marker;
+}
 
 // Compile-time value tag (e.g. a ring-slot phase).
 template <int V>

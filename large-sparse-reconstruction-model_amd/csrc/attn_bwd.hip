@@ -68,6 +68,9 @@ sel_attn_dq_kernel(AttnArgs a) {
   int32_t* queue = a.plan.counter + (GATHER ? KC_QUEUE_SLOT : (UNION ? 4 : 0));
   // A plan built without its backward part: nothing here is valid to read.
   if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC) return;
+  if constexpr (GATHER) {
+    if (!kc_plan_ok(a)) return;  // nor without the key-centric part of this run
+  }
   const int total = head_off[a.hkv];
   // An empty queue: leave it untouched (no fetch, so nothing to reset).
   if (total == 0) return;
@@ -1009,6 +1012,7 @@ kc_resident_dq_kernel(AttnArgs a) {
   const int hb = lane >> 5, l32 = lane & 31;
   // A plan built without its backward part: nothing here is valid to read.
   if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC) return;
+  if (!kc_plan_ok(a)) return;  // nor without the key-centric part of this run
   const int32_t* head_off = BIG ? a.kc.r2item_off : a.kc.ritem_off;
   const int4* items = BIG ? a.kc.r2items : a.kc.ritems;
   const int64_t item_cap = BIG ? a.kc.r2item_cap : a.kc.ritem_cap;
@@ -1208,6 +1212,7 @@ kc_resident_dq_kernel(AttnArgs a) {
 // head), 16-byte loads, fp32 sum in channel order.
 template <int DT, int D>
 __global__ __launch_bounds__(256) void kc_delta_kernel(AttnArgs a) {
+  if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC || !kc_plan_ok(a)) return;
   const int64_t n_items = (int64_t)a.hkv * a.nq * a.g;
   for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
        it += (int64_t)gridDim.x * blockDim.x) {
@@ -1239,10 +1244,12 @@ __global__ __launch_bounds__(256) void kc_delta_kernel(AttnArgs a) {
 // gathered tiles are added in slot order in fp32 and rounded once.  Slots
 // are taken 16 at a time with their ids and shares loaded together (a slot
 // without a block is loaded and ignored: the buffer covers every slot).
+// These rows' Delta was written by kc_delta_kernel.
 template <int DT, int D>
 __global__ __launch_bounds__(256) void kc_dq_merge_kernel(AttnArgs a) {
   constexpr int CPT = 8;  // output channels per thread: one 16-byte load per slot
   constexpr int U = 16;   // slots whose shares are loaded together
+  if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC || !kc_plan_ok(a)) return;
   const int64_t per_q = (int64_t)a.g * (D / CPT);
   const int64_t n_items = (int64_t)a.hkv * a.nq * per_q;
   for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
@@ -1260,7 +1267,6 @@ __global__ __launch_bounds__(256) void kc_dq_merge_kernel(AttnArgs a) {
     float acc[CPT];
 #pragma unroll
     for (int c = 0; c < CPT; ++c) acc[c] = 0.0f;
-    bool any = false;
     for (int j0 = 0; j0 < a.topk_n; j0 += U) {
       int v[U];
       u32x4 pv[U];
@@ -1275,7 +1281,6 @@ __global__ __launch_bounds__(256) void kc_dq_merge_kernel(AttnArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (!(v[u] >= 0 && v[u] < nbb && (int64_t)bs + v[u] < a.nb)) continue;
-        any = true;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           acc[2 * e] += to_f32<DT>((uint16_t)(pv[u][e] & 0xffffu));
@@ -1287,14 +1292,6 @@ __global__ __launch_bounds__(256) void kc_dq_merge_kernel(AttnArgs a) {
     *reinterpret_cast<u32x4*>(a.out + (q * a.hq + hh) * D + d0) =
         u32x4{pack2<DT>(acc[0], acc[1]), pack2<DT>(acc[2], acc[3]), pack2<DT>(acc[4], acc[5]),
               pack2<DT>(acc[6], acc[7])};
-    if (!any && d0 == 0) {
-      // No slot names a block: no gathered row wrote this row's Delta.
-      const uint16_t* orow = a.o + (q * a.hq + hh) * D;
-      const uint16_t* drow = a.dout + (q * a.hq + hh) * D;
-      float dl = 0.0f;
-      for (int d = 0; d < D; ++d) dl += to_f32<DT>(orow[d]) * to_f32<DT>(drow[d]);
-      a.lse[(int64_t)hh * a.nq + q] = dl;
-    }
   }
 }
 

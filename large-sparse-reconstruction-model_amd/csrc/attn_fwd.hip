@@ -97,6 +97,9 @@ sel_attn_fwd_kernel(AttnArgs a) {
       GATHER ? a.kc.fitem_off : (UNION ? a.plan.ghead_off : a.plan.head_off);
   const int2* tiles = UNION ? a.plan.gtiles : a.plan.tiles;
   int32_t* queue = a.plan.counter + (GATHER ? KC_QUEUE_SLOT : (UNION ? 4 : 0));
+  if constexpr (GATHER) {
+    if (!kc_plan_ok(a)) return;  // no key-centric part for this run: read nothing
+  }
   const int total = head_off[a.hkv];
   // An empty queue: leave it untouched (no fetch, so nothing to reset).
   if (total == 0) return;
@@ -641,6 +644,7 @@ kc_resident_fwd_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int wg = wv >> 2, wl = wv & 3;  // wave group, wave inside the group
   const int hb = lane >> 5, l32 = lane & 31;
+  if (!kc_plan_ok(a)) return;  // no key-centric part for this run: read nothing
   const int32_t* head_off = BIG ? a.kc.r2item_off : a.kc.ritem_off;
   const int4* items = BIG ? a.kc.r2items : a.kc.ritems;
   const int64_t item_cap = BIG ? a.kc.r2item_cap : a.kc.ritem_cap;
@@ -876,6 +880,7 @@ template <int DT, int D>
 __global__ __launch_bounds__(256) void kc_merge_kernel(AttnArgs a) {
   constexpr int CPT = 8;  // output channels per thread: one 16-byte load per slot
   constexpr int U = 16;   // slots loaded together
+  if (!kc_plan_ok(a)) return;  // no key-centric part for this run: read nothing
   const int64_t per_q = (int64_t)a.g * (D / CPT);
   const int64_t n_items = (int64_t)a.hkv * a.nq * per_q;
   for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;

@@ -128,7 +128,7 @@ int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
                            ws, kc.grev, st, kc.qmark, true);
     if (rc) return rc;
     rc = build_kc_items(kc.grev, cu_blk, nk, hkv, nb, tq, head_dim, ws, kc, w.plan.counter,
-                        st);
+                        kc_plan_marker(flags, (int)head_dim), st);
     if (rc) return rc;
     if (backward && ws.base && !ws.dry) {
       rc = derive_query_map(kc.grev, w.qrev, hkv, nb, topk_n, st);
@@ -274,6 +274,7 @@ int attn_setup(const void* q, const void* k, const void* v, int dtype,
   a.qrev = w.qrev;
   a.items = w.items;
   a.kc = w.kc;
+  a.kc_marker = kc_plan_marker(flags, (int)head_dim);
   return LSRM_OK;
 }
 

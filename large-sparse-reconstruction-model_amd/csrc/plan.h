@@ -107,6 +107,16 @@ constexpr int KC_RES_CHUNKS = 16;  // query chunks of tq listings per resident i
 // Largest block the resident forward takes at head dim d; larger blocks run
 // as streaming gathered tiles.
 __host__ __device__ constexpr int kc_res_max(int d) { return d <= 64 ? KC_RES2_KEYS : KC_RES_KEYS; }
+// Marks a plan whose key-centric part was built, with the plan flags and the
+// head dim's resident-block limit it was built for: the key-centric kernels
+// exit without touching memory unless the slot holds the marker of the flags
+// and head dim they run with (a plan built without the part, with other
+// flags -- a different workspace carving -- or for a head dim whose blocks
+// of 257..512 keys take another kernel).
+constexpr int PLAN_KC_SLOT = 33;
+__host__ __device__ constexpr int32_t kc_plan_marker(int flags, int head_dim) {
+  return (int32_t)(0x4b430000 | ((flags & 3) << 12) | kc_res_max(head_dim));
+}
 
 // plain = enc with every listing q * topk + slot replaced by q (the same
 // blocks, counts and order: the map of the same queries without slots).
@@ -114,7 +124,7 @@ int derive_query_map(const RevMap& enc, const RevMap& plain, int64_t hkv, int64_
                      int64_t topk_n, hipStream_t st);
 int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
                    int64_t nb, int tq, int64_t head_dim, Carver& ws, KcPlan& kc,
-                   int32_t* counter, hipStream_t st);
+                   int32_t* counter, int32_t marker, hipStream_t st);
 
 // Key chunks of at most KEY_CHUNK tokens inside each block (head
 // independent): item i = (block, first token, length) packed in an int4

@@ -346,6 +346,7 @@ __global__ void plan_offsets_kernel(const int32_t* n_groups, int32_t* tile_count
     }
     for (int i = 0; i < PLAN_BWD_SLOT; ++i) counter[i] = 0;
     counter[PLAN_BWD_SLOT] = 0;  // set again by mark_backward_plan
+    counter[PLAN_KC_SLOT] = 0;   // set again by the key-centric part
   }
 }
 
@@ -895,7 +896,7 @@ struct KcCounts {
   const int32_t* count[3];
   int32_t* off[3];
 };
-__global__ void kc_offsets_kernel(KcCounts c, int hkv, int32_t* counter) {
+__global__ void kc_offsets_kernel(KcCounts c, int hkv, int32_t* counter, int32_t marker) {
   if (threadIdx.x < 3 && blockIdx.x == 0) {
     const int32_t* cnt = c.count[threadIdx.x];
     int32_t* off = c.off[threadIdx.x];
@@ -913,12 +914,13 @@ __global__ void kc_offsets_kernel(KcCounts c, int hkv, int32_t* counter) {
     counter[KC_REXIT_SLOT] = 0;
     counter[KC_R2QUEUE_SLOT] = 0;
     counter[KC_R2EXIT_SLOT] = 0;
+    counter[PLAN_KC_SLOT] = marker;
   }
 }
 
 int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
                    int64_t nb, int tq, int64_t head_dim, Carver& ws, KcPlan& kc,
-                   int32_t* counter, hipStream_t st) {
+                   int32_t* counter, int32_t marker, hipStream_t st) {
   const int rq = tq * KC_RES_CHUNKS;
   const int res_max = kc_res_max((int)(head_dim > 0 ? head_dim : 1));
   kc.ritem_cap = grev.cap / (rq > 0 ? rq : 1) + nb + 1;
@@ -957,7 +959,8 @@ int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_
   if (rc) return rc;
   const KcCounts c{{kc.ritem_count, kc.r2item_count, kc.fitem_count},
                    {kc.ritem_off, kc.r2item_off, kc.fitem_off}};
-  hipLaunchKernelGGL(kc_offsets_kernel, dim3(1), dim3(64), 0, st, c, (int)hkv, counter);
+  hipLaunchKernelGGL(kc_offsets_kernel, dim3(1), dim3(64), 0, st, c, (int)hkv, counter,
+                     marker);
   LSRM_CHECK_LAUNCH();
   return LSRM_OK;
 }

@@ -165,6 +165,42 @@ def _dev_check(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
+def _attn_check(q, k, v, topk_idx, do=None, o=None, lse=None) -> torch.device:
+    """Device, dtype, shape and layout checks shared by every attention entry
+    (the C ABI takes raw pointers: a CPU tensor or a mis-shaped buffer must
+    stop here, before any kernel sees its address)."""
+    dev = _dev_check(q, k, v, topk_idx, do, o, lse)
+    if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape:
+        raise ValueError("q [Nq, Hq, D], k and v [Nk, Hkv, D] expected")
+    if q.shape[2] != k.shape[2]:
+        raise ValueError("q and k must share the head dim")
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or \
+            v.dtype != q.dtype:
+        raise TypeError("q, k and v must share dtype float16 or bfloat16")
+    if topk_idx.dim() != 3 or topk_idx.dtype != torch.int32 or \
+            topk_idx.shape[0] != k.shape[1] or topk_idx.shape[1] != q.shape[0]:
+        raise ValueError("topk_idx must be int32 [Hkv, Nq, topk]")
+    for name, t in (("do", do), ("o", o)):
+        if t is not None and (t.shape != q.shape or t.dtype != q.dtype):
+            raise ValueError(f"{name} must match q in shape and dtype")
+    if lse is not None and (tuple(lse.shape) != (q.shape[1], q.shape[0]) or
+                            lse.dtype != torch.float32):
+        raise ValueError("lse must be float32 [Hq, Nq]")
+    for t in (q, k, v, topk_idx, do, o, lse):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("attention tensors must be contiguous")
+    return dev
+
+
+def _no_capture(what: str) -> None:
+    """Backward and key-centric plans sort with rocPRIM, whose radix sort
+    clears its state with hipMemsetAsync: such plans are not built under HIP
+    graph capture (a memset node has given wrong results on graph replays)."""
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(f"{what} cannot be built under HIP graph capture (its sort "
+                           "issues memsets); build the plan before capturing")
+
+
 def _i32(t: torch.Tensor) -> torch.Tensor:
     if t.dtype != torch.int32:
         t = t.to(torch.int32)
@@ -342,7 +378,8 @@ def sel_attn_fwd(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
     key_centric: plan with LSRM_PLAN_KEY_CENTRIC (per-token rows without
     locality run as per-block gathered tiles plus a merge; the workspace
     then holds up to Hq * Nq * topk * (2 * D + 4) bytes of partial results)."""
-    dev = _dev_check(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q)
+    dev = _attn_check(q, k, v, topk_idx)
+    _dev_check(q, cu_seqblocks, cu_block_tokens, cu_seqlens_q)
     nq, hq, d = q.shape
     nk, hkv, _ = k.shape
     topk = topk_idx.shape[-1]
@@ -371,11 +408,13 @@ def sel_attn_bwd(do, q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens,
                  cu_seqlens_q, softmax_scale: float, key_centric: bool = False):
     """Selected-block attention backward -> (dq, dk, dv, delta)
     (key_centric: dQ of per-token rows without locality on gathered tiles)."""
+    dev = _attn_check(q, k, v, topk_idx, do=do, o=o, lse=lse)
+    _dev_check(q, cu_seqblocks, cu_block_tokens, cu_seqlens_q)
     if key_centric and q.shape[0] > 0:
         plan = SelAttnPlan(q.shape, k.shape, topk_idx, cu_seqblocks, cu_block_tokens,
                            cu_seqlens_q, backward=True, key_centric=True)
         return plan.bwd(do, q, k, v, o, lse, softmax_scale)
-    dev = _dev_check(do, q, k, v, o, lse, topk_idx)
+    _no_capture("the backward plan")
     nq, hq, d = q.shape
     nk, hkv, _ = k.shape
     topk = topk_idx.shape[-1]
@@ -419,6 +458,8 @@ class SelAttnPlan:
         self.batch = cu_seqlens_q.numel() - 1
         self.backward = backward
         self.flags = (PLAN_BACKWARD if backward else 0) | (PLAN_KEY_CENTRIC if key_centric else 0)
+        if self.flags:
+            _no_capture("a backward or key-centric plan")
         with torch.cuda.device(dev):
             n = lib().lsrm_sel_attn_workspace_size2(self.nq, self.nk, self.hq, self.hkv,
                                                     self.d, self.topk, self.nb, self.flags)
@@ -431,10 +472,17 @@ class SelAttnPlan:
                 self.batch, self.flags, _ptr(self.ws), self.ws.numel(), _stream(dev)),
                 "lsrm_sel_attn_plan2")
 
+    def _check_shapes(self, q, k, v, do=None, o=None, lse=None):
+        dev = _attn_check(q, k, v, self.topk_idx, do=do, o=o, lse=lse)
+        if dev != self.dev or tuple(q.shape) != (self.nq, self.hq, self.d) or \
+                tuple(k.shape[:2]) != (self.nk, self.hkv):
+            raise ValueError("q / k / v do not match the shapes or device the plan was built for")
+
     def fwd(self, q, k, v, softmax_scale: float, out=None, lse=None):
         out = torch.empty_like(q) if out is None else out
         lse = torch.empty(self.hq, self.nq, dtype=torch.float32, device=self.dev) \
             if lse is None else lse
+        self._check_shapes(q, k, v, o=out, lse=lse)
         with torch.cuda.device(self.dev):
             _check(lib().lsrm_sel_attn_fwd_run2(
                 _ptr(q), _ptr(k), _ptr(v), _DTYPE_CODE[q.dtype], self.nq, self.nk, self.hq,
@@ -447,6 +495,7 @@ class SelAttnPlan:
     def bwd(self, do, q, k, v, o, lse, softmax_scale: float):
         if not self.backward:
             raise RuntimeError("plan was built without backward=True")
+        self._check_shapes(q, k, v, do=do, o=o, lse=lse)
         dq = torch.empty_like(q)
         dk = torch.zeros_like(k)
         dv = torch.zeros_like(v)

@@ -161,6 +161,16 @@ def config(idx: int, n: Optional[int] = None, heads: Optional[int] = None) -> Wo
     raise ValueError(f"unknown config {idx}")
 
 
+def product_shape(n: Optional[int] = None) -> Workload:
+    """Config 3's token layout with LSRM's own decoder head layout:
+    num_q_heads 32, num_kv_heads 2 (main_lrm_vol_sparse.py:561-562), head dim
+    32, top-16 (test_rgb.sh:97)."""
+    w = config(3, n=n)
+    w.name = "cfg3-product"
+    w.hq, w.hkv, w.d = 32, 2, 32
+    return w
+
+
 def tensors(w: Workload, device, dtype: Optional[torch.dtype] = None, with_grad_out: bool = False):
     """Seeded Q, K, V (and dO) for a workload on `device`."""
     dtype = dtype or w.dtype

@@ -87,3 +87,23 @@ def test_reference_api_asserts_dtypes_on_cpu():
     with pytest.raises(AssertionError):
         ops.native_sparse_attend(q, q, q, torch.zeros(2, 8, 1, dtype=torch.int32),
                                  torch.tensor([0, 1], dtype=torch.int32), cu, cu, cu)
+
+
+def test_attention_entries_refuse_host_tensors_before_any_launch():
+    # Every attention entry point checks devices, dtypes and shapes before a
+    # pointer reaches the C ABI; a CPU dO on the key-centric backward path
+    # raises like everywhere else.
+    import lsrm_hip as H
+
+    q = torch.zeros(8, 2, 64, dtype=torch.bfloat16)
+    k = torch.zeros(8, 2, 64, dtype=torch.bfloat16)
+    rows = torch.zeros(2, 8, 1, dtype=torch.int32)
+    lse = torch.zeros(2, 8)
+    cu = torch.tensor([0, 1], dtype=torch.int32)
+    cu_blk = torch.tensor([0, 8], dtype=torch.int32)
+    cu_q = torch.tensor([0, 8], dtype=torch.int32)
+    for kc in (True, False):
+        with pytest.raises(RuntimeError, match="no CPU fallback"):
+            H.sel_attn_bwd(q, q, k, k, q, lse, rows, cu, cu_blk, cu_q, 0.125, key_centric=kc)
+        with pytest.raises(RuntimeError, match="no CPU fallback"):
+            H.sel_attn_fwd(q, k, k, rows, cu, cu_blk, cu_q, 0.125, key_centric=kc)

@@ -308,3 +308,104 @@ def test_backward_all_gathered_dq_kernels(hq, hkv, d, topk):
     torch.testing.assert_close(delta.cpu(), delta_ref, rtol=1e-4, atol=1e-4)
     again = plan.bwd(do.to(DEV), dev[0], dev[1], dev[2], o, lse, 0.125)
     assert all(torch.equal(x, y) for x, y in zip((dq, dk, dv, delta), again))
+
+
+@pytest.mark.parametrize("hq,topk", [(2, 64), (16, 64), (2, 128), (16, 128)])
+def test_long_rows_forward_and_backward(hq, topk):
+    # get_block_score emits rows of up to 128 blocks: the forward merge
+    # rescales its running maximum across up to 8 groups of 16 slots, the dQ
+    # merge adds up to 128 slot shares, each already rounded to the input
+    # type.
+    args = _random_rows(n=3000, hq=hq, hkv=2, d=64, topk=topk,
+                        seed=15 + topk, sizes=(4, 24))
+    q, k, v, rows, cu_sb, cu_blk, cu_q = args
+    dev = [t.to(DEV) for t in args]
+    plan = H.SelAttnPlan(dev[0].shape, dev[1].shape, dev[3], dev[4], dev[5], dev[6],
+                         backward=True, key_centric=True)
+    o, lse = plan.fwd(dev[0], dev[1], dev[2], 0.125)
+    _check_oracle(args, o, lse)
+    g = torch.Generator().manual_seed(115)
+    do = (0.5 * torch.randn(q.shape, generator=g)).to(q.dtype)
+    dq, dk, dv, _ = plan.bwd(do.to(DEV), dev[0], dev[1], dev[2], o, lse, 0.125)
+    dq_r, dk_r, dv_r, _ = sel_attn_bwd_ref(q.float(), k.float(), v.float(), do.float(), rows,
+                                           cu_sb, cu_blk, cu_q, 0.125)
+    assert_attn_close(dq, dq_r, "dq")
+    assert_attn_close(dk, dk_r, "dk")
+    assert_attn_close(dv, dv_r, "dv")
+
+
+def _raw_plan(args, flags, head_dim, ws_flags, ws_head_dim):
+    """A plan built through the C ABI with `flags` / `head_dim` in a
+    workspace sized for `ws_flags` / `ws_head_dim`."""
+    q, k, rows, cu_sb, cu_blk, cu_q = args
+    nq, hq, _ = q.shape
+    nk, hkv, _ = k.shape
+    nb = cu_blk.numel() - 1
+    lib = H.lib()
+    n = max(lib.lsrm_sel_attn_workspace_size2(nq, nk, hq, hkv, ws_head_dim, rows.shape[-1], nb,
+                                              ws_flags),
+            lib.lsrm_sel_attn_workspace_size2(nq, nk, hq, hkv, head_dim, rows.shape[-1], nb,
+                                              flags))
+    ws = torch.empty(n, dtype=torch.uint8, device=DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    rc = lib.lsrm_sel_attn_plan2(rows.data_ptr(), nq, nk, hq, hkv, head_dim, rows.shape[-1],
+                                 cu_sb.data_ptr(), cu_blk.data_ptr(), nb, cu_q.data_ptr(), 1,
+                                 flags, ws.data_ptr(), ws.numel(), st)
+    assert rc == 0
+    return ws
+
+
+def _raw_fwd(q, k, v, rows, cu_sb, cu_blk, cu_q, ws, flags):
+    nq, hq, d = q.shape
+    nk, hkv, _ = k.shape
+    out = torch.full_like(q, float("nan"))
+    lse = torch.full((hq, nq), float("nan"), dtype=torch.float32, device=DEV)
+    rc = H.lib().lsrm_sel_attn_fwd_run2(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), H.BF16, nq, nk, hq, hkv, d, rows.data_ptr(),
+        rows.shape[-1], cu_sb.data_ptr(), cu_blk.data_ptr(), cu_blk.numel() - 1,
+        cu_q.data_ptr(), 1, 0.125, out.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws.numel(),
+        flags, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def test_key_centric_run_needs_a_key_centric_plan():
+    # A forward-only plan run with the key-centric flag: the carving finds
+    # item lists that were never built; the key-centric kernels read the
+    # plan's marker and exit without touching memory, so the grouped
+    # queries' rows stay as they were (NaN here) and nothing faults.  The
+    # run-tile rows are still computed and correct.
+    args = list(_random_rows(n=3000, seed=16))
+    args[3] = args[3].clone()
+    args[3][:, :1024] = args[3][:, :1]  # 1024 identical rows: run tiles
+    q, k, v, rows, cu_sb, cu_blk, cu_q = (t.to(DEV) for t in args)
+    ws = _raw_plan((q, k, rows, cu_sb, cu_blk, cu_q), 0, 64, H.PLAN_KEY_CENTRIC, 64)
+    out, lse = _raw_fwd(q, k, v, rows, cu_sb, cu_blk, cu_q, ws, H.PLAN_KEY_CENTRIC)
+    untouched = torch.isnan(lse)
+    assert untouched.any()
+    o_ref, lse_ref = sel_attn_ref(*(t.float() for t in args[:3]), *args[3:], 0.125)
+    done = ~untouched.cpu()
+    lr = lse_ref[done]
+    fin = torch.isfinite(lr)
+    assert float((lse.cpu()[done][fin] - lr[fin]).abs().max()) <= 2e-2
+    rows_done = done.transpose(0, 1)  # [nq, hq]
+    assert_attn_close(out.cpu()[rows_done], o_ref[rows_done], "run-tile rows")
+
+
+def test_key_centric_plan_for_another_head_dim_is_refused():
+    # A key-centric plan built for head dim 64 (blocks of 257..512 keys in
+    # the eight-wave resident list) run at head dim 128, where that kernel
+    # does not exist: the marker differs, the key-centric kernels exit, and
+    # no partial is merged unwritten.
+    args = _random_rows(n=3000, seed=17, d=128, sizes=(200, 400))
+    q, k, v, rows, cu_sb, cu_blk, cu_q = (t.to(DEV) for t in args)
+    ws = _raw_plan((q, k, rows, cu_sb, cu_blk, cu_q), H.PLAN_KEY_CENTRIC, 64,
+                   H.PLAN_KEY_CENTRIC, 128)
+    _, lse = _raw_fwd(q, k, v, rows, cu_sb, cu_blk, cu_q, ws, H.PLAN_KEY_CENTRIC)
+    assert torch.isnan(lse).any()
+    # the same plan built for head dim 128 gives the oracle's result
+    ws = _raw_plan((q, k, rows, cu_sb, cu_blk, cu_q), H.PLAN_KEY_CENTRIC, 128,
+                   H.PLAN_KEY_CENTRIC, 128)
+    o, lse = _raw_fwd(q, k, v, rows, cu_sb, cu_blk, cu_q, ws, H.PLAN_KEY_CENTRIC)
+    _check_oracle(args, o, lse)
