@@ -130,7 +130,7 @@ sel_attn_dq_kernel(AttnArgs a) {
     const bool row_ok = r < rows;
     const int qr = row_ok ? r / a.g : 0;  // the row's query within the tile
     const bool row_in_pass = row_ok && qr >= q_lo && qr < q_hi;
-    const bool wave_on = wv * 32 < q_hi * a.g && wv * 32 + 32 > q_lo * a.g;
+    const bool wave_on = uniform(wv * 32 < q_hi * a.g && wv * 32 + 32 > q_lo * a.g) != 0;
     // Gathered tiles: row r is listing ge0 + r / g (query * topk + slot).
     int64_t qi, gslot = 0;
     if constexpr (GATHER) {

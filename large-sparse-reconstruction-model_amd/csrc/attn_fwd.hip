@@ -21,11 +21,13 @@
 //     ds_read_b64_tr_b16 and P^T from the score registers, so V is never
 //     transposed in memory;
 //   * the loop is a three-stage software pipeline: step t issues the score
-//     MFMAs of tile t+1 and the P.V MFMAs of tile t-1 next to the softmax
-//     arithmetic of tile t, in a fixed order of slots (one MFMA, then two
-//     scores' worth of softmax) so that matrix and vector work co-issue
-//     inside one wave; K and V live in four-slot LDS rings whose copies are
-//     issued two or three steps before they are read, one barrier per tile;
+//     MFMAs of tile t+1 and the P.V MFMAs of tile t-1 (alternating) next to
+//     the softmax arithmetic of tile t, in a fixed order of slots (one MFMA,
+//     then two scores' worth of softmax) so that matrix and vector work
+//     co-issue inside one wave; K and V live in four-slot LDS rings whose
+//     copies are issued two or three steps before they are read, one
+//     barrier per tile; only the steps that can hold the stream's last
+//     (partial) key tile carry the tail mask;
 //   * the softmax reference is the row maximum of the first key tile and is
 //     not updated afterwards (no per-tile maximum, no rescaling); a tile
 //     whose row sums leave the safe range is recomputed with the exact
@@ -170,7 +172,7 @@ sel_attn_fwd_kernel(AttnArgs a) {
     const bool row_ok = r < rows;
     const int qr = row_ok ? r / a.g : 0;  // the row's query within the tile
     const bool row_in_pass = row_ok && qr >= q_lo && qr < q_hi;
-    const bool wave_on = wv * 32 < q_hi * a.g && wv * 32 + 32 > q_lo * a.g;
+    const bool wave_on = uniform(wv * 32 < q_hi * a.g && wv * 32 + 32 > q_lo * a.g) != 0;
     // Gathered tiles: row r is listing ge0 + r / g of the block's segment,
     // which stores query * topk + slot.
     int64_t qi, gslot = 0;
@@ -360,13 +362,14 @@ sel_attn_fwd_kernel(AttnArgs a) {
       l_run = sum2<DT>(pb[blk][c][e], l_run);
     };
     // The fast step's matrix and vector work in a fixed issue order: slot i
-    // issues one MFMA (the score MFMAs of tile kt+1, alternating between the
-    // two independent 32-key accumulators, then the P.V MFMAs of tile kt-1,
-    // alternating between output blocks) followed by its share of the
-    // softmax of tile kt, so that the vector ALU works while the matrix core
-    // runs.  All K operands are read at the start; the V operands of P.V
-    // MFMA i are read during score slot i.  Scheduling barriers keep the
-    // compiler from regrouping the slots.
+    // issues one MFMA -- score MFMAs of tile kt+1 and P.V MFMAs of tile kt-1
+    // alternate, so consecutive MFMAs on one accumulator are three slots
+    // apart -- followed by its share of the softmax of tile kt, so that the
+    // vector ALU works while the matrix core runs.  Each MFMA's operand (a K
+    // row block, or the two transposed V reads) is read from LDS two slots
+    // ahead: only three operands are live at a time, which keeps the step
+    // within the register budget.  Scheduling barriers keep the compiler
+    // from regrouping the slots.
     auto fast_body = [&](auto first, const char* ks, const char* vs, const f32x16* sc,
                          f32x16* sn, const u32x4 (*pp)[2], u32x4 (*pc)[2],
                          float negm) __attribute__((always_inline)) {
@@ -375,39 +378,50 @@ sel_attn_fwd_kernel(AttnArgs a) {
       constexpr int NPV = FIRST ? 0 : 4 * ND;  // P.V MFMAs
       constexpr int NSLOT = NSM + NPV;
       constexpr int NPAIR = 16;
-      u32x4 ka[2][NS], va[ND][2][2];
-      read_k(ks, ka);
+      constexpr int LA = 2;  // operand reads run LA slots ahead of their MFMA
+      // Slot i's MFMA: score and P.V MFMAs alternate (a score MFMA when the
+      // step has no P.V work).  kind 0: score MFMA idx (32-key block idx & 1,
+      // head-dim step idx >> 1); kind 1: P.V MFMA idx.
+      auto kind_of = [](int i) constexpr { return (NPV == 0 || (i & 1) == 0) ? 0 : 1; };
+      auto idx_of = [](int i) constexpr { return NPV == 0 ? i : (i >> 1); };
       const int gi = lane & 15, dh = (lane >> 4) & 1;
-      auto read_v1 = [&](int i) __attribute__((always_inline)) {  // operands of P.V MFMA i
-        const int db = i % ND, bc = i / ND, blk = bc >> 1, c = bc & 1;
-        const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
-        const int k0 = blk * 32 + c * 16 + hb * 4 + (gi >> 2);
-        const int cb = dcol >> 3, half = (dcol & 4) * 2;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)(vs + G::off(k0, cb) + half));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)(vs + G::off(k0 + 8, cb) + half));
-        const u32x2 lw = __builtin_bit_cast(u32x2, lo);
-        const u32x2 hw = __builtin_bit_cast(u32x2, hi);
-        va[db][blk][c] = u32x4{lw[0], lw[1], hw[0], hw[1]};
+      auto read_op = [&](int i, u32x4& dst) __attribute__((always_inline)) {
+        const int x = idx_of(i);
+        if (kind_of(i) == 0) {
+          const int blk = x & 1, s = x >> 1;
+          dst = *reinterpret_cast<const u32x4*>(ks + G::off(blk * 32 + l32, 2 * s + hb));
+        } else {
+          const int db = x % ND, bc = x / ND, blk = bc >> 1, c = bc & 1;
+          const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+          const int k0 = blk * 32 + c * 16 + hb * 4 + (gi >> 2);
+          const int cb = dcol >> 3, half = (dcol & 4) * 2;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)(vs + G::off(k0, cb) + half));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)(vs + G::off(k0 + 8, cb) + half));
+          const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+          const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+          dst = u32x4{lw[0], lw[1], hw[0], hw[1]};
+        }
       };
+      u32x4 op[LA + 1];
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
+      for (int i = 0; i < LA && i < NSLOT; ++i) read_op(i, op[i % (LA + 1)]);
+#pragma unroll
       for (int i = 0; i < NSLOT; ++i) {
-        if (i < NSM) {
-          const int blk = i & 1, s = i >> 1;
+        if (i + LA < NSLOT) read_op(i + LA, op[(i + LA) % (LA + 1)]);
+        const int x = idx_of(i);
+        if (kind_of(i) == 0) {
+          const int blk = x & 1, s = x >> 1;
           if (s == 0) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) sn[blk][v] = 0.0f;
           }
-          sn[blk] = mfma32<DT>(ka[blk][s], qb[s], sn[blk]);
-          if constexpr (!FIRST) {
-#pragma unroll
-            for (int r = (i * NPV) / NSM; r < ((i + 1) * NPV) / NSM; ++r) read_v1(r);
-          }
+          sn[blk] = mfma32<DT>(op[i % (LA + 1)], qb[s], sn[blk]);
         } else {
-          const int j = i - NSM, db = j % ND, bc = j / ND, blk = bc >> 1, c = bc & 1;
-          oacc[db] = mfma32<DT>(va[db][blk][c], pp[blk][c], oacc[db]);
+          const int db = x % ND, bc = x / ND, blk = bc >> 1, c = bc & 1;
+          oacc[db] = mfma32<DT>(op[i % (LA + 1)], pp[blk][c], oacc[db]);
         }
 #pragma unroll
         for (int j = (i * NPAIR) / NSLOT; j < ((i + 1) * NPAIR) / NSLOT; ++j)
@@ -473,11 +487,13 @@ sel_attn_fwd_kernel(AttnArgs a) {
     // at tile 0's row maximum (p may exceed 1; the caller checks the row sums
     // afterwards); with `safe` true it follows the online maximum with lazy
     // rescaling.
-    auto step = [&](auto ph, auto safe, auto first, int kt, f32x16* sc, f32x16* sn,
+    auto step = [&](auto ph, auto safe, auto first, auto tail, int kt, f32x16* sc, f32x16* sn,
                     const u32x4 (*pp)[2], u32x4 (*pc)[2]) __attribute__((always_inline)) {
       constexpr int PH = decltype(ph)::value;
       constexpr bool SAFE = decltype(safe)::value != 0;
       constexpr bool FIRST = decltype(first)::value != 0;
+      // TAIL: this step may hold the stream's last (partial) key tile
+      constexpr bool TAIL = decltype(tail)::value != 0;
       const int k_rd = PH >= 0 ? (PH + 1) & 3 : (kt + 1) & 3;  // K(kt+1)
       const int k_wr = PH >= 0 ? (PH + 3) & 3 : (kt + 3) & 3;  // K(kt+3), = V(kt-1)
       const int v_wr = PH >= 0 ? (PH + 2) & 3 : (kt + 2) & 3;  // V(kt+2)
@@ -488,13 +504,14 @@ sel_attn_fwd_kernel(AttnArgs a) {
 
       if (wave_on) {
         if constexpr (SAFE) {
-          if (umode == 0)
-            mask_tail(kt, sc);
-          else
+          if (umode == 0) {
+            if constexpr (TAIL) mask_tail(kt, sc);
+          } else {
             mask_keys(kt, sc);
+          }
         } else {
           if (umode == 0) {
-            mask_tail(kt, sc);
+            if constexpr (TAIL) mask_tail(kt, sc);
           } else {
             // Grouped tiles.  A 64-key tile mostly lies inside one block, so
             // a row attends all of it or none of it: a row with no key here
@@ -545,18 +562,21 @@ sel_attn_fwd_kernel(AttnArgs a) {
     // All steps of one pass, then O += P(last) V(last).
     auto run = [&](auto safe) __attribute__((always_inline)) {
       if (ntiles == 0) return;
-      step(Phase<0>{}, safe, Phase<1>{}, 0, sA, sB, pB, pA);
+      step(Phase<0>{}, safe, Phase<1>{}, Phase<1>{}, 0, sA, sB, pB, pA);
       int kt = 1;
-      for (; kt + 4 <= ntiles; kt += 4) {
-        step(Phase<1>{}, safe, Phase<0>{}, kt, sB, sA, pA, pB);
-        step(Phase<2>{}, safe, Phase<0>{}, kt + 1, sA, sB, pB, pA);
-        step(Phase<3>{}, safe, Phase<0>{}, kt + 2, sB, sA, pA, pB);
-        step(Phase<0>{}, safe, Phase<0>{}, kt + 3, sA, sB, pB, pA);
+      // The loop never reaches the last key tile (kt + 3 <= ntiles - 2), so
+      // its steps carry no tail mask.
+      for (; kt + 4 < ntiles; kt += 4) {
+        step(Phase<1>{}, safe, Phase<0>{}, Phase<0>{}, kt, sB, sA, pA, pB);
+        step(Phase<2>{}, safe, Phase<0>{}, Phase<0>{}, kt + 1, sA, sB, pB, pA);
+        step(Phase<3>{}, safe, Phase<0>{}, Phase<0>{}, kt + 2, sB, sA, pA, pB);
+        step(Phase<0>{}, safe, Phase<0>{}, Phase<0>{}, kt + 3, sA, sB, pB, pA);
       }
-      // kt % 4 == 1 here
-      if (kt < ntiles) step(Phase<1>{}, safe, Phase<0>{}, kt, sB, sA, pA, pB);
-      if (kt + 1 < ntiles) step(Phase<2>{}, safe, Phase<0>{}, kt + 1, sA, sB, pB, pA);
-      if (kt + 2 < ntiles) step(Phase<3>{}, safe, Phase<0>{}, kt + 2, sB, sA, pA, pB);
+      // kt % 4 == 1 here; at most four tiles remain
+      if (kt < ntiles) step(Phase<1>{}, safe, Phase<0>{}, Phase<1>{}, kt, sB, sA, pA, pB);
+      if (kt + 1 < ntiles) step(Phase<2>{}, safe, Phase<0>{}, Phase<1>{}, kt + 1, sA, sB, pB, pA);
+      if (kt + 2 < ntiles) step(Phase<3>{}, safe, Phase<0>{}, Phase<1>{}, kt + 2, sB, sA, pA, pB);
+      if (kt + 3 < ntiles) step(Phase<0>{}, safe, Phase<0>{}, Phase<1>{}, kt + 3, sA, sB, pB, pA);
       if (wave_on) {
         const char* vs = sV[(ntiles - 1) & 3];
         if ((ntiles - 1) & 1)
