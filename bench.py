@@ -58,10 +58,13 @@ def event_time_ms(fn, reps: int) -> float:
     return start.elapsed_time(end) / reps
 
 
-def measured_traffic():
-    """HBM bytes per attention-forward launch at config 3, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (already scaled by the
-    plain-copy calibration recorded there), or None when absent."""
+def measured_traffic(config: int):
+    """HBM bytes per attention-forward launch from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (already scaled by the plain-copy
+    calibration recorded there); only config 3 has one, other configs and a
+    missing summary give None."""
+    if config != 3:
+        return None
     path = ROOT / "profiles" / "attn_fwd_cfg3_hbm_traffic.txt"
     if not path.exists():
         return None
@@ -112,14 +115,11 @@ def cpu_baseline(w, q, k, v, topk_idx, flops_per_head_q, budget_s: float):
     }
 
 
-def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
-    """Config-3 paths with per-token selection rows (reported beside the
-    headline, not part of it): the forward over the 3D-aware rows of the
-    voxel tokens (nearest 16 block centroids, built on the GPU), and the
-    learned selection (compressed attention + get_block_score, top-16)."""
-    import sparse.ops as ops
-    from sparse import builders
-
+def aware_rows_case(w, q, k, v, label):
+    """Forward and backward over the 3D-aware rows of config 3's voxel tokens
+    (each token's nearest 16 block centroids, built on the GPU) for the
+    head layout of w / q / k / v: the key-centric plan and the grouped-tile
+    plan, each built once (backward-capable) and timed apart."""
     dev = q.device
     n_img = w.n_image_tokens
     nb_img = w.n_image_blocks
@@ -131,30 +131,62 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
     cu_q_v = torch.tensor([0, nv], dtype=torch.int32, device=dev)
     pts = H.volume_points(coords.to(dev), 64, 1.0)
     rows = H.nearest_blocks(pts, cu_v, cu_sb_v, cu_q_v, 16, w.hkv)
-    qv, kv, vv = (t[n_img:] for t in (q, k, v))
+    qv, kv, vv = (t[n_img:].contiguous() for t in (q, k, v))
     lens = (cu_v[1:] - cu_v[:-1]).long()
-    flops3 = 4.0 * w.d * w.hq * float(lens[rows[0].long().clamp(min=0)].masked_fill(
+    # every kv head carries the same rows; each of its hq / hkv query heads
+    # attends them
+    flops = 4.0 * w.d * w.hq * float(lens[rows[0].long().clamp(min=0)].masked_fill(
         rows[0] < 0, 0).sum())
-    # The key-centric plan: the grouped tiles' queries run as per-block
-    # gathered tiles with their partials merged; forward, backward and the
-    # plan (built once per selection, shared by both) timed apart.  The
-    # grouped-tile plan alone is timed beside it.
-    do3 = torch.randn(qv.shape, generator=torch.Generator(device=dev).manual_seed(7),
-                      device=dev).to(qv.dtype)
-    out3 = torch.empty_like(qv)
-    lse3 = torch.empty(w.hq, nv, dtype=torch.float32, device=dev)
-    times3 = {}
+    do = torch.randn(qv.shape, generator=torch.Generator(device=dev).manual_seed(7),
+                     device=dev).to(qv.dtype)
+    out = torch.empty_like(qv)
+    lse = torch.empty(w.hq, nv, dtype=torch.float32, device=dev)
+    times = {}
     for kc in (True, False):
-        plan3 = H.SelAttnPlan(qv.shape, kv.shape, rows, cu_sb_v, cu_v, cu_q_v, backward=True,
-                              key_centric=kc)
-        ms_f = event_time_ms(lambda: plan3.fwd(qv, kv, vv, w.scale, out3, lse3), 5)
-        ms_b = event_time_ms(lambda: plan3.bwd(do3, qv, kv, vv, out3, lse3, w.scale), 3)
-        del plan3
+        plan = H.SelAttnPlan(qv.shape, kv.shape, rows, cu_sb_v, cu_v, cu_q_v, backward=True,
+                             key_centric=kc)
+        ms_f = event_time_ms(lambda: plan.fwd(qv, kv, vv, w.scale, out, lse), 5)
+        ms_b = event_time_ms(lambda: plan.bwd(do, qv, kv, vv, out, lse, w.scale), 3)
+        del plan
         ms_p = event_time_ms(lambda: H.SelAttnPlan(qv.shape, kv.shape, rows, cu_sb_v, cu_v,
                                                    cu_q_v, backward=True, key_centric=kc), 2)
-        times3[kc] = (ms_f, ms_b, ms_p)
-    ms3, ms3b, ms3p = times3[True]
-    del do3, out3, lse3
+        times[kc] = (ms_f, ms_b, ms_p)
+        torch.cuda.empty_cache()
+    ms_f, ms_b, ms_p = times[True]
+    tf = flops / (ms_f * 1e-3) / 1e12
+    tb = 2.5 * flops / (ms_b * 1e-3) / 1e12
+    return {
+        f"attn_fwd_3d_aware_rows{label}": {
+            "ms": round(ms_f, 4), "tflops": round(tf, 2),
+            "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+            "plan": "key-centric", "plan_ms": round(ms_p, 4),
+            "grouped_tiles_ms": round(times[False][0], 4),
+            "grouped_tiles_plan_ms": round(times[False][2], 4),
+            "workload": f"{nv} voxel tokens, {cu_v.numel() - 1} blocks, per-token nearest 16 "
+                        f"block centroids, Hq={w.hq}, Hkv={w.hkv}, D={w.d}"},
+        f"attn_bwd_3d_aware_rows{label}": {
+            "ms": round(ms_b, 4), "tflops": round(tb, 2),
+            "frac_bf16_peak": round(tb / PEAK_BF16_TFLOPS, 4),
+            "plan": "key-centric", "grouped_tiles_ms": round(times[False][1], 4)},
+    }
+
+
+def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
+    """Config-3 paths with per-token selection rows (reported beside the
+    headline, not part of it): the forward over the 3D-aware rows of the
+    voxel tokens (nearest 16 block centroids, built on the GPU), and the
+    learned selection (compressed attention + get_block_score, top-16)."""
+    import sparse.ops as ops
+
+    dev = q.device
+    res = aware_rows_case(w, q, k, v, "")
+    # LSRM's own decoder heads (main_lrm_vol_sparse.py:561-562): 32 query
+    # heads over 2 kv heads, head dim 32, on the same tokens
+    wp = W.product_shape()
+    qp, kp, vp = W.tensors(wp, dev)
+    res.update(aware_rows_case(wp, qp, kp, vp, "_product_heads"))
+    del qp, kp, vp
+    torch.cuda.empty_cache()
 
     ops.set_validation(False)
     ck = H.block_mean_pool(k.view(w.n, -1), cu_blk).view(-1, w.hkv, w.d)
@@ -194,18 +226,7 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
     gm_bytes = 7 * w.n * hid * q.element_size()
     del gate, brs
     return {
-        "attn_fwd_3d_aware_rows": {
-            "ms": round(ms3, 4), "tflops": round(flops3 / (ms3 * 1e-3) / 1e12, 2),
-            "frac_bf16_peak": round(flops3 / (ms3 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "plan": "key-centric", "plan_ms": round(ms3p, 4),
-            "grouped_tiles_ms": round(times3[False][0], 4),
-            "grouped_tiles_plan_ms": round(times3[False][2], 4),
-            "workload": f"{nv} voxel tokens, {cu_v.numel() - 1} blocks, per-token nearest 16 "
-                        f"block centroids, H={w.hq}"},
-        "attn_bwd_3d_aware_rows": {
-            "ms": round(ms3b, 4), "tflops": round(2.5 * flops3 / (ms3b * 1e-3) / 1e12, 2),
-            "frac_bf16_peak": round(2.5 * flops3 / (ms3b * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "plan": "key-centric", "grouped_tiles_ms": round(times3[False][1], 4)},
+        **res,
         "learned_selection": {"compressed_attn_ms": round(ms_ca, 4),
                               "get_block_score_ms": round(ms_bs, 4), "topk": 16},
         "attn_fwd_learned_rows_key_centric": {
@@ -218,6 +239,56 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
         "gate_merge": {"ms": round(ms_gm, 4), "bytes": gm_bytes,
                        "gbs": round(gm_bytes / (ms_gm * 1e-3) / 1e9, 1),
                        "frac_hbm_peak": round(gm_bytes / (ms_gm * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+    }
+
+
+def stress_config5(dev, reps: int):
+    """BASELINE config 5 (N=524288, 4 heads, top-32, heavy-tailed blocks,
+    near-tie scores) measured beside the headline: the same layer (keys and
+    values pooled in one launch pair, selection from the pooled keys, plan,
+    attention forward), then the kernels one by one and the backward."""
+    w = W.config(5)
+    q, k, v = W.tensors(w, dev)
+    cu_blk, cu_sb, cu_q = (t.to(dev) for t in (w.cu_block_tokens, w.cu_seqblocks, w.cu_seqlens))
+    n, hkv, d = w.n, w.hkv, w.d
+    k2, v2 = k.view(n, hkv * d), v.view(n, hkv * d)
+
+    def layer():
+        pk, _ = H.block_mean_pool2(k2, v2, cu_blk, torch.float32, None)
+        topk_idx, _ = H.select_blocks(q, k, cu_sb, cu_blk, w.topk, None, True, pooled_k=pk)
+        return H.sel_attn_fwd(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, w.scale)
+
+    ms_layer = event_time_ms(layer, 5)
+    pk, _ = H.block_mean_pool2(k2, v2, cu_blk, torch.float32, None)
+    topk_idx, compact = H.select_blocks(q, k, cu_sb, cu_blk, w.topk, None, True, pooled_k=pk)
+    flops = 4.0 * d * (w.hq // hkv) * W.attended_tokens(compact, w.cu_block_tokens,
+                                                        w.cu_seqblocks)
+    plan = H.SelAttnPlan(q.shape, k.shape, topk_idx, cu_sb, cu_blk, cu_q, backward=True)
+    out = torch.empty_like(q)
+    lse = torch.empty(w.hq, n, dtype=torch.float32, device=dev)
+    ms_f = event_time_ms(lambda: plan.fwd(q, k, v, w.scale, out, lse), reps)
+    do = torch.randn_like(q)
+    ms_b = event_time_ms(lambda: plan.bwd(do, q, k, v, out, lse, w.scale), max(2, reps // 4))
+    ms_sel = event_time_ms(lambda: H.select_blocks(q, k, cu_sb, cu_blk, w.topk, None, True,
+                                                   pooled_k=pk), reps)
+    ms_pool = event_time_ms(lambda: H.block_mean_pool(k2, cu_blk), reps)
+    nb = w.n_blocks
+    pool_bytes = n * hkv * d * 2 + nb * hkv * d * 2 + 4 * (nb + 1)
+    del plan, do, out, lse
+    torch.cuda.empty_cache()
+    tf = flops / (ms_f * 1e-3) / 1e12
+    tb = 2.5 * flops / (ms_b * 1e-3) / 1e12
+    gbs = pool_bytes / (ms_pool * 1e-3) / 1e9
+    return {
+        "workload": f"cfg5: N={n}, H={w.hq}, D={d}, top-{w.topk}, {nb} lognormal blocks",
+        "ms_per_layer": round(ms_layer, 4),
+        "attn_fwd": {"ms": round(ms_f, 4), "tflops": round(tf, 2),
+                     "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)},
+        "attn_bwd": {"ms": round(ms_b, 4), "tflops": round(tb, 2),
+                     "frac_bf16_peak": round(tb / PEAK_BF16_TFLOPS, 4)},
+        "select": {"ms": round(ms_sel, 4)},
+        "pool_k": {"ms": round(ms_pool, 4), "bytes": pool_bytes, "gbs": round(gbs, 1),
+                   "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)},
     }
 
 
@@ -323,6 +394,8 @@ def main() -> int:
                            max(2, reps // 4))
     del bplan, do
     extra = per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q) if args.config == 3 else {}
+    if args.config == 3:
+        extra["cfg5_stress"] = stress_config5(dev, reps)
     nb = w.n_blocks
     pool_bytes = n * hkv * d * 2 + nb * hkv * d * 2 + 4 * (nb + 1)
     attn_tflops = flops / (ms_attn * 1e-3) / 1e12
@@ -375,7 +448,7 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic(),
+            "traffic": measured_traffic(args.config),
         },
     }
     if args.cpu_budget > 0:

@@ -474,8 +474,7 @@ sel_attn_dq_kernel(AttnArgs a) {
     if (row_in_pass) {
       // gathered rows: the slot's share of dQ, summed by kc_dq_merge_kernel
       uint16_t* drow =
-          GATHER ? a.kc.part_o + ((((int64_t)h * a.nq + qi) * a.topk_n + gslot) * a.g +
-                                  (r % a.g)) * D
+          GATHER ? a.kc.part_o + a.kc.pidx(h, qi, gslot, a.topk_n, a.g, r % a.g) * D
                  : a.out + (qi * a.hq + hh) * D;
 #pragma unroll
       for (int db = 0; db < ND; ++db)
@@ -1186,8 +1185,7 @@ kc_resident_dq_kernel(AttnArgs a) {
         }
       }
       if (row_ok) {
-        uint16_t* drow = a.kc.part_o + ((((int64_t)h * a.nq + qi) * a.topk_n + slot) * a.g +
-                                        (r % a.g)) * D;
+        uint16_t* drow = a.kc.part_o + a.kc.pidx(h, qi, slot, a.topk_n, a.g, r % a.g) * D;
 #pragma unroll
         for (int db = 0; db < ND; ++db)
 #pragma unroll
@@ -1251,15 +1249,17 @@ __global__ __launch_bounds__(256) void kc_dq_merge_kernel(AttnArgs a) {
   constexpr int U = 16;   // slots whose shares are loaded together
   if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC || !kc_plan_ok(a)) return;
   const int64_t per_q = (int64_t)a.g * (D / CPT);
-  const int64_t n_items = (int64_t)a.hkv * a.nq * per_q;
+  // the queries of this launch's pass
+  const int64_t n_items = (int64_t)a.hkv * a.kc.q_span * per_q;
   for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
        it += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t hq_idx = it / per_q;  // h * nq + q
+    const int64_t hq_rel = it / per_q;  // h * q_span + (q - q_base)
+    const int h = (int)(hq_rel / a.kc.q_span);
+    const int64_t q = a.kc.q_base + (hq_rel - (int64_t)h * a.kc.q_span);
+    const int64_t hq_idx = (int64_t)h * a.nq + q;
     if (!a.kc.qmark[hq_idx]) continue;
-    const int sub = (int)(it - hq_idx * per_q);
+    const int sub = (int)(it - hq_rel * per_q);
     const int gi = sub / (D / CPT), d0 = (sub % (D / CPT)) * CPT;
-    const int h = (int)(hq_idx / a.nq);
-    const int64_t q = hq_idx - (int64_t)h * a.nq;
     int b, bs, nbb;
     bool st;
     query_batch(a.cu_q, a.batch, a.cu_sb, q, &b, &bs, &nbb, &st);
@@ -1275,7 +1275,7 @@ __global__ __launch_bounds__(256) void kc_dq_merge_kernel(AttnArgs a) {
         const int j = j0 + u;
         const bool in = j < a.topk_n;
         v[u] = in ? row[j] : -1;
-        const int64_t pidx = (hq_idx * a.topk_n + (in ? j : 0)) * a.g + gi;
+        const int64_t pidx = (hq_rel * a.topk_n + (in ? j : 0)) * a.g + gi;
         pv[u] = *reinterpret_cast<const u32x4*>(a.kc.part_o + pidx * D + d0);
       }
 #pragma unroll
@@ -1323,26 +1323,31 @@ int launch_bwd_t(const AttnArgs& a, hipStream_t st) {
     }
     const void* fn = reinterpret_cast<const void*>(&sel_attn_dq_kernel<DT, D, DQ_GATHER>);
     const int grid = persistent_grid(fn, 256, 0);
-    if (grid <= 0) return LSRM_ERR_LAUNCH;
-    hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D, DQ_GATHER>), dim3(grid), dim3(256), 0,
-                       st, a);
-    LSRM_CHECK_LAUNCH();
     const void* fr = reinterpret_cast<const void*>(&kc_resident_dq_kernel<DT, D, 0>);
     const int gr = persistent_grid(fr, 256, 0);
-    if (gr <= 0) return LSRM_ERR_LAUNCH;
-    hipLaunchKernelGGL((kc_resident_dq_kernel<DT, D, 0>), dim3(gr), dim3(256), 0, st, a);
-    LSRM_CHECK_LAUNCH();
-    if constexpr (kc_res_max(D) > KC_RES_KEYS) {
-      const void* fr2 = reinterpret_cast<const void*>(&kc_resident_dq_kernel<DT, D, 1>);
-      const int gr2 = persistent_grid(fr2, 512, 0);
-      if (gr2 <= 0) return LSRM_ERR_LAUNCH;
-      hipLaunchKernelGGL((kc_resident_dq_kernel<DT, D, 1>), dim3(gr2), dim3(512), 0, st, a);
+    int gr2 = 1;
+    if constexpr (kc_res_max(D) > KC_RES_KEYS)
+      gr2 = persistent_grid(reinterpret_cast<const void*>(&kc_resident_dq_kernel<DT, D, 1>),
+                            512, 0);
+    const int gm = device_cu_count() * 16;
+    if (grid <= 0 || gr <= 0 || gr2 <= 0 || gm <= 0) return LSRM_ERR_LAUNCH;
+    // one range of queries at a time: its gathered dQ shares, then their
+    // merge, before the next range reuses the partial buffer
+    for (int p = 0; p < a.kc.n_pass; ++p) {
+      AttnArgs ap = a;
+      ap.kc = a.kc.pass(p, a.hkv, a.nq);
+      hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D, DQ_GATHER>), dim3(grid), dim3(256), 0,
+                         st, ap);
+      LSRM_CHECK_LAUNCH();
+      hipLaunchKernelGGL((kc_resident_dq_kernel<DT, D, 0>), dim3(gr), dim3(256), 0, st, ap);
+      LSRM_CHECK_LAUNCH();
+      if constexpr (kc_res_max(D) > KC_RES_KEYS) {
+        hipLaunchKernelGGL((kc_resident_dq_kernel<DT, D, 1>), dim3(gr2), dim3(512), 0, st, ap);
+        LSRM_CHECK_LAUNCH();
+      }
+      hipLaunchKernelGGL((kc_dq_merge_kernel<DT, D>), dim3(gm), dim3(256), 0, st, ap);
       LSRM_CHECK_LAUNCH();
     }
-    const int gm = device_cu_count() * 16;
-    if (gm <= 0) return LSRM_ERR_LAUNCH;
-    hipLaunchKernelGGL((kc_dq_merge_kernel<DT, D>), dim3(gm), dim3(256), 0, st, a);
-    LSRM_CHECK_LAUNCH();
   }
   {
     const void* fn = reinterpret_cast<const void*>(&sel_attn_dkdv_kernel<DT, D>);

@@ -608,7 +608,7 @@ sel_attn_fwd_kernel(AttnArgs a) {
     const float l_tot = l_run + __shfl_xor(l_run, 32);
     if (row_in_pass) {
       const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-      const int64_t pidx = (((int64_t)h * a.nq + qi) * a.topk_n + gslot) * a.g + (r % a.g);
+      const int64_t pidx = GATHER ? a.kc.pidx(h, qi, gslot, a.topk_n, a.g, r % a.g) : 0;
       uint16_t* orow = GATHER ? a.kc.part_o + pidx * D : a.out + (qi * a.hq + hh) * D;
 #pragma unroll
       for (int db = 0; db < ND; ++db)
@@ -865,7 +865,7 @@ kc_resident_fwd_kernel(AttnArgs a) {
       const float l_tot = l_run + __shfl_xor(l_run, 32);
       if (row_ok) {
         const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-        const int64_t pidx = (((int64_t)h * a.nq + qi) * a.topk_n + slot) * a.g + (r % a.g);
+        const int64_t pidx = a.kc.pidx(h, qi, slot, a.topk_n, a.g, r % a.g);
         uint16_t* orow = a.kc.part_o + pidx * D;
 #pragma unroll
         for (int db = 0; db < ND; ++db)
@@ -902,20 +902,22 @@ __global__ __launch_bounds__(256) void kc_merge_kernel(AttnArgs a) {
   constexpr int U = 16;   // slots loaded together
   if (!kc_plan_ok(a)) return;  // no key-centric part for this run: read nothing
   const int64_t per_q = (int64_t)a.g * (D / CPT);
-  const int64_t n_items = (int64_t)a.hkv * a.nq * per_q;
+  // the queries of this launch's pass
+  const int64_t n_items = (int64_t)a.hkv * a.kc.q_span * per_q;
   for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
        it += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t hq_idx = it / per_q;  // h * nq + q
+    const int64_t hq_rel = it / per_q;  // h * q_span + (q - q_base)
+    const int h = (int)(hq_rel / a.kc.q_span);
+    const int64_t q = a.kc.q_base + (hq_rel - (int64_t)h * a.kc.q_span);
+    const int64_t hq_idx = (int64_t)h * a.nq + q;
     if (!a.kc.qmark[hq_idx]) continue;
-    const int sub = (int)(it - hq_idx * per_q);
+    const int sub = (int)(it - hq_rel * per_q);
     const int gi = sub / (D / CPT), d0 = (sub % (D / CPT)) * CPT;
-    const int h = (int)(hq_idx / a.nq);
-    const int64_t q = hq_idx - (int64_t)h * a.nq;
     int b, bs, nbb;
     bool st;
     query_batch(a.cu_q, a.batch, a.cu_sb, q, &b, &bs, &nbb, &st);
     const int32_t* row = a.topk + hq_idx * a.topk_n;
-    const int64_t pbase = hq_idx * a.topk_n;  // partial (q, slot 0)
+    const int64_t pbase = hq_rel * a.topk_n;  // partial (q, slot 0) of the pass
     float mx = -__builtin_inf();
     float acc[CPT];
 #pragma unroll
@@ -991,26 +993,31 @@ int launch_fwd_t(const AttnArgs& a, hipStream_t st) {
   if (a.kc.fitems) {  // key-centric plans: gathered tiles, then the merge
     const void* fg = reinterpret_cast<const void*>(&sel_attn_fwd_kernel<DT, D, FWD_GATHER>);
     const int gg = persistent_grid(fg, 256, 0);
-    if (gg <= 0) return LSRM_ERR_LAUNCH;
-    hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, FWD_GATHER>), dim3(gg), dim3(256), 0, st,
-                       a);
-    LSRM_CHECK_LAUNCH();
     const void* fr = reinterpret_cast<const void*>(&kc_resident_fwd_kernel<DT, D, 0>);
     const int gr = persistent_grid(fr, 256, 0);
-    if (gr <= 0) return LSRM_ERR_LAUNCH;
-    hipLaunchKernelGGL((kc_resident_fwd_kernel<DT, D, 0>), dim3(gr), dim3(256), 0, st, a);
-    LSRM_CHECK_LAUNCH();
-    if constexpr (kc_res_max(D) > KC_RES_KEYS) {
-      const void* fr2 = reinterpret_cast<const void*>(&kc_resident_fwd_kernel<DT, D, 1>);
-      const int gr2 = persistent_grid(fr2, 512, 0);
-      if (gr2 <= 0) return LSRM_ERR_LAUNCH;
-      hipLaunchKernelGGL((kc_resident_fwd_kernel<DT, D, 1>), dim3(gr2), dim3(512), 0, st, a);
+    int gr2 = 1;
+    if constexpr (kc_res_max(D) > KC_RES_KEYS)
+      gr2 = persistent_grid(reinterpret_cast<const void*>(&kc_resident_fwd_kernel<DT, D, 1>),
+                            512, 0);
+    const int gm = device_cu_count() * 16;
+    if (gg <= 0 || gr <= 0 || gr2 <= 0 || gm <= 0) return LSRM_ERR_LAUNCH;
+    // one range of queries at a time: its gathered tiles, then their merge,
+    // before the next range reuses the partial buffer
+    for (int p = 0; p < a.kc.n_pass; ++p) {
+      AttnArgs ap = a;
+      ap.kc = a.kc.pass(p, a.hkv, a.nq);
+      hipLaunchKernelGGL((sel_attn_fwd_kernel<DT, D, FWD_GATHER>), dim3(gg), dim3(256), 0, st,
+                         ap);
+      LSRM_CHECK_LAUNCH();
+      hipLaunchKernelGGL((kc_resident_fwd_kernel<DT, D, 0>), dim3(gr), dim3(256), 0, st, ap);
+      LSRM_CHECK_LAUNCH();
+      if constexpr (kc_res_max(D) > KC_RES_KEYS) {
+        hipLaunchKernelGGL((kc_resident_fwd_kernel<DT, D, 1>), dim3(gr2), dim3(512), 0, st, ap);
+        LSRM_CHECK_LAUNCH();
+      }
+      hipLaunchKernelGGL((kc_merge_kernel<DT, D>), dim3(gm), dim3(256), 0, st, ap);
       LSRM_CHECK_LAUNCH();
     }
-    const int gm = device_cu_count() * 16;
-    if (gm <= 0) return LSRM_ERR_LAUNCH;
-    hipLaunchKernelGGL((kc_merge_kernel<DT, D>), dim3(gm), dim3(256), 0, st, a);
-    LSRM_CHECK_LAUNCH();
   }
   return LSRM_OK;
 }

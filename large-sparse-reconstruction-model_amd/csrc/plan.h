@@ -72,31 +72,65 @@ int mark_grouped_queries(const TilePlan& plan, int64_t hkv, int64_t nq,
 // (query, slot, query head) -- O normalised by its own row sum in the input
 // type and its log2 LSE -- and the dQ pass the slot's share of dQ; merge
 // passes combine each query's partials in slot order.
+//
+// The partial buffer holds the queries of one pass: queries are taken in
+// n_pass ranges of q_span_max consecutive queries (sized so that a pass's
+// partials stay within KC_PART_BUDGET bytes), each range's gathered tiles
+// run and merge before the next range reuses the buffer.  Items never
+// straddle a range, and the item lists are stored per (pass, kv head):
+// entry (p, h) of a list is "head" p * hkv + h.
 struct KcPlan {
   uint8_t* qmark;        // [hkv, n_q] queries of grouped tiles
   RevMap grev;           // block -> marked queries, cap = n_q * topk per head
-  uint16_t* part_o;      // [hkv, n_q, topk, g, D] input type
-  float* part_lse;       // [hkv, n_q, topk, g]
+  uint16_t* part_o;      // [hkv, q_span_max, topk, g, D] input type
+  float* part_lse;       // [hkv, q_span_max, topk, g]
+  int n_pass;
+  int64_t q_span_max;
+  // the pass a launch works on (set by the launcher): queries
+  // [q_base, q_base + q_span); the item lists below then point at that
+  // pass's entries
+  int64_t q_base, q_span;
   // Items of blocks with 1..KC_RES_KEYS keys, run with the block resident
   // in LDS (forward and dQ): up to KC_RES_CHUNKS * tq listings each.
-  int4* ritems;
+  int4* ritems;          // [n_pass * hkv, ritem_cap]
   int64_t ritem_cap;
-  int32_t* ritem_count;  // [hkv]
-  int32_t* ritem_off;    // [hkv + 1]
+  int32_t* ritem_count;  // [n_pass * hkv]
+  int32_t* ritem_off;    // [n_pass, hkv + 1]
   // The same for blocks of KC_RES_KEYS + 1 .. KC_RES2_KEYS keys (head dim
   // <= 64; empty otherwise), run by the eight-wave resident kernels.
   int4* r2items;
   int64_t r2item_cap;
-  int32_t* r2item_count;  // [hkv]
-  int32_t* r2item_off;    // [hkv + 1]
+  int32_t* r2item_count;  // [n_pass * hkv]
+  int32_t* r2item_off;    // [n_pass, hkv + 1]
   // The streaming gathered tiles' items: blocks the resident kernels do not
   // take (no keys, or more than kc_res_max of the plan's head dim), at most
   // tq listings each.  fitems is null in plans without this part.
   int4* fitems;
   int64_t fitem_cap;
-  int32_t* fitem_count;  // [hkv]
-  int32_t* fitem_off;    // [hkv + 1]
+  int32_t* fitem_count;  // [n_pass * hkv]
+  int32_t* fitem_off;    // [n_pass, hkv + 1]
+
+  // The plan's pass p: the item lists of that pass and its query range.
+  __host__ __device__ KcPlan pass(int p, int64_t hkv, int64_t n_q) const {
+    KcPlan k = *this;
+    k.q_base = p * q_span_max;
+    k.q_span = n_q - k.q_base < q_span_max ? n_q - k.q_base : q_span_max;
+    k.ritems = ritems + p * hkv * ritem_cap;
+    k.ritem_off = ritem_off + p * (hkv + 1);
+    k.r2items = r2items + p * hkv * r2item_cap;
+    k.r2item_off = r2item_off + p * (hkv + 1);
+    k.fitems = fitems + p * hkv * fitem_cap;
+    k.fitem_off = fitem_off + p * (hkv + 1);
+    return k;
+  }
+  // Index of the partial of (kv head h, query q of this pass, slot, query
+  // head gi of the group) in part_lse (times D in part_o).
+  __device__ int64_t pidx(int h, int64_t q, int64_t slot, int topk, int g, int gi) const {
+    return (((int64_t)h * q_span + (q - q_base)) * topk + slot) * g + gi;
+  }
 };
+// Bytes of key-centric partial results one pass may hold.
+constexpr int64_t KC_PART_BUDGET = int64_t{1} << 30;
 // Work counters of the gathered-tile kernels inside TilePlan::counter.
 constexpr int KC_QUEUE_SLOT = 16, KC_EXIT_SLOT = 18;
 constexpr int KC_RQUEUE_SLOT = 20, KC_REXIT_SLOT = 22;
@@ -122,9 +156,13 @@ __host__ __device__ constexpr int32_t kc_plan_marker(int flags, int head_dim) {
 // blocks, counts and order: the map of the same queries without slots).
 int derive_query_map(const RevMap& enc, const RevMap& plain, int64_t hkv, int64_t nb,
                      int64_t topk_n, hipStream_t st);
+// Passes of a key-centric plan: (n_pass, queries per pass) so that one
+// pass's partials fit KC_PART_BUDGET.
+void kc_passes(int64_t n_q, int64_t hkv, int64_t topk, int g, int64_t head_dim, int* n_pass,
+               int64_t* q_span);
 int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
-                   int64_t nb, int tq, int64_t head_dim, Carver& ws, KcPlan& kc,
-                   int32_t* counter, int32_t marker, hipStream_t st);
+                   int64_t nb, int tq, int64_t head_dim, int64_t topk_n, Carver& ws,
+                   KcPlan& kc, int32_t* counter, int32_t marker, hipStream_t st);
 
 // Key chunks of at most KEY_CHUNK tokens inside each block (head
 // independent): item i = (block, first token, length) packed in an int4

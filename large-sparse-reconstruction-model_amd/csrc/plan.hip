@@ -817,47 +817,74 @@ __device__ inline int64_t kc_block_len(const int32_t* cu_blk, int64_t nk, int64_
   return s1 - s0;
 }
 
-// Gathered tiles of block c: ceil(listings / tq) pieces of its grev segment.
-// With cu_blk set, only blocks of lo + 1 .. hi keys count (the resident
-// forwards' items, lo >= 0), or with `outside` only the other blocks (the
-// streaming forward's); with cu_blk null, every block counts.
-struct KcItemsF {
+// The listings of block c of grev's segment of kv head h that belong to
+// queries [p * pq, (p + 1) * pq) (pass p of pq queries): [s, e) of the
+// segment, found by binary search (listings q * topk + slot ascend).
+struct KcPassRange {
   const int32_t* cu_rev;
+  const int32_t* rev;
   int64_t nb, cap;
+  int hkv;
+  int64_t pass_listings;  // pq * topk; 0 = one pass
+  __device__ void operator()(int vs, int64_t c, int64_t& s, int64_t& e) const {
+    const int p = vs / hkv, h = vs - p * hkv;
+    const int32_t* cr = cu_rev + (int64_t)h * (nb + 1);
+    s = cr[c];
+    e = cr[c + 1];
+    e = e < cap ? e : cap;
+    if (pass_listings == 0 || e <= s) return;
+    const int32_t* r = rev + (int64_t)h * cap;
+    auto first_at = [&](int64_t x) {  // first i in [s, e) with r[i] >= x
+      int64_t lo = s, hi = e;
+      while (lo < hi) {
+        const int64_t m = (lo + hi) >> 1;
+        if ((int64_t)r[m] < x) lo = m + 1; else hi = m;
+      }
+      return lo;
+    };
+    const int64_t a = first_at(p * pass_listings), b = first_at((p + 1) * pass_listings);
+    s = a;
+    e = b;
+  }
+};
+
+// Gathered tiles of block c in the segment "vs" = (pass p, kv head h):
+// ceil(listings / tq) pieces of the pass's listings of the block.  With
+// cu_blk set, only blocks of lo + 1 .. hi keys count (the resident forwards'
+// items, lo >= 0), or with `outside` only the other blocks (the streaming
+// forward's); with cu_blk null, every block counts.
+struct KcItemsF {
+  KcPassRange rg;
   int tq;
   const int32_t* cu_blk;
   int64_t nk;
   int lo, hi;
   bool outside;
   __device__ int64_t limit(int, int64_t n) const { return n; }
-  __device__ int operator()(int h, int64_t c) const {
+  __device__ int operator()(int vs, int64_t c) const {
     if (cu_blk) {
       const int64_t len = kc_block_len(cu_blk, nk, c);
       const bool in = len > lo && len <= hi;
       if (in == outside) return 0;
     }
-    const int32_t* p = cu_rev + (int64_t)h * (nb + 1);
-    int64_t s = p[c], e = p[c + 1];
-    e = e < cap ? e : cap;
+    int64_t s, e;
+    rg(vs, c, s, e);
     return e > s ? (int)((e - s + tq - 1) / tq) : 0;
   }
 };
 struct KcItemsW {
-  const int32_t* cu_rev;
-  int64_t nb, cap;
+  KcPassRange rg;
   int tq;
   int4* items;
   int64_t item_cap;
-  __device__ void operator()(int h, int64_t c, int ex, int v, int64_t) const {
+  __device__ void operator()(int vs, int64_t c, int ex, int v, int64_t) const {
     if (v == 0) return;
-    const int32_t* p = cu_rev + (int64_t)h * (nb + 1);
-    const int64_t s = p[c];
-    int64_t e = p[c + 1];
-    e = e < cap ? e : cap;
+    int64_t s, e;
+    rg(vs, c, s, e);
     for (int t = 0; t < v && ex + t < item_cap; ++t) {
       const int64_t e0 = s + (int64_t)tq * t;
       const int64_t n = e - e0 < tq ? e - e0 : tq;
-      items[(int64_t)h * item_cap + ex + t] = make_int4((int)c, (int)e0, (int)n, 0);
+      items[(int64_t)vs * item_cap + ex + t] = make_int4((int)c, (int)e0, (int)n, 0);
     }
   }
 };
@@ -890,21 +917,25 @@ int derive_query_map(const RevMap& enc, const RevMap& plain, int64_t hkv, int64_
   return LSRM_OK;
 }
 
-// Per-head offsets of the item lists (resident, eight-wave resident,
-// streaming) and their cleared work counters.
+// Per-(pass, head) offsets of the item lists (resident, eight-wave
+// resident, streaming) -- each pass's heads from 0 -- and their cleared work
+// counters.
 struct KcCounts {
   const int32_t* count[3];
   int32_t* off[3];
 };
-__global__ void kc_offsets_kernel(KcCounts c, int hkv, int32_t* counter, int32_t marker) {
+__global__ void kc_offsets_kernel(KcCounts c, int hkv, int n_pass, int32_t* counter,
+                                  int32_t marker) {
   if (threadIdx.x < 3 && blockIdx.x == 0) {
     const int32_t* cnt = c.count[threadIdx.x];
     int32_t* off = c.off[threadIdx.x];
-    int acc = 0;
-    off[0] = 0;
-    for (int h = 0; h < hkv; ++h) {
-      acc += cnt[h];
-      off[h + 1] = acc;
+    for (int p = 0; p < n_pass; ++p) {
+      int acc = 0;
+      off[p * (hkv + 1)] = 0;
+      for (int h = 0; h < hkv; ++h) {
+        acc += cnt[p * hkv + h];
+        off[p * (hkv + 1) + h + 1] = acc;
+      }
     }
   }
   if (threadIdx.x == 0 && blockIdx.x == 0) {
@@ -918,48 +949,62 @@ __global__ void kc_offsets_kernel(KcCounts c, int hkv, int32_t* counter, int32_t
   }
 }
 
+void kc_passes(int64_t n_q, int64_t hkv, int64_t topk, int g, int64_t head_dim, int* n_pass,
+               int64_t* q_span) {
+  const int64_t per_q = hkv * topk * g * (2 * (head_dim > 0 ? head_dim : 1) + 4);
+  int64_t span = per_q > 0 ? KC_PART_BUDGET / per_q : n_q;
+  if (span < 1) span = 1;
+  if (span >= n_q) span = n_q > 0 ? n_q : 1;
+  *q_span = span;
+  *n_pass = (int)((n_q + span - 1) / span > 0 ? (n_q + span - 1) / span : 1);
+}
+
 int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
-                   int64_t nb, int tq, int64_t head_dim, Carver& ws, KcPlan& kc,
-                   int32_t* counter, int32_t marker, hipStream_t st) {
+                   int64_t nb, int tq, int64_t head_dim, int64_t topk_n, Carver& ws,
+                   KcPlan& kc, int32_t* counter, int32_t marker, hipStream_t st) {
   const int rq = tq * KC_RES_CHUNKS;
   const int res_max = kc_res_max((int)(head_dim > 0 ? head_dim : 1));
-  kc.ritem_cap = grev.cap / (rq > 0 ? rq : 1) + nb + 1;
-  kc.ritems = ws.take<int4>((size_t)(hkv * kc.ritem_cap));
-  kc.ritem_count = ws.take<int32_t>((size_t)hkv);
-  kc.ritem_off = ws.take<int32_t>((size_t)(hkv + 1));
+  const int np = kc.n_pass > 0 ? kc.n_pass : 1;
+  // listings of one (pass, head): at most the pass's queries times topk
+  const int64_t lst = np > 1 ? kc.q_span_max * topk_n : grev.cap;
+  kc.ritem_cap = lst / (rq > 0 ? rq : 1) + nb + 1;
+  kc.ritems = ws.take<int4>((size_t)(np * hkv * kc.ritem_cap));
+  kc.ritem_count = ws.take<int32_t>((size_t)(np * hkv));
+  kc.ritem_off = ws.take<int32_t>((size_t)(np * (hkv + 1)));
   kc.r2item_cap = kc.ritem_cap;
-  kc.r2items = ws.take<int4>((size_t)(hkv * kc.r2item_cap));
-  kc.r2item_count = ws.take<int32_t>((size_t)hkv);
-  kc.r2item_off = ws.take<int32_t>((size_t)(hkv + 1));
-  kc.fitem_cap = grev.cap / (tq > 0 ? tq : 1) + nb + 1;
-  kc.fitems = ws.take<int4>((size_t)(hkv * kc.fitem_cap));
-  kc.fitem_count = ws.take<int32_t>((size_t)hkv);
-  kc.fitem_off = ws.take<int32_t>((size_t)(hkv + 1));
-  int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, hkv));
+  kc.r2items = ws.take<int4>((size_t)(np * hkv * kc.r2item_cap));
+  kc.r2item_count = ws.take<int32_t>((size_t)(np * hkv));
+  kc.r2item_off = ws.take<int32_t>((size_t)(np * (hkv + 1)));
+  kc.fitem_cap = lst / (tq > 0 ? tq : 1) + nb + 1;
+  kc.fitems = ws.take<int4>((size_t)(np * hkv * kc.fitem_cap));
+  kc.fitem_count = ws.take<int32_t>((size_t)(np * hkv));
+  kc.fitem_off = ws.take<int32_t>((size_t)(np * (hkv + 1)));
+  int32_t* sums = ws.take<int32_t>((size_t)scan_sums_size(nb, np * hkv));
   if (!ws.base || ws.dry) return LSRM_OK;
   if (!ws.ok()) return LSRM_ERR_WORKSPACE;
   for (int32_t* cnt : {kc.ritem_count, kc.r2item_count, kc.fitem_count}) {
-    const int rc = launch_zero_i32(cnt, hkv, st);
+    const int rc = launch_zero_i32(cnt, np * hkv, st);
     if (rc) return rc;
   }
-  int rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, rq, cu_blk, nk, 0, KC_RES_KEYS, false},
-                    KcItemsW{grev.cu_rev, nb, grev.cap, rq, kc.ritems, kc.ritem_cap}, nb,
-                    (int)hkv, sums, kc.ritem_count, st);
+  const KcPassRange rg{grev.cu_rev, grev.rev, nb, grev.cap, (int)hkv,
+                       np > 1 ? kc.q_span_max * topk_n : 0};
+  const int nseg = (int)(np * hkv);
+  int rc = run_scan(KcItemsF{rg, rq, cu_blk, nk, 0, KC_RES_KEYS, false},
+                    KcItemsW{rg, rq, kc.ritems, kc.ritem_cap}, nb, nseg, sums, kc.ritem_count,
+                    st);
   if (rc) return rc;
   if (res_max > KC_RES_KEYS) {
-    rc = run_scan(
-        KcItemsF{grev.cu_rev, nb, grev.cap, rq, cu_blk, nk, KC_RES_KEYS, res_max, false},
-        KcItemsW{grev.cu_rev, nb, grev.cap, rq, kc.r2items, kc.r2item_cap}, nb, (int)hkv, sums,
-        kc.r2item_count, st);
+    rc = run_scan(KcItemsF{rg, rq, cu_blk, nk, KC_RES_KEYS, res_max, false},
+                  KcItemsW{rg, rq, kc.r2items, kc.r2item_cap}, nb, nseg, sums, kc.r2item_count,
+                  st);
     if (rc) return rc;
   }
-  rc = run_scan(KcItemsF{grev.cu_rev, nb, grev.cap, tq, cu_blk, nk, 0, res_max, true},
-                KcItemsW{grev.cu_rev, nb, grev.cap, tq, kc.fitems, kc.fitem_cap}, nb,
-                (int)hkv, sums, kc.fitem_count, st);
+  rc = run_scan(KcItemsF{rg, tq, cu_blk, nk, 0, res_max, true},
+                KcItemsW{rg, tq, kc.fitems, kc.fitem_cap}, nb, nseg, sums, kc.fitem_count, st);
   if (rc) return rc;
   const KcCounts c{{kc.ritem_count, kc.r2item_count, kc.fitem_count},
                    {kc.ritem_off, kc.r2item_off, kc.fitem_off}};
-  hipLaunchKernelGGL(kc_offsets_kernel, dim3(1), dim3(64), 0, st, c, (int)hkv, counter,
+  hipLaunchKernelGGL(kc_offsets_kernel, dim3(1), dim3(64), 0, st, c, (int)hkv, np, counter,
                      marker);
   LSRM_CHECK_LAUNCH();
   return LSRM_OK;

@@ -7,6 +7,7 @@ PyTorch fallback: a missing library or a CPU tensor raises.
 
 from __future__ import annotations
 
+import collections
 import ctypes
 import math
 from pathlib import Path
@@ -375,67 +376,90 @@ def sel_attn_fwd(q, k, v, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
                  softmax_scale: float, key_centric: bool = False):
     """Selected-block attention forward -> (out [Nq, Hq, D], lse [Hq, Nq] log2).
 
-    key_centric: plan with LSRM_PLAN_KEY_CENTRIC (per-token rows without
-    locality run as per-block gathered tiles plus a merge; the workspace
-    then holds up to Hq * Nq * topk * (2 * D + 4) bytes of partial results)."""
+    The device plan comes from plan_for (one plan per selection, shared with
+    a later backward of the same selection).  key_centric: plan with
+    LSRM_PLAN_KEY_CENTRIC (per-token rows without locality run as per-block
+    gathered tiles plus a merge, over query ranges whose partial results
+    stay within 1 GiB)."""
     dev = _attn_check(q, k, v, topk_idx)
     _dev_check(q, cu_seqblocks, cu_block_tokens, cu_seqlens_q)
-    nq, hq, d = q.shape
-    nk, hkv, _ = k.shape
-    topk = topk_idx.shape[-1]
-    nb = cu_block_tokens.numel() - 1
-    batch = cu_seqlens_q.numel() - 1
     out = torch.empty_like(q)
-    lse = torch.empty(hq, nq, dtype=torch.float32, device=dev)
-    if nq == 0:
+    lse = torch.empty(q.shape[1], q.shape[0], dtype=torch.float32, device=dev)
+    if q.shape[0] == 0:
         return out, lse
-    if key_centric:
-        plan = SelAttnPlan(q.shape, k.shape, topk_idx, cu_seqblocks, cu_block_tokens,
-                           cu_seqlens_q, key_centric=True)
-        return plan.fwd(q, k, v, softmax_scale, out, lse)
-    with torch.cuda.device(dev):
-        ws_n = lib().lsrm_sel_attn_workspace_size(nq, nk, hq, hkv, topk, nb, 0)
-        ws = _workspace(ws_n, dev)
-        _check(lib().lsrm_sel_attn_fwd(
-            _ptr(q), _ptr(k), _ptr(v), _DTYPE_CODE[q.dtype], nq, nk, hq, hkv, d,
-            _ptr(topk_idx), topk, _ptr(cu_seqblocks), _ptr(cu_block_tokens), nb,
-            _ptr(cu_seqlens_q), batch, float(softmax_scale), _ptr(out), _ptr(lse),
-            _ptr(ws), ws.numel(), _stream(dev)), "lsrm_sel_attn_fwd")
-    return out, lse
+    plan = plan_for(q.shape, k.shape, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
+                    backward=False, key_centric=key_centric)
+    return plan.fwd(q, k, v, softmax_scale, out, lse)
 
 
 def sel_attn_bwd(do, q, k, v, o, lse, topk_idx, cu_seqblocks, cu_block_tokens,
                  cu_seqlens_q, softmax_scale: float, key_centric: bool = False):
-    """Selected-block attention backward -> (dq, dk, dv, delta)
-    (key_centric: dQ of per-token rows without locality on gathered tiles)."""
+    """Selected-block attention backward -> (dq, dk, dv, delta) on the plan
+    of the selection (plan_for: the forward's plan when it was built with
+    its backward part, otherwise a new backward plan).  key_centric: dQ of
+    per-token rows without locality on gathered tiles."""
     dev = _attn_check(q, k, v, topk_idx, do=do, o=o, lse=lse)
     _dev_check(q, cu_seqblocks, cu_block_tokens, cu_seqlens_q)
-    if key_centric and q.shape[0] > 0:
-        plan = SelAttnPlan(q.shape, k.shape, topk_idx, cu_seqblocks, cu_block_tokens,
-                           cu_seqlens_q, backward=True, key_centric=True)
-        return plan.bwd(do, q, k, v, o, lse, softmax_scale)
-    _no_capture("the backward plan")
-    nq, hq, d = q.shape
-    nk, hkv, _ = k.shape
-    topk = topk_idx.shape[-1]
-    nb = cu_block_tokens.numel() - 1
-    batch = cu_seqlens_q.numel() - 1
-    dq = torch.empty_like(q)
-    dk = torch.zeros_like(k)   # keys outside every block get zero gradient
-    dv = torch.zeros_like(v)
-    delta = torch.empty(hq, nq, dtype=torch.float32, device=dev)
-    if nq == 0:
-        return dq, dk, dv, delta
-    with torch.cuda.device(dev):
-        ws_n = lib().lsrm_sel_attn_workspace_size(nq, nk, hq, hkv, topk, nb, 1)
-        ws = _workspace(ws_n, dev)
-        _check(lib().lsrm_sel_attn_bwd(
-            _ptr(do), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse),
-            _DTYPE_CODE[q.dtype], nq, nk, hq, hkv, d, _ptr(topk_idx), topk,
-            _ptr(cu_seqblocks), _ptr(cu_block_tokens), nb, _ptr(cu_seqlens_q), batch,
-            float(softmax_scale), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta),
-            _ptr(ws), ws.numel(), _stream(dev)), "lsrm_sel_attn_bwd")
-    return dq, dk, dv, delta
+    if q.shape[0] == 0:
+        return (torch.empty_like(q), torch.zeros_like(k), torch.zeros_like(v),
+                torch.empty(q.shape[1], 0, dtype=torch.float32, device=dev))
+    plan = plan_for(q.shape, k.shape, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
+                    backward=True, key_centric=key_centric)
+    return plan.bwd(do, q, k, v, o, lse, softmax_scale)
+
+
+# Plans of the most recent selections, keyed by the selection's tensors
+# (address, version counter, shape) and the plan flags: the forward, an
+# activation-checkpoint recompute and the backward of one selection share one
+# plan.  A cached plan holds its selection tensors, so their memory cannot be
+# handed to another tensor while the entry lives; an in-place change of a
+# tensor bumps its version and misses.
+_PLAN_CACHE_SIZE = 2
+_plan_cache: "collections.OrderedDict" = collections.OrderedDict()
+plan_builds = 0  # plans built through plan_for (a counter for tests)
+
+
+def _plan_key(q_shape, k_shape, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
+              key_centric):
+    ts = (topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q)
+    return (tuple(q_shape), tuple(k_shape[:2]), bool(key_centric), str(topk_idx.device),
+            tuple(topk_idx.shape)) + tuple((t.data_ptr(), t._version, t.numel()) for t in ts)
+
+
+def plan_for(q_shape, k_shape, topk_idx, cu_seqblocks, cu_block_tokens, cu_seqlens_q,
+             backward: bool = False, key_centric: bool = False) -> "SelAttnPlan":
+    """The SelAttnPlan of a selection, built once and reused: a cached plan
+    with the backward part also serves forwards; a forward-only plan is
+    replaced by one with the backward part when a backward asks.  Under HIP
+    graph capture the plan is always built inside the capture (a replay then
+    rebuilds it from the replayed selection)."""
+    global plan_builds
+    capturing = torch.cuda.is_current_stream_capturing()
+    if capturing and not backward:
+        # the key-centric part sorts with rocPRIM (memsets): a captured
+        # forward takes the grouped-tile plan, which captures
+        key_centric = False
+    key = None if capturing else _plan_key(q_shape, k_shape, topk_idx, cu_seqblocks,
+                                           cu_block_tokens, cu_seqlens_q, key_centric)
+    if key is not None:
+        hit = _plan_cache.get(key)
+        if hit is not None and (hit.backward or not backward):
+            _plan_cache.move_to_end(key)
+            return hit
+    plan = SelAttnPlan(q_shape, k_shape, topk_idx, cu_seqblocks, cu_block_tokens,
+                       cu_seqlens_q, backward=backward, key_centric=key_centric)
+    plan_builds += 1
+    if key is not None:
+        _plan_cache[key] = plan
+        _plan_cache.move_to_end(key)
+        while len(_plan_cache) > _PLAN_CACHE_SIZE:
+            _plan_cache.popitem(last=False)
+    return plan
+
+
+def clear_plan_cache() -> None:
+    """Drops the cached plans (and the workspace memory they hold)."""
+    _plan_cache.clear()
 
 
 class SelAttnPlan:

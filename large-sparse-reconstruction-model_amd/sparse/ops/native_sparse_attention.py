@@ -20,7 +20,7 @@ import lsrm_hip as _hip
 
 _default_variant = "a"
 _validate = True
-_key_centric = False
+_key_centric = "auto"
 
 
 def set_variant(variant: str) -> None:
@@ -38,16 +38,32 @@ def set_validation(enabled: bool) -> None:
     _validate = bool(enabled)
 
 
-def set_key_centric(enabled: bool) -> None:
+def set_key_centric(enabled) -> None:
     """Plans the forward and dQ with the key-centric pass for per-token rows
     (learned selections, 3D-aware maps): the grouped tiles (consecutive
     queries whose rows differ) are taken out of the grouped-tile passes,
     each block's selecting queries are gathered into full tiles and the
-    per-block partial results merged in row order.  Off by default: the
-    workspace then holds up to Hq * N * topk * (2 * D + 4) bytes of partial
-    results."""
+    per-block partial results merged in row order, one range of queries at
+    a time so that the partial results stay within 1 GiB.  True, False, or
+    "auto" (the default): per selection, on when its runs of identical rows
+    are short enough for the plan to form grouped tiles (one device
+    reduction and one host read per selection)."""
     global _key_centric
-    _key_centric = bool(enabled)
+    _key_centric = enabled if enabled == "auto" else bool(enabled)
+
+
+def _use_key_centric(q, k, topk_idx) -> bool:
+    """The key-centric choice for this selection (see set_key_centric)."""
+    if _key_centric != "auto":
+        return bool(_key_centric)
+    if topk_idx.shape[1] < 2 or torch.compiler.is_compiling():
+        return False
+    # The plan groups runs shorter than a quarter of a 128-row tile's
+    # queries; the key-centric part pays off when such runs dominate.
+    short = max(1, (128 // (q.shape[1] // k.shape[1])) // 4)
+    changes = int((topk_idx[:, 1:] != topk_idx[:, :-1]).any(-1).sum())
+    runs = changes + topk_idx.shape[0]
+    return runs * short > topk_idx.shape[0] * topk_idx.shape[1]
 
 
 def _check_meta(q, k, topk_idx, cu_seqblocks, cu_block_include_tokens, cu_seqlens_q,
@@ -95,13 +111,20 @@ class NSA(torch.autograd.Function):
 
         _check_meta(q, k, topk_idx, cu_seqblocks, cu_block_include_tokens, cu_seqlens_q,
                     cu_seqlens_k)
+        key_centric = _use_key_centric(q, k, topk_idx)
+        if any(t.requires_grad for t in (q, k, v)) and q.is_cuda and q.shape[0] > 0 and \
+                not torch.compiler.is_compiling():
+            # One plan per selection: built here with its backward part, it
+            # serves this forward, a checkpoint recompute and the backward.
+            _hip.plan_for(q.shape, k.shape, topk_idx, cu_seqblocks, cu_block_include_tokens,
+                          cu_seqlens_q, backward=True, key_centric=key_centric)
         o, lse = torch.ops.lsrm_hip.sel_attn_fwd(q, k, v, topk_idx, cu_seqblocks,
                                                  cu_block_include_tokens, cu_seqlens_q,
-                                                 float(softmax_scale), _key_centric)
+                                                 float(softmax_scale), key_centric)
         ctx.save_for_backward(q, k, v, o, lse, cu_seqlens_q, cu_seqlens_k, topk_idx,
                               cu_seqblocks, cu_block_include_tokens)
         ctx.softmax_scale = softmax_scale
-        ctx.key_centric = _key_centric
+        ctx.key_centric = key_centric
         ctx.mark_non_differentiable(lse)
         return o, lse
 

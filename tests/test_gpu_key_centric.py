@@ -219,7 +219,7 @@ def test_sparse_ops_knob_with_autograd():
         out = ops.native_sparse_attend(qd, kd, vd, rows.to(DEV), cu_sb.to(DEV),
                                        cu_blk.to(DEV), cu_q.to(DEV), cu_q.to(DEV), 0.125)
     finally:
-        ops.set_key_centric(False)
+        ops.set_key_centric("auto")
     qf, kf, vf = (t.float().requires_grad_() for t in (q, k, v))
     o_ref, _ = sel_attn_ref(qf, kf, vf, rows, cu_sb, cu_blk, cu_q, 0.125)
     assert_attn_close(out, o_ref, "out")
