@@ -42,6 +42,11 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 
+def progress(msg: str) -> None:
+    """A progress line on stderr (stdout carries only the result line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def event_time_ms(fn, reps: int) -> float:
     """Average ms per call of fn() measured with HIP events on torch's
     current stream (the stream every lsrm_hip call launches on), after one
@@ -179,7 +184,9 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
     import sparse.ops as ops
 
     dev = q.device
+    progress("3D-aware rows, H=24 D=64")
     res = aware_rows_case(w, q, k, v, "")
+    progress("3D-aware rows, product heads (Hq=32, Hkv=2, D=32)")
     # LSRM's own decoder heads (main_lrm_vol_sparse.py:561-562): 32 query
     # heads over 2 kv heads, head dim 32, on the same tokens
     wp = W.product_shape()
@@ -188,6 +195,7 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
     del qp, kp, vp
     torch.cuda.empty_cache()
 
+    progress("learned selection")
     ops.set_validation(False)
     ck = H.block_mean_pool(k.view(w.n, -1), cu_blk).view(-1, w.hkv, w.d)
     cv = H.block_mean_pool(v.view(w.n, -1), cu_blk).view(-1, w.hkv, w.d)
@@ -216,6 +224,7 @@ def per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q):
                               key_centric=True), 2)
     del out_l, lse_l
 
+    progress("gate merge")
     # gated merge of the three branch outputs at the layer shape (streams
     # gate [N, 3*hidden] and three [N, hidden] inputs, writes [N, hidden])
     hid = w.hq * w.d
@@ -363,6 +372,7 @@ def main() -> int:
         per_head.append(4.0 * d * g * float((att_per_block[h] * lens).sum()))
     flops = sum(per_head)
 
+    progress(f"{w.name}: layer steps")
     for _ in range(args.warmup):
         layer()
     torch.cuda.synchronize()
@@ -372,6 +382,7 @@ def main() -> int:
     torch.cuda.synchronize()
     ms_layer = (time.perf_counter() - t0) * 1e3 / args.steps
 
+    progress("kernel timings")
     # Per-kernel times (HIP events on the launch stream).
     reps = args.kernel_reps
     plan = H.SelAttnPlan(q.shape, k.shape, topk_idx, cu_sb, cu_blk, cu_q)
@@ -395,6 +406,7 @@ def main() -> int:
     del bplan, do
     extra = per_token_paths(w, q, k, v, cu_sb, cu_blk, cu_q) if args.config == 3 else {}
     if args.config == 3:
+        progress("cfg5 stress config")
         extra["cfg5_stress"] = stress_config5(dev, reps)
     nb = w.n_blocks
     pool_bytes = n * hkv * d * 2 + nb * hkv * d * 2 + 4 * (nb + 1)
@@ -452,6 +464,7 @@ def main() -> int:
         },
     }
     if args.cpu_budget > 0:
+        progress("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(w, q, k, v, topk_idx, per_head, args.cpu_budget)
     else:
         result["cpu_baseline"] = None

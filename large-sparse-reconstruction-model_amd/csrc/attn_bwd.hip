@@ -1250,12 +1250,13 @@ __global__ __launch_bounds__(256) void kc_dq_merge_kernel(AttnArgs a) {
   if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC || !kc_plan_ok(a)) return;
   const int64_t per_q = (int64_t)a.g * (D / CPT);
   // the queries of this launch's pass
-  const int64_t n_items = (int64_t)a.hkv * a.kc.q_span * per_q;
+  const int64_t n_items = (int64_t)a.kc.h_count * a.kc.q_span * per_q;
   for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
        it += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t hq_rel = it / per_q;  // h * q_span + (q - q_base)
-    const int h = (int)(hq_rel / a.kc.q_span);
-    const int64_t q = a.kc.q_base + (hq_rel - (int64_t)h * a.kc.q_span);
+    const int64_t hq_rel = it / per_q;  // (h - h_base) * q_span + (q - q_base)
+    const int hr = (int)(hq_rel / a.kc.q_span);
+    const int h = a.kc.h_base + hr;
+    const int64_t q = a.kc.q_base + (hq_rel - (int64_t)hr * a.kc.q_span);
     const int64_t hq_idx = (int64_t)h * a.nq + q;
     if (!a.kc.qmark[hq_idx]) continue;
     const int sub = (int)(it - hq_rel * per_q);

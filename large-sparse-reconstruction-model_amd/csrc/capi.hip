@@ -127,7 +127,7 @@ int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
     rc = build_reverse_map(topk, hkv, nq, topk_n, cu_q, batch, cu_sb, nb, false, nullptr,
                            ws, kc.grev, st, kc.qmark, true);
     if (rc) return rc;
-    kc_passes(nq, hkv, topk_n, g, head_dim, &kc.n_pass, &kc.q_span_max);
+    kc_passes(nq, hkv, topk_n, g, head_dim, &kc.n_pass, &kc.pass_heads, &kc.q_span_max);
     rc = build_kc_items(kc.grev, cu_blk, nk, hkv, nb, tq, head_dim, topk_n, ws, kc,
                         w.plan.counter, kc_plan_marker(flags, (int)head_dim), st);
     if (rc) return rc;
@@ -135,7 +135,8 @@ int attn_plan(Carver& ws, const int32_t* topk, int64_t nq, int64_t nk,
       rc = derive_query_map(kc.grev, w.qrev, hkv, nb, topk_n, st);
       if (rc) return rc;
     }
-    const size_t parts = (size_t)(hkv * kc.q_span_max * topk_n * g);
+    const size_t parts =
+        (size_t)((kc.pass_heads > 0 ? kc.pass_heads : hkv) * kc.q_span_max * topk_n * g);
     kc.part_o = ws.take<uint16_t>(parts * (size_t)(head_dim > 0 ? head_dim : 1));
     kc.part_lse = ws.take<float>(parts);
     if (ws.base && !ws.ok()) return LSRM_ERR_WORKSPACE;

@@ -73,12 +73,14 @@ int mark_grouped_queries(const TilePlan& plan, int64_t hkv, int64_t nq,
 // type and its log2 LSE -- and the dQ pass the slot's share of dQ; merge
 // passes combine each query's partials in slot order.
 //
-// The partial buffer holds the queries of one pass: queries are taken in
-// n_pass ranges of q_span_max consecutive queries (sized so that a pass's
-// partials stay within KC_PART_BUDGET bytes), each range's gathered tiles
-// run and merge before the next range reuses the buffer.  Items never
-// straddle a range, and the item lists are stored per (pass, kv head):
-// entry (p, h) of a list is "head" p * hkv + h.
+// The partial buffer holds the rows of one pass, sized so that a pass's
+// partials stay within KC_PART_BUDGET bytes: when one kv head's partials
+// fit, pass p takes kv heads [p * pass_heads, (p + 1) * pass_heads) with all
+// their queries (every block's listings stay in one pass); otherwise pass p
+// takes queries [p * q_span_max, (p + 1) * q_span_max) of every head (items
+// are then cut at the range's bounds).  Each pass's gathered tiles run and
+// merge before the next pass reuses the buffer.  The item lists are stored
+// per (pass, kv head): entry (p, h) of a list is "head" p * hkv + h.
 struct KcPlan {
   uint8_t* qmark;        // [hkv, n_q] queries of grouped tiles
   RevMap grev;           // block -> marked queries, cap = n_q * topk per head
@@ -86,10 +88,12 @@ struct KcPlan {
   float* part_lse;       // [hkv, q_span_max, topk, g]
   int n_pass;
   int64_t q_span_max;
+  int pass_heads;  // kv heads per pass (head passes), 0 for query passes
   // the pass a launch works on (set by the launcher): queries
-  // [q_base, q_base + q_span); the item lists below then point at that
-  // pass's entries
+  // [q_base, q_base + q_span) of kv heads [h_base, h_base + h_count); the
+  // item lists below then point at that pass's entries
   int64_t q_base, q_span;
+  int h_base, h_count;
   // Items of blocks with 1..KC_RES_KEYS keys, run with the block resident
   // in LDS (forward and dQ): up to KC_RES_CHUNKS * tq listings each.
   int4* ritems;          // [n_pass * hkv, ritem_cap]
@@ -113,8 +117,17 @@ struct KcPlan {
   // The plan's pass p: the item lists of that pass and its query range.
   __host__ __device__ KcPlan pass(int p, int64_t hkv, int64_t n_q) const {
     KcPlan k = *this;
-    k.q_base = p * q_span_max;
-    k.q_span = n_q - k.q_base < q_span_max ? n_q - k.q_base : q_span_max;
+    if (pass_heads > 0) {
+      k.h_base = p * pass_heads;
+      k.h_count = (int)(hkv - k.h_base < pass_heads ? hkv - k.h_base : pass_heads);
+      k.q_base = 0;
+      k.q_span = n_q;
+    } else {
+      k.h_base = 0;
+      k.h_count = (int)hkv;
+      k.q_base = p * q_span_max;
+      k.q_span = n_q - k.q_base < q_span_max ? n_q - k.q_base : q_span_max;
+    }
     k.ritems = ritems + p * hkv * ritem_cap;
     k.ritem_off = ritem_off + p * (hkv + 1);
     k.r2items = r2items + p * hkv * r2item_cap;
@@ -126,7 +139,7 @@ struct KcPlan {
   // Index of the partial of (kv head h, query q of this pass, slot, query
   // head gi of the group) in part_lse (times D in part_o).
   __device__ int64_t pidx(int h, int64_t q, int64_t slot, int topk, int g, int gi) const {
-    return (((int64_t)h * q_span + (q - q_base)) * topk + slot) * g + gi;
+    return (((int64_t)(h - h_base) * q_span + (q - q_base)) * topk + slot) * g + gi;
   }
 };
 // Bytes of key-centric partial results one pass may hold.
@@ -156,10 +169,10 @@ __host__ __device__ constexpr int32_t kc_plan_marker(int flags, int head_dim) {
 // blocks, counts and order: the map of the same queries without slots).
 int derive_query_map(const RevMap& enc, const RevMap& plain, int64_t hkv, int64_t nb,
                      int64_t topk_n, hipStream_t st);
-// Passes of a key-centric plan: (n_pass, queries per pass) so that one
-// pass's partials fit KC_PART_BUDGET.
+// Passes of a key-centric plan so that one pass's partials fit
+// KC_PART_BUDGET: kv heads per pass (0: query ranges), queries per pass.
 void kc_passes(int64_t n_q, int64_t hkv, int64_t topk, int g, int64_t head_dim, int* n_pass,
-               int64_t* q_span);
+               int* pass_heads, int64_t* q_span);
 int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
                    int64_t nb, int tq, int64_t head_dim, int64_t topk_n, Carver& ws,
                    KcPlan& kc, int32_t* counter, int32_t marker, hipStream_t st);

@@ -825,13 +825,15 @@ struct KcPassRange {
   const int32_t* rev;
   int64_t nb, cap;
   int hkv;
-  int64_t pass_listings;  // pq * topk; 0 = one pass
+  int64_t pass_listings;  // query passes: pq * topk; 0 = no query cut
+  int pass_heads;         // head passes: kv heads per pass; 0 = none
   __device__ void operator()(int vs, int64_t c, int64_t& s, int64_t& e) const {
     const int p = vs / hkv, h = vs - p * hkv;
     const int32_t* cr = cu_rev + (int64_t)h * (nb + 1);
     s = cr[c];
     e = cr[c + 1];
     e = e < cap ? e : cap;
+    if (pass_heads > 0 && h / pass_heads != p) e = s;  // another pass's head
     if (pass_listings == 0 || e <= s) return;
     const int32_t* r = rev + (int64_t)h * cap;
     auto first_at = [&](int64_t x) {  // first i in [s, e) with r[i] >= x
@@ -950,13 +952,26 @@ __global__ void kc_offsets_kernel(KcCounts c, int hkv, int n_pass, int32_t* coun
 }
 
 void kc_passes(int64_t n_q, int64_t hkv, int64_t topk, int g, int64_t head_dim, int* n_pass,
-               int64_t* q_span) {
-  const int64_t per_q = hkv * topk * g * (2 * (head_dim > 0 ? head_dim : 1) + 4);
-  int64_t span = per_q > 0 ? KC_PART_BUDGET / per_q : n_q;
+               int* pass_heads, int64_t* q_span) {
+  const int64_t nq = n_q > 0 ? n_q : 1;
+  const int64_t per_row = topk * g * (2 * (head_dim > 0 ? head_dim : 1) + 4);
+  const int64_t per_head = nq * per_row;
+  if (per_head * hkv <= KC_PART_BUDGET || per_head <= KC_PART_BUDGET) {
+    // whole kv heads per pass (one pass when everything fits)
+    int64_t hp = KC_PART_BUDGET / per_head;
+    hp = hp < 1 ? 1 : (hp > hkv ? hkv : hp);
+    *pass_heads = hkv > 1 && hp < hkv ? (int)hp : 0;
+    *q_span = nq;
+    *n_pass = (int)((hkv + hp - 1) / hp);
+    if (*pass_heads == 0) *n_pass = 1;
+    return;
+  }
+  int64_t span = KC_PART_BUDGET / (hkv * per_row);
   if (span < 1) span = 1;
-  if (span >= n_q) span = n_q > 0 ? n_q : 1;
+  if (span >= nq) span = nq;
+  *pass_heads = 0;
   *q_span = span;
-  *n_pass = (int)((n_q + span - 1) / span > 0 ? (n_q + span - 1) / span : 1);
+  *n_pass = (int)((nq + span - 1) / span);
 }
 
 int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_t hkv,
@@ -966,7 +981,7 @@ int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_
   const int res_max = kc_res_max((int)(head_dim > 0 ? head_dim : 1));
   const int np = kc.n_pass > 0 ? kc.n_pass : 1;
   // listings of one (pass, head): at most the pass's queries times topk
-  const int64_t lst = np > 1 ? kc.q_span_max * topk_n : grev.cap;
+  const int64_t lst = (np > 1 && kc.pass_heads == 0) ? kc.q_span_max * topk_n : grev.cap;
   kc.ritem_cap = lst / (rq > 0 ? rq : 1) + nb + 1;
   kc.ritems = ws.take<int4>((size_t)(np * hkv * kc.ritem_cap));
   kc.ritem_count = ws.take<int32_t>((size_t)(np * hkv));
@@ -987,7 +1002,8 @@ int build_kc_items(const RevMap& grev, const int32_t* cu_blk, int64_t nk, int64_
     if (rc) return rc;
   }
   const KcPassRange rg{grev.cu_rev, grev.rev, nb, grev.cap, (int)hkv,
-                       np > 1 ? kc.q_span_max * topk_n : 0};
+                       (np > 1 && kc.pass_heads == 0) ? kc.q_span_max * topk_n : 0,
+                       kc.pass_heads};
   const int nseg = (int)(np * hkv);
   int rc = run_scan(KcItemsF{rg, rq, cu_blk, nk, 0, KC_RES_KEYS, false},
                     KcItemsW{rg, rq, kc.ritems, kc.ritem_cap}, nb, nseg, sums, kc.ritem_count,
