@@ -475,6 +475,13 @@ __device__ inline uint32_t lds_addr(const void* p) {
   return (uint32_t)(size_t)((__attribute__((address_space(3))) const char*)p);
 }
 
+// LDS pointer of byte address a (the inverse of lds_addr); used for reads
+// (the transposed-read builtin takes a non-const pointer).
+template <typename T>
+__device__ inline __attribute__((address_space(3))) T* lds_ptr(uint32_t a) {
+  return reinterpret_cast<__attribute__((address_space(3))) T*>((size_t)a);
+}
+
 // One 16-byte-per-lane global -> LDS copy: lane l's bytes base + voff land at
 // LDS address lds + 16 * l.  Issued as inline assembly so that the compiler
 // does not order every later LDS read behind it (it cannot tell which LDS

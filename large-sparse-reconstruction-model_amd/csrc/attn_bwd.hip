@@ -515,6 +515,23 @@ sel_attn_dkdv_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
   static_assert(KEY_CHUNK == 4 * 32, "four waves of 32 keys cover a chunk");
+  // Lane-dependent parts of the Q / dO tile reads (the tile row's high bits
+  // do not enter the swizzle): row-major reads of head-dim step sk, and the
+  // two transposed reads (rows k0, k0 + 8) of output block db.
+  uint32_t kl_off[NS], vl_off[ND][2];
+  {
+    const int gi = lane & 15, dh = (lane >> 4) & 1;
+#pragma unroll
+    for (int sk = 0; sk < NS; ++sk) kl_off[sk] = (uint32_t)G::off(l32, 2 * sk + hb);
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+      const int k0 = hb * 4 + (gi >> 2);
+      const int cb = dcol >> 3, half = (dcol & 4) * 2;
+      vl_off[db][0] = (uint32_t)(G::off(k0, cb) + half);
+      vl_off[db][1] = (uint32_t)(G::off(k0 + 8, cb) + half);
+    }
+  }
   // A plan built without its backward part: no reverse maps or key chunks.
   if (a.plan.counter[PLAN_BWD_SLOT] != PLAN_BWD_MAGIC) return;
   const int n_items = a.items.n_items[0];
@@ -815,8 +832,28 @@ sel_attn_dkdv_kernel(AttnArgs a) {
         // slots.
         // dS is kept unscaled (dK is scaled once at the end).
         constexpr int NA = 2 * NS, NC = 4 * ND, NSLOT = 2 * NA + 2 * NC, LA = 2;
-        const int gi = lane & 15, dh = (lane >> 4) & 1;
         f32x16 sc[2], dp[2];
+        // Per-lane LDS addresses of this row half's reads (ring slot and row
+        // half added once; row block, 16-row half and transposed-row offsets
+        // are immediates): row-major Q / dO rows of head-dim step sk, and
+        // transposed Q / dO reads (rows r0, r0 + 8) of output block db.
+        const uint32_t qh = lds_addr(qs) + (uint32_t)(rh * 64 * (D * 2));
+        const uint32_t oh = lds_addr(os) + (uint32_t)(rh * 64 * (D * 2));
+        uint32_t rq[NS], ro[NS], tq[ND][2], to[ND][2];
+#pragma unroll
+        for (int sk = 0; sk < NS; ++sk) {
+          rq[sk] = qh + kl_off[sk];
+          ro[sk] = oh + kl_off[sk];
+          asm volatile("" : "+v"(rq[sk]), "+v"(ro[sk]));
+        }
+#pragma unroll
+        for (int db = 0; db < ND; ++db)
+#pragma unroll
+          for (int x = 0; x < 2; ++x) {
+            tq[db][x] = qh + vl_off[db][x];
+            to[db][x] = oh + vl_off[db][x];
+            asm volatile("" : "+v"(tq[db][x]), "+v"(to[db][x]));
+          }
         u32x4 pb[2][2], dsb[2][2];
         f32x4 lv[2][4], dl[2][4];
         u32x4 opnd[LA + 1];
@@ -826,20 +863,17 @@ sel_attn_dkdv_kernel(AttnArgs a) {
         auto read_op = [&](int i) __attribute__((always_inline)) {
           if (i < 2 * NA) {
             const int rb = i / NA, j = i % NA, sk = j >> 1;
-            const char* src = (j & 1) ? os : qs;
-            opnd[i % (LA + 1)] = *reinterpret_cast<const u32x4*>(
-                src + G::off(rh * 64 + rb * 32 + l32, 2 * sk + hb));
+            const uint32_t ad = ((j & 1) ? ro[sk] : rq[sk]) + rb * 32 * (D * 2);
+            opnd[i % (LA + 1)] = *lds_ptr<u32x4>(ad);
           } else {
             const int j = (i - 2 * NA) % NC, rb = (i - 2 * NA) / NC;
             const int db = j >> 2, cc = (j >> 1) & 1;
-            const char* src = (j & 1) ? qs : os;
-            const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
-            const int cb = dcol >> 3, half = (dcol & 4) * 2;
-            const int r0 = rh * 64 + rb * 32 + cc * 16 + hb * 4 + (gi >> 2);
+            const uint32_t (*t)[2] = (j & 1) ? tq : to;
+            const uint32_t rbc = (uint32_t)((rb * 32 + cc * 16) * (D * 2));
             const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_s16x4*)(src + G::off(r0, cb) + half)));
+                lds_ptr<s16x4>(t[db][0] + rbc)));
             const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_s16x4*)(src + G::off(r0 + 8, cb) + half)));
+                lds_ptr<s16x4>(t[db][1] + rbc)));
             opnd[i % (LA + 1)] = u32x4{lo[0], lo[1], hi[0], hi[1]};
           }
         };

@@ -196,6 +196,29 @@ sel_attn_fwd_kernel(AttnArgs a) {
 
     const char* kbase = reinterpret_cast<const char*>(a.k + (int64_t)h * D);
     const char* vbase = reinterpret_cast<const char*>(a.v + (int64_t)h * D);
+    // The lane-dependent parts of the LDS operand addresses (the 32-key
+    // block, 16-key half and ring slot are compile-time offsets): the K row
+    // block read of head-dim step s, and the two transposed V reads (rows
+    // k0, k0 + 8) of output block db.  Pinned in registers so the reads
+    // take them as base plus an immediate offset.
+    uint32_t kl_off[NS], vl_off[ND][2];
+    {
+      const int gi = lane & 15, dh = (lane >> 4) & 1;
+#pragma unroll
+      for (int s2 = 0; s2 < NS; ++s2) {
+        kl_off[s2] = (uint32_t)G::off(l32, 2 * s2 + hb);
+        asm volatile("" : "+v"(kl_off[s2]));
+      }
+#pragma unroll
+      for (int db = 0; db < ND; ++db) {
+        const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+        const int k0 = hb * 4 + (gi >> 2);
+        const int cb = dcol >> 3, half = (dcol & 4) * 2;
+        vl_off[db][0] = (uint32_t)(G::off(k0, cb) + half);
+        vl_off[db][1] = (uint32_t)(G::off(k0 + 8, cb) + half);
+        asm volatile("" : "+v"(vl_off[db][0]), "+v"(vl_off[db][1]));
+      }
+    }
 
     // Scalar cursors of the K copies (three tiles ahead, one per load
     // group); the V copies (two tiles ahead) reuse the K offsets of the
@@ -389,16 +412,16 @@ sel_attn_fwd_kernel(AttnArgs a) {
         const int x = idx_of(i);
         if (kind_of(i) == 0) {
           const int blk = x & 1, s = x >> 1;
-          dst = *reinterpret_cast<const u32x4*>(ks + G::off(blk * 32 + l32, 2 * s + hb));
+          // row blk * 32 + l32: the swizzle sees only l32's low bits
+          dst = *reinterpret_cast<const u32x4*>(ks + blk * 32 * (D * 2) + kl_off[s]);
         } else {
           const int db = x % ND, bc = x / ND, blk = bc >> 1, c = bc & 1;
-          const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
-          const int k0 = blk * 32 + c * 16 + hb * 4 + (gi >> 2);
-          const int cb = dcol >> 3, half = (dcol & 4) * 2;
+          // rows blk * 32 + c * 16 + k0 (+ 8): the swizzle sees only k0's bits
+          const int rb = (blk * 32 + c * 16) * (D * 2);
           const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4*)(vs + G::off(k0, cb) + half));
+              (lds_s16x4*)(vs + rb + vl_off[db][0]));
           const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4*)(vs + G::off(k0 + 8, cb) + half));
+              (lds_s16x4*)(vs + rb + vl_off[db][1]));
           const u32x2 lw = __builtin_bit_cast(u32x2, lo);
           const u32x2 hw = __builtin_bit_cast(u32x2, hi);
           dst = u32x4{lw[0], lw[1], hw[0], hw[1]};
@@ -675,6 +698,27 @@ kc_resident_fwd_kernel(AttnArgs a) {
   const uint32_t row_bytes = (uint32_t)a.hkv * D * 2;
   const int tq = ROWS / a.g;
   const int64_t cap = a.kc.grev.cap;
+  // Lane-dependent parts of the LDS operand addresses (see the streaming
+  // kernel), pinned in registers: K row block reads per head-dim step,
+  // transposed V reads (rows k0, k0 + 8) per output block.
+  uint32_t kl_off[NS], vl_off[ND][2];
+  {
+    const int gi = lane & 15, dh = (lane >> 4) & 1;
+#pragma unroll
+    for (int s2 = 0; s2 < NS; ++s2) {
+      kl_off[s2] = (uint32_t)G::off(l32, 2 * s2 + hb);
+      asm volatile("" : "+v"(kl_off[s2]));
+    }
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+      const int k0 = hb * 4 + (gi >> 2);
+      const int cb = dcol >> 3, half = (dcol & 4) * 2;
+      vl_off[db][0] = (uint32_t)(G::off(k0, cb) + half);
+      vl_off[db][1] = (uint32_t)(G::off(k0 + 8, cb) + half);
+      asm volatile("" : "+v"(vl_off[db][0]), "+v"(vl_off[db][1]));
+    }
+  }
 
   for (;;) {
     const int w = uniform(fetch_work(queue, &s_slot));
@@ -776,7 +820,7 @@ kc_resident_fwd_kernel(AttnArgs a) {
 #pragma unroll
                 for (int s = 0; s < NS; ++s) {
                   const u32x4 ka = *reinterpret_cast<const u32x4*>(
-                      sK[kt] + G::off(blk * 32 + l32, 2 * s + hb));
+                      sK[kt] + blk * 32 * (D * 2) + kl_off[s]);
                   sc[t4][blk] = mfma32<DT>(ka, qb[s], sc[t4][blk]);
                 }
               }
@@ -838,22 +882,19 @@ kc_resident_fwd_kernel(AttnArgs a) {
                 for (int e = 0; e < 4; ++e) l_run = sum2<DT>(pb[blk][cc][e], l_run);
               }
             }
-            const int gi = lane & 15, dh = (lane >> 4) & 1;
             const int nblk = kt * KT + 32 < len ? 2 : 1;  // halves holding keys (P = 0 past)
 #pragma unroll
             for (int db = 0; db < ND; ++db) {
-              const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
 #pragma unroll
               for (int blk = 0; blk < 2; ++blk)
                 if (blk < nblk)
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {
-                  const int k0 = blk * 32 + cc * 16 + hb * 4 + (gi >> 2);
-                  const int cbk = dcol >> 3, half = (dcol & 4) * 2;
+                  const int rb = (blk * 32 + cc * 16) * (D * 2);
                   const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                      (lds_s16x4*)(sV[kt] + G::off(k0, cbk) + half));
+                      (lds_s16x4*)(sV[kt] + rb + vl_off[db][0]));
                   const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                      (lds_s16x4*)(sV[kt] + G::off(k0 + 8, cbk) + half));
+                      (lds_s16x4*)(sV[kt] + rb + vl_off[db][1]));
                   const u32x2 lw = __builtin_bit_cast(u32x2, lo);
                   const u32x2 hw = __builtin_bit_cast(u32x2, hi);
                   oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]}, pb[blk][cc], oacc[db]);
