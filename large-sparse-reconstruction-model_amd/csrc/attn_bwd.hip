@@ -82,6 +82,28 @@ sel_attn_dq_kernel(AttnArgs a) {
     ld_byte[j] = (((lane % G::CH) ^ G::swz(ld_key[j])) << 4);
   }
   const uint32_t row_bytes = (uint32_t)a.hkv * D * 2;
+  // Per-lane LDS offsets of the operand reads, fixed for the kernel (the
+  // swizzle repeats every 16 rows, so a 16- or 32-key block adds a constant
+  // that folds into the read's immediate): row-major K / V rows of head-dim
+  // step s, and the transposed K reads (rows k0, k0 + 8) of output block db.
+  uint32_t kl_off[NS], vl_off[ND][2];
+  {
+    const int gi = lane & 15, dh = (lane >> 4) & 1;
+#pragma unroll
+    for (int s2 = 0; s2 < NS; ++s2) {
+      kl_off[s2] = (uint32_t)G::off(l32, 2 * s2 + hb);
+      asm volatile("" : "+v"(kl_off[s2]));
+    }
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+      const int cb = dcol >> 3, half = (dcol & 4) * 2;
+      const int k0 = hb * 4 + (gi >> 2);
+      vl_off[db][0] = (uint32_t)(G::off(k0, cb) + half);
+      vl_off[db][1] = (uint32_t)(G::off(k0 + 8, cb) + half);
+      asm volatile("" : "+v"(vl_off[db][0]), "+v"(vl_off[db][1]));
+    }
+  }
 
   for (;;) {
     const int w = uniform(fetch_work(queue, &s_slot));
@@ -293,7 +315,6 @@ sel_attn_dq_kernel(AttnArgs a) {
         // MFMA, then its share of the vector work; scheduling barriers keep
         // the order.  dS is kept unscaled (dQ is scaled once at the end).
         constexpr int NA = 2 * NS, NC = 2 * ND, NSLOT = 2 * NA + 2 * NC, LA = 2;
-        const int gi = lane & 15, dh = (lane >> 4) & 1;
         f32x16 sc[2], dp[2];
         u32x4 dsb[2][2];
         u32x4 opnd[LA + 1];
@@ -305,17 +326,15 @@ sel_attn_dq_kernel(AttnArgs a) {
             const int blk = i / NA, j = i % NA, sk = j >> 1;
             const char* src = (j & 1) ? vs : ks;
             opnd[i % (LA + 1)] =
-                *reinterpret_cast<const u32x4*>(src + G::off(blk * 32 + l32, 2 * sk + hb));
+                *reinterpret_cast<const u32x4*>(src + blk * 32 * (D * 2) + kl_off[sk]);
           } else {
             const int j = (i - 2 * NA) % NC, blk = (i - 2 * NA) / NC;
             const int db = j >> 1, c = j & 1;
-            const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
-            const int cb = dcol >> 3, half = (dcol & 4) * 2;
-            const int k0 = blk * 32 + c * 16 + hb * 4 + (gi >> 2);
+            const int rb = (blk * 32 + c * 16) * (D * 2);
             const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_s16x4*)(ks + G::off(k0, cb) + half)));
+                (lds_s16x4*)(ks + rb + vl_off[db][0])));
             const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_s16x4*)(ks + G::off(k0 + 8, cb) + half)));
+                (lds_s16x4*)(ks + rb + vl_off[db][1])));
             opnd[i % (LA + 1)] = u32x4{lo[0], lo[1], hi[0], hi[1]};
           }
         };
