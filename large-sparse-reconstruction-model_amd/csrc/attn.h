@@ -9,6 +9,8 @@
 // last key tile of a query tile is partial.
 #pragma once
 
+#include <mutex>
+
 #include "common.h"
 #include "plan.h"
 
@@ -461,6 +463,22 @@ __device__ inline int head_of(const int32_t* head_off, int hkv, int w) {
 
 // Persistent-grid size for a kernel: CUs x resident workgroups per CU.
 int persistent_grid(const void* kernel, int block, size_t dyn_lds);
+
+// A second stream of the current device (created on first use, default
+// priority, non-blocking) with a fork and a join event, for launch sequences
+// that put independent kernels on two streams: record `fork` on the caller's
+// stream and make `s` wait for it, launch, then record `join` on `s` and make
+// the caller's stream wait for it.  The events are shared per device, so such
+// a sequence holds `*m` from its first fork to its last join.
+struct SideStream {
+  hipStream_t s;
+  hipEvent_t fork, join;
+  std::mutex* m;
+};
+int side_stream(SideStream& out);
+// True when `st` is capturing a graph (or the query fails): launch sequences
+// then stay on `st`.
+bool stream_capturing(hipStream_t st);
 
 // ------------------------------------------------ LDS tile streaming --
 // Shared by the forward and backward kernels: 16-byte global -> LDS copies,

@@ -1385,20 +1385,33 @@ int launch_bwd_t(const AttnArgs& a, hipStream_t st) {
                             512, 0);
     const int gm = device_cu_count() * 16;
     if (grid <= 0 || gr <= 0 || gr2 <= 0 || gm <= 0) return LSRM_ERR_LAUNCH;
-    // one range of queries at a time: its gathered dQ shares, then their
-    // merge, before the next range reuses the partial buffer
+    // One range of queries at a time: its gathered dQ shares, then their
+    // merge, before the next range reuses the partial buffer; the streaming
+    // and eight-wave kernels run on a second stream beside the four-wave one
+    // (disjoint partials), as in the forward.
+    SideStream ss{};
+    const bool two = !stream_capturing(st) && side_stream(ss) == LSRM_OK;
+    std::unique_lock<std::mutex> seq;
+    if (two) seq = std::unique_lock<std::mutex>(*ss.m);
+    hipStream_t s2 = two ? ss.s : st;
     for (int p = 0; p < a.kc.n_pass; ++p) {
       AttnArgs ap = a;
       ap.kc = a.kc.pass(p, a.hkv, a.nq);
+      if (two && (hipEventRecord(ss.fork, st) != hipSuccess ||
+                  hipStreamWaitEvent(ss.s, ss.fork, 0) != hipSuccess))
+        return LSRM_ERR_LAUNCH;
+      if constexpr (kc_res_max(D) > KC_RES_KEYS) {
+        hipLaunchKernelGGL((kc_resident_dq_kernel<DT, D, 1>), dim3(gr2), dim3(512), 0, s2, ap);
+        LSRM_CHECK_LAUNCH();
+      }
       hipLaunchKernelGGL((sel_attn_dq_kernel<DT, D, DQ_GATHER>), dim3(grid), dim3(256), 0,
-                         st, ap);
+                         s2, ap);
       LSRM_CHECK_LAUNCH();
       hipLaunchKernelGGL((kc_resident_dq_kernel<DT, D, 0>), dim3(gr), dim3(256), 0, st, ap);
       LSRM_CHECK_LAUNCH();
-      if constexpr (kc_res_max(D) > KC_RES_KEYS) {
-        hipLaunchKernelGGL((kc_resident_dq_kernel<DT, D, 1>), dim3(gr2), dim3(512), 0, st, ap);
-        LSRM_CHECK_LAUNCH();
-      }
+      if (two && (hipEventRecord(ss.join, ss.s) != hipSuccess ||
+                  hipStreamWaitEvent(st, ss.join, 0) != hipSuccess))
+        return LSRM_ERR_LAUNCH;
       hipLaunchKernelGGL((kc_dq_merge_kernel<DT, D>), dim3(gm), dim3(256), 0, st, ap);
       LSRM_CHECK_LAUNCH();
     }

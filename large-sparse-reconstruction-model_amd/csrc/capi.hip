@@ -25,6 +25,40 @@ int device_cu_count() {
   return cache[dev];
 }
 
+int side_stream(SideStream& out) {
+  static std::mutex mu;
+  static std::mutex seq[64];
+  static hipStream_t streams[64];
+  static hipEvent_t forks[64], joins[64];
+  static bool made[64] = {false};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return LSRM_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!made[dev]) {
+    hipStream_t s = nullptr;
+    hipEvent_t f = nullptr, j = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return LSRM_ERR_LAUNCH;
+    if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+      if (f) (void)hipEventDestroy(f);
+      (void)hipStreamDestroy(s);
+      return LSRM_ERR_LAUNCH;
+    }
+    streams[dev] = s;
+    forks[dev] = f;
+    joins[dev] = j;
+    made[dev] = true;
+  }
+  out = SideStream{streams[dev], forks[dev], joins[dev], &seq[dev]};
+  return LSRM_OK;
+}
+
+bool stream_capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) return true;
+  return cs != hipStreamCaptureStatusNone;
+}
+
 int persistent_grid(const void* kernel, int block, size_t dyn_lds) {
   static std::mutex mu;
   struct Entry {
