@@ -56,7 +56,10 @@ def _use_key_centric(q, k, topk_idx) -> bool:
     """The key-centric choice for this selection (see set_key_centric)."""
     if _key_centric != "auto":
         return bool(_key_centric)
-    if topk_idx.shape[1] < 2 or torch.compiler.is_compiling():
+    # Under graph capture or compilation the count cannot be read back (and a
+    # key-centric plan is not built under capture): the grouped-tile plan.
+    if topk_idx.shape[1] < 2 or torch.compiler.is_compiling() or \
+            (topk_idx.is_cuda and torch.cuda.is_current_stream_capturing()):
         return False
     # The plan groups runs shorter than a quarter of a 128-row tile's
     # queries; the key-centric part pays off when such runs dominate.

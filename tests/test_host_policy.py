@@ -47,3 +47,23 @@ def test_explicit_key_centric_settings():
         assert not nsa._use_key_centric(q, k, torch.arange(64, dtype=torch.int32).view(2, 8, 4))
     finally:
         ops.set_key_centric("auto")
+
+
+def test_plan_cache_key_tracks_the_selection():
+    # A cached plan is reused only for the same selection tensors, unchanged
+    # since the plan was built (same storage, same version counter).
+    import lsrm_hip as H
+    rows = torch.zeros(2, 16, 4, dtype=torch.int32)
+    cu_sb = torch.tensor([0, 4], dtype=torch.int32)
+    cu_blk = torch.tensor([0, 4, 8, 12, 16], dtype=torch.int32)
+    cu_q = torch.tensor([0, 16], dtype=torch.int32)
+    key = lambda r, kc=False: H._plan_key((16, 2, 8), (16, 2, 8), r, cu_sb, cu_blk, cu_q, kc)
+    k0 = key(rows)
+    assert key(rows) == k0
+    assert key(rows, True) != k0                      # another plan kind
+    assert key(rows.clone()) != k0                    # same values, other storage
+    rows[0, 0, 0] = 1                                 # in-place change of the selection
+    assert key(rows) != k0
+    k1 = key(rows)
+    cu_blk[1] = 3                                     # in-place change of the metadata
+    assert key(rows) != k1
