@@ -64,13 +64,15 @@ def test_pool_matches_segment_reduce_and_empty_block():
     torch.testing.assert_close(out[keep], ref[keep], rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize("c", [512, 1024])
+@pytest.mark.parametrize("c", [512, 1024, 1536, 3072])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("out_dtype", [None, torch.float32])
 @pytest.mark.parametrize("n_blocks", [300, 800])
 def test_pool_slab_path_small_and_empty_blocks(c, dtype, out_dtype, n_blocks):
-    # Channel counts that are multiples of 512 take the slab kernel (with the
-    # in-kernel block lookup below 512 blocks, the lookup table above).
+    # Channel counts that are multiples of 512 take the 16-bit piece kernels:
+    # one 512-channel slab per wave (512), two (1024), three (1536: whole
+    # rows; 3072: two waves per chunk), with the in-kernel block lookup below
+    # 512 blocks and the lookup table above.
     # Blocks of length 0..40 put several block boundaries (and empty blocks,
     # whose mean is NaN) inside one 64-row piece; rows before the first and
     # after the last block are ignored.
@@ -94,7 +96,9 @@ def test_pool_slab_path_small_and_empty_blocks(c, dtype, out_dtype, n_blocks):
 
 @pytest.mark.parametrize("c,n_blocks,out_a,out_b", [
     (512, 300, torch.float32, None),      # slab path, in-kernel block lookup
-    (1024, 800, None, torch.float32),     # slab path, lookup table
+    (1024, 800, None, torch.float32),     # two slabs per wave, lookup table
+    (1536, 300, torch.float32, None),     # whole rows per wave, in-kernel lookup
+    (3072, 800, None, torch.float32),     # three slabs per wave, lookup table
     (256, 300, torch.float32, None),      # single-tensor fallback (C % 512 != 0)
 ])
 def test_pool2_equals_oracle_and_single_calls(c, n_blocks, out_a, out_b):
