@@ -794,113 +794,234 @@ kc_resident_fwd_kernel(AttnArgs a) {
       lv_next = load_listing(cb + 2 * step);
       if (wl * 32 >= rows) continue;  // wave-uniform: no row of this chunk
       f32x16 oacc[ND];
+      float m_run = 0.0f, l_run = 0.0f;
+      // Fast pass over the resident tiles, as the streaming kernel's: the
+      // reference is tile 0's row maximum (tile 0 holds a key, so it is
+      // finite) and stays fixed; step t issues the score MFMAs of tile t+1 and
+      // the P.V MFMAs of tile t-1, alternating, beside the softmax of tile t,
+      // with each MFMA's LDS operand read two slots ahead.
+      {
 #pragma unroll
-      for (int i = 0; i < ND; ++i)
+        for (int i = 0; i < ND; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
-      float m_run = -__builtin_inf();
-      float l_run = 0.0f;
-#pragma unroll
-      for (int kb = 0; kb < NT; kb += 4) {
-        if (kb >= ntiles) break;  // uniform
-        // Phase 1: the scores of the group's tiles, keys past the block
-        // masked, and the exact row maximum.
-        f32x16 sc[4][2];
-        float mx = -__builtin_inf();
-#pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) {
-          const int kt = kb + t4;
-          if (kt < ntiles) {
-#pragma unroll
-            for (int blk = 0; blk < 2; ++blk) {
-#pragma unroll
-              for (int v = 0; v < 16; ++v) sc[t4][blk][v] = 0.0f;
-              // a 32-key half past the block's end stays all masked
-              if (kt * KT + blk * 32 < len) {
-#pragma unroll
-                for (int s = 0; s < NS; ++s) {
-                  const u32x4 ka = *reinterpret_cast<const u32x4*>(
-                      sK[kt] + blk * 32 * (D * 2) + kl_off[s]);
-                  sc[t4][blk] = mfma32<DT>(ka, qb[s], sc[t4][blk]);
-                }
-              }
-            }
-            if (kt * KT + KT > len) {
-#pragma unroll
-              for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-                  if (kt * KT + blk * 32 + acc_row(v, hb) >= len) sc[t4][blk][v] = -__builtin_inf();
-            }
+          for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
+        f32x16 sA[2], sB[2];
+        u32x4 pA[2][2], pB[2][2];
+        auto mask_last = [&](int kt, f32x16* sc) __attribute__((always_inline)) {
+          if (kt * KT + KT > len) {  // uniform: the block's last, partial tile
 #pragma unroll
             for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-              for (int v = 0; v < 16; v += 4)
-                mx = __builtin_elementwise_maximum(
-                    mx, max3f(sc[t4][blk][v], sc[t4][blk][v + 1],
-                              __builtin_elementwise_maximum(sc[t4][blk][v + 2], sc[t4][blk][v + 3])));
+              for (int v = 0; v < 16; ++v)
+                if (kt * KT + blk * 32 + acc_row(v, hb) >= len) sc[blk][v] = -__builtin_inf();
+          }
+        };
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) sA[blk][v] = 0.0f;
+#pragma unroll
+          for (int s2 = 0; s2 < NS; ++s2)
+            sA[blk] = mfma32<DT>(*reinterpret_cast<const u32x4*>(sK[0] + blk * 32 * (D * 2) +
+                                                                 kl_off[s2]),
+                                 qb[s2], sA[blk]);
+        }
+        // keys past the block load its first key, so tile 0's unmasked maximum is the block's
+        m_run = row_max(sA) * a.scale_log2;
+        // One softmax pair (scores 2j, 2j+1 of the lane's 32) against the
+        // reference, packed to the 16-bit type and added to the row sum.
+        auto softmax_pair = [&](const f32x16* sc, u32x4 (*pb)[2], int j, float negm)
+                                __attribute__((always_inline)) {
+          const int blk = j >> 3, c = (j >> 2) & 1, e = j & 3, v0 = c * 8 + 2 * e;
+          const float p0 =
+              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0], a.scale_log2, negm));
+          const float p1 =
+              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0 + 1], a.scale_log2, negm));
+          pb[blk][c][e] = pack2<DT>(p0, p1);
+          l_run = sum2<DT>(pb[blk][c][e], l_run);
+        };
+        // Step body: HS = the step has score MFMAs (a next tile exists), FP =
+        // the step has P.V MFMAs (a previous tile exists).
+        auto body = [&](auto hs, auto fp, const char* ks, const char* vs, const f32x16* sc,
+                        f32x16* sn, const u32x4 (*pp)[2], u32x4 (*pc)[2], float negm)
+                        __attribute__((always_inline)) {
+          constexpr bool HS = decltype(hs)::value != 0;
+          constexpr bool FP = decltype(fp)::value != 0;
+          constexpr int NSM = HS ? 2 * NS : 0;
+          constexpr int NPV = FP ? 4 * ND : 0;
+          constexpr int NSLOT = NSM + NPV;
+          constexpr int NPAIR = 16;
+          constexpr int LA = 2;
+          auto kind_of = [](int i) constexpr {
+            return NPV == 0 ? 0 : (NSM == 0 ? 1 : ((i & 1) == 0 ? 0 : 1));
+          };
+          auto idx_of = [](int i) constexpr { return (NPV == 0 || NSM == 0) ? i : (i >> 1); };
+          auto read_op = [&](int i, u32x4& dst) __attribute__((always_inline)) {
+            const int x = idx_of(i);
+            if (kind_of(i) == 0) {
+              const int blk = x & 1, s2 = x >> 1;
+              dst = *reinterpret_cast<const u32x4*>(ks + blk * 32 * (D * 2) + kl_off[s2]);
+            } else {
+              const int db = x % ND, bc = x / ND, blk = bc >> 1, c = bc & 1;
+              const int rb = (blk * 32 + c * 16) * (D * 2);
+              const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_s16x4*)(vs + rb + vl_off[db][0]));
+              const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_s16x4*)(vs + rb + vl_off[db][1]));
+              const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+              const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+              dst = u32x4{lw[0], lw[1], hw[0], hw[1]};
+            }
+          };
+          if constexpr (NSLOT == 0) {
+#pragma unroll
+            for (int j = 0; j < NPAIR; ++j) softmax_pair(sc, pc, j, negm);
+          } else {
+            u32x4 op[LA + 1];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < LA && i < NSLOT; ++i) read_op(i, op[i % (LA + 1)]);
+#pragma unroll
+            for (int i = 0; i < NSLOT; ++i) {
+              if (i + LA < NSLOT) read_op(i + LA, op[(i + LA) % (LA + 1)]);
+              const int x = idx_of(i);
+              if (kind_of(i) == 0) {
+                const int blk = x & 1, s2 = x >> 1;
+                if (s2 == 0) {
+#pragma unroll
+                  for (int v = 0; v < 16; ++v) sn[blk][v] = 0.0f;
+                }
+                sn[blk] = mfma32<DT>(op[i % (LA + 1)], qb[s2], sn[blk]);
+              } else {
+                const int db = x % ND, bc = x / ND, blk = bc >> 1, c = bc & 1;
+                oacc[db] = mfma32<DT>(op[i % (LA + 1)], pp[blk][c], oacc[db]);
+              }
+#pragma unroll
+              for (int j = (i * NPAIR) / NSLOT; j < ((i + 1) * NPAIR) / NSLOT; ++j)
+                softmax_pair(sc, pc, j, negm);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        };
+        using T1 = std::integral_constant<int, 1>;
+        using T0 = std::integral_constant<int, 0>;
+        const float negm = -m_run;
+        // Steps 0 .. ntiles-1 (ntiles <= NT, unrolled; the score and packed-P
+        // buffers alternate by step parity).
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt) {
+          if (kt < ntiles) {
+            f32x16* sc = (kt & 1) ? sB : sA;
+            f32x16* sn = (kt & 1) ? sA : sB;
+            u32x4 (*pc)[2] = (kt & 1) ? pB : pA;
+            const u32x4 (*pp)[2] = (kt & 1) ? pA : pB;
+            mask_last(kt, sc);
+            const char* vs = sV[kt > 0 ? kt - 1 : 0];
+            if (kt + 1 < ntiles) {
+              const char* ks = sK[kt + 1 < NT ? kt + 1 : 0];
+              if (kt == 0) body(T1{}, T0{}, ks, vs, sc, sn, pp, pc, negm);
+              else body(T1{}, T1{}, ks, vs, sc, sn, pp, pc, negm);
+            } else {
+              if (kt == 0) body(T0{}, T0{}, sK[0], vs, sc, sn, pp, pc, negm);
+              else body(T0{}, T1{}, sK[0], vs, sc, sn, pp, pc, negm);
+            }
           }
         }
+        // P.V of the last tile
         {
-          const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
-                                                           __builtin_bit_cast(unsigned, mx),
-                                                           false, false);
-          mx = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)sw[0]),
-                                             __builtin_bit_cast(float, (unsigned)sw[1]));
+          const int kl = ntiles - 1;
+          const u32x4 (*pl)[2] = (kl & 1) ? pB : pA;
+#pragma unroll
+          for (int db = 0; db < ND; ++db)
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+              for (int cc = 0; cc < 2; ++cc) {
+                const int rb = (blk * 32 + cc * 16) * (D * 2);
+                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(sV[kl] + rb + vl_off[db][0]));
+                const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(sV[kl] + rb + vl_off[db][1]));
+                const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+                const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+                oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]}, pl[blk][cc], oacc[db]);
+              }
         }
-        // The group's first tile holds a key: mx is finite.
-        const float m_new = __builtin_elementwise_maximum(m_run, mx * a.scale_log2);
-        if (kb > 0) {
-          const float al = __builtin_amdgcn_exp2f(m_run - m_new);
+      }
+      // A row sum out of [0, 2^32) (inf and NaN included): the wave reruns its
+      // rows tile by tile with the exact online maximum (O and the row sum
+      // rescaled whenever a tile raises a row's maximum).
+      if (uniform(__builtin_amdgcn_ballot_w64(!(l_run + __shfl_xor(l_run, 32) < 4294967296.0f)) !=
+                  0 ? 1 : 0)) {
+#pragma unroll
+        for (int i = 0; i < ND; ++i)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) oacc[i][v] = 0.0f;
+        m_run = -__builtin_inf();
+        l_run = 0.0f;
+#pragma unroll 1
+        for (int kt = 0; kt < ntiles; ++kt) {
+          const char* ks = sK[0] + kt * G::BYTES;
+          const char* vs = sV[0] + kt * G::BYTES;
+          f32x16 sc[2];
+#pragma unroll
+          for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sc[blk][v] = 0.0f;
+#pragma unroll
+            for (int s2 = 0; s2 < NS; ++s2)
+              sc[blk] = mfma32<DT>(
+                  *reinterpret_cast<const u32x4*>(ks + blk * 32 * (D * 2) + kl_off[s2]), qb[s2],
+                  sc[blk]);
+          }
+          if (kt * KT + KT > len) {
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+              for (int v = 0; v < 16; ++v)
+                if (kt * KT + blk * 32 + acc_row(v, hb) >= len) sc[blk][v] = -__builtin_inf();
+          }
+          // the tile holds a key of the block: its row maximum is finite
+          const float m_new = __builtin_elementwise_maximum(m_run, row_max(sc) * a.scale_log2);
+          const float al = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
           l_run *= al;
 #pragma unroll
           for (int i = 0; i < ND; ++i)
 #pragma unroll
             for (int v = 0; v < 16; ++v) oacc[i][v] *= al;
-        }
-        m_run = m_new;
-        // Phase 2: P = exp2(s * scale * log2(e) - m) rounded to the input
-        // type, row sums, O^T += V^T P^T, tile by tile.
+          m_run = m_new;
+          u32x4 pb[2][2];
 #pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) {
-          const int kt = kb + t4;
-          if (kt < ntiles) {
-            u32x4 pb[2][2];
+          for (int blk = 0; blk < 2; ++blk) {
+            float p[16];
 #pragma unroll
-            for (int blk = 0; blk < 2; ++blk) {
-              float p[16];
+            for (int v = 0; v < 16; ++v)
+              p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v], a.scale_log2, -m_run));
 #pragma unroll
-              for (int v = 0; v < 16; ++v)
-                p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t4][blk][v], a.scale_log2, -m_run));
+            for (int cc = 0; cc < 2; ++cc) {
+              pb[blk][cc] = u32x4{pack2<DT>(p[cc * 8 + 0], p[cc * 8 + 1]),
+                                  pack2<DT>(p[cc * 8 + 2], p[cc * 8 + 3]),
+                                  pack2<DT>(p[cc * 8 + 4], p[cc * 8 + 5]),
+                                  pack2<DT>(p[cc * 8 + 6], p[cc * 8 + 7])};
 #pragma unroll
-              for (int cc = 0; cc < 2; ++cc) {
-                pb[blk][cc] = u32x4{pack2<DT>(p[cc * 8 + 0], p[cc * 8 + 1]),
-                                    pack2<DT>(p[cc * 8 + 2], p[cc * 8 + 3]),
-                                    pack2<DT>(p[cc * 8 + 4], p[cc * 8 + 5]),
-                                    pack2<DT>(p[cc * 8 + 6], p[cc * 8 + 7])};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) l_run = sum2<DT>(pb[blk][cc][e], l_run);
-              }
-            }
-            const int nblk = kt * KT + 32 < len ? 2 : 1;  // halves holding keys (P = 0 past)
-#pragma unroll
-            for (int db = 0; db < ND; ++db) {
-#pragma unroll
-              for (int blk = 0; blk < 2; ++blk)
-                if (blk < nblk)
-#pragma unroll
-                for (int cc = 0; cc < 2; ++cc) {
-                  const int rb = (blk * 32 + cc * 16) * (D * 2);
-                  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                      (lds_s16x4*)(sV[kt] + rb + vl_off[db][0]));
-                  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                      (lds_s16x4*)(sV[kt] + rb + vl_off[db][1]));
-                  const u32x2 lw = __builtin_bit_cast(u32x2, lo);
-                  const u32x2 hw = __builtin_bit_cast(u32x2, hi);
-                  oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]}, pb[blk][cc], oacc[db]);
-                }
+              for (int e = 0; e < 4; ++e) l_run = sum2<DT>(pb[blk][cc][e], l_run);
             }
           }
+#pragma unroll
+          for (int db = 0; db < ND; ++db)
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+              for (int cc = 0; cc < 2; ++cc) {
+                const int rb = (blk * 32 + cc * 16) * (D * 2);
+                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(vs + rb + vl_off[db][0]));
+                const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(vs + rb + vl_off[db][1]));
+                const u32x2 lw = __builtin_bit_cast(u32x2, lo);
+                const u32x2 hw = __builtin_bit_cast(u32x2, hi);
+                oacc[db] = mfma32<DT>(u32x4{lw[0], lw[1], hw[0], hw[1]}, pb[blk][cc], oacc[db]);
+              }
         }
       }
       const float l_tot = l_run + __shfl_xor(l_run, 32);

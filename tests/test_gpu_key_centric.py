@@ -409,3 +409,32 @@ def test_key_centric_plan_for_another_head_dim_is_refused():
                    H.PLAN_KEY_CENTRIC, 128)
     o, lse = _raw_fwd(q, k, v, rows, cu_sb, cu_blk, cu_q, ws, H.PLAN_KEY_CENTRIC)
     _check_oracle(args, o, lse)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("sizes", [(65, 257), (257, 513)])
+def test_resident_blocks_later_tiles_dominate(dtype, sizes):
+    # Blocks of 65..256 keys (four-wave resident kernel) or 257..512 keys
+    # (eight-wave) whose first 64-key tile is scaled down: the row maxima of
+    # the later tiles exceed the first tile's by ~17 log2 units, so against
+    # the first tile's maximum the probabilities reach 2^17 -- bf16 holds
+    # them, fp16 overflows and the kernel must rerun those rows with the
+    # exact online maximum.  Outputs must match the oracle either way.
+    n, hkv, d, topk = 6000, 2, 64, 3
+    rng = np.random.default_rng(41)
+    lens = rng.integers(sizes[0], sizes[1], size=n // sizes[0] + 1)
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    cu = cu[cu <= n]
+    cu[-1] = n
+    nb = len(cu) - 1
+    g = torch.Generator().manual_seed(42)
+    q = 2.0 * torch.randn(n, hkv, d, generator=g)
+    k = 2.0 * torch.randn(n, hkv, d, generator=g)
+    for c in range(nb):
+        k[cu[c]:min(cu[c] + 64, cu[c + 1])] *= 0.02
+    v = torch.randn(n, hkv, d, generator=g)
+    rows = torch.randint(0, nb, (hkv, n, topk), generator=g, dtype=torch.int32)
+    args = (q.to(dtype), k.to(dtype), v.to(dtype), rows, torch.tensor([0, nb], dtype=torch.int32),
+            torch.from_numpy(cu.astype(np.int32)), torch.tensor([0, n], dtype=torch.int32))
+    o, lse = _fwd(args, True)
+    _check_oracle(args, o.cpu(), lse)
