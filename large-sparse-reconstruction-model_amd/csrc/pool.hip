@@ -181,14 +181,16 @@ __global__ __launch_bounds__(256) void pool_pieces(
 constexpr int POOL_G = 4;  // rows per load group
 
 // NT = 2 pools a second tensor of the same shape and blocks (x2 -> partial2)
-// in the same launch: its items follow the first tensor's.
-template <int DT, bool IF, int NT = 1>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void
-pool_pieces_slab(const uint16_t* __restrict__ x, int64_t n, int64_t ch,
-                 const int32_t* __restrict__ cu, int64_t nb,
-                 const int32_t* __restrict__ first, float* __restrict__ partial,
-                 const uint16_t* __restrict__ x2 = nullptr,
-                 float* __restrict__ partial2 = nullptr) {
+// in the same launch: its items follow the first tensor's.  LPC = 32 (256
+// channels, with the lookup table; kernel pool_pieces_half): a wave covers
+// two chunks, one per half, the chunk index and block state per lane.
+template <int DT, bool IF, int NT, int LPC>
+__device__ __forceinline__ void pool_slab_body(const uint16_t* __restrict__ x, int64_t n,
+                                               int64_t ch, const int32_t* __restrict__ cu,
+                                               int64_t nb, const int32_t* __restrict__ first,
+                                               float* __restrict__ partial,
+                                               const uint16_t* __restrict__ x2,
+                                               float* __restrict__ partial2) {
   // Item counts stay below 2^31 (checked by the launcher): 32-bit indexing.
   const uint32_t n_vec = (uint32_t)(ch / 8);
   const uint32_t n_chunks = (uint32_t)((n + POOL_CHUNK - 1) / POOL_CHUNK);
@@ -201,7 +203,9 @@ pool_pieces_slab(const uint16_t* __restrict__ x, int64_t n, int64_t ch,
       partial = partial2;
     }
   }
-  const int64_t j = __builtin_amdgcn_readfirstlane(item / n_vec);
+  static_assert(LPC == 64 || !IF, "the in-kernel lookup needs one chunk per wave");
+  const int64_t j =
+      LPC == 64 ? (int64_t)__builtin_amdgcn_readfirstlane(item / n_vec) : (int64_t)(item / n_vec);
   const int64_t c0 = (int64_t)(item - (uint32_t)j * n_vec) * 8;
   const int64_t r0 = j * POOL_CHUNK;
   const int64_t r1 = r0 + POOL_CHUNK < n ? r0 + POOL_CHUNK : n;
@@ -304,6 +308,25 @@ pool_pieces_slab(const uint16_t* __restrict__ x, int64_t n, int64_t ch,
     }
   }
   if (have && b >= 0 && b < nb) flush();
+}
+
+template <int DT, bool IF, int NT = 1>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void
+pool_pieces_slab(const uint16_t* __restrict__ x, int64_t n, int64_t ch,
+                 const int32_t* __restrict__ cu, int64_t nb,
+                 const int32_t* __restrict__ first, float* __restrict__ partial,
+                 const uint16_t* __restrict__ x2 = nullptr,
+                 float* __restrict__ partial2 = nullptr) {
+  pool_slab_body<DT, IF, NT, 64>(x, n, ch, cu, nb, first, partial, x2, partial2);
+}
+
+// 256 channels: two chunks per wave (block state per lane, up to 128 VGPRs).
+template <int DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void
+pool_pieces_half(const uint16_t* __restrict__ x, int64_t n, int64_t ch,
+                 const int32_t* __restrict__ cu, int64_t nb,
+                 const int32_t* __restrict__ first, float* __restrict__ partial) {
+  pool_slab_body<DT, false, 1, 32>(x, n, ch, cu, nb, first, partial, nullptr, nullptr);
 }
 
 // 16-bit rows, channel count a multiple of S x 512 (S = 2 or 3): one wave
@@ -597,6 +620,20 @@ __global__ __launch_bounds__(256) void pool_combine2(
   }
 }
 
+// 16-bit rows of 256 channels: the slab kernel with two chunks per wave
+// (false for fp32 rows, which take pool_pieces).
+template <int DT>
+bool launch_half_chunks(const void* x, int64_t n, int64_t ch, const int32_t* cu, int64_t nb,
+                        const int32_t* first, float* partial, dim3 grid, hipStream_t st) {
+  if constexpr (DT == LSRM_F32) {
+    return false;
+  } else {
+    hipLaunchKernelGGL((pool_pieces_half<DT>), grid, dim3(256), 0, st,
+                       reinterpret_cast<const uint16_t*>(x), n, ch, cu, nb, first, partial);
+    return true;
+  }
+}
+
 int64_t pool_partial_rows(int64_t n, int64_t nb) {
   return nb + (n + POOL_CHUNK - 1) / POOL_CHUNK;
 }
@@ -637,7 +674,10 @@ int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
     dim3 grid((unsigned)((items + 255) / 256));
 #define LSRM_POOL_P(DT)                                                      \
   do {                                                                       \
-    if (vec && n_vec % 64 == 0)                                              \
+    if (vec && n_vec == 32 && n_chunks * n_vec < (int64_t{1} << 31) &&      \
+        launch_half_chunks<DT>(x, n, ch, cu, nb, first, partial, grid, st))  \
+      ;                                                                      \
+    else if (vec && n_vec % 64 == 0)                                         \
       hipLaunchKernelGGL((pool_pieces<DT, 8, true>), grid, dim3(256), 0, st, \
                          x, n, ch, cu, nb, first, partial);                  \
     else if (vec)                                                            \

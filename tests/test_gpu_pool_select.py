@@ -64,12 +64,12 @@ def test_pool_matches_segment_reduce_and_empty_block():
     torch.testing.assert_close(out[keep], ref[keep], rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize("c", [512, 1024, 1536, 3072])
+@pytest.mark.parametrize("c", [256, 512, 1024, 1536, 3072])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("out_dtype", [None, torch.float32])
 @pytest.mark.parametrize("n_blocks", [300, 800])
 def test_pool_slab_path_small_and_empty_blocks(c, dtype, out_dtype, n_blocks):
-    # Channel counts that are multiples of 512 take the 16-bit piece kernels:
+    # 16-bit rows of 256 channels take two chunks per wave; multiples of 512
     # one 512-channel slab per wave (512), two (1024), three (1536: whole
     # rows; 3072: two waves per chunk), with the in-kernel block lookup below
     # 512 blocks and the lookup table above.
