@@ -1075,6 +1075,27 @@ kc_resident_dq_kernel(AttnArgs a) {
   const uint32_t row_bytes = (uint32_t)a.hkv * D * 2;
   const int tq = ROWS / a.g;
   const int64_t cap = a.kc.grev.cap;
+  // Lane-dependent parts of the LDS operand addresses, pinned in registers:
+  // K / V row block reads per head-dim step, transposed K reads (rows k0,
+  // k0 + 8) per output block.
+  uint32_t kl_off[NS], vl_off[ND][2];
+  {
+    const int gi = lane & 15, dh = (lane >> 4) & 1;
+#pragma unroll
+    for (int s2 = 0; s2 < NS; ++s2) {
+      kl_off[s2] = (uint32_t)G::off(l32, 2 * s2 + hb);
+      asm volatile("" : "+v"(kl_off[s2]));
+    }
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      const int dcol = db * 32 + dh * 16 + (gi & 3) * 4;
+      const int k0 = hb * 4 + (gi >> 2);
+      const int cb = dcol >> 3, half = (dcol & 4) * 2;
+      vl_off[db][0] = (uint32_t)(G::off(k0, cb) + half);
+      vl_off[db][1] = (uint32_t)(G::off(k0 + 8, cb) + half);
+      asm volatile("" : "+v"(vl_off[db][0]), "+v"(vl_off[db][1]));
+    }
+  }
 
   for (;;) {
     const int w = uniform(fetch_work(queue, &s_slot));
@@ -1172,7 +1193,97 @@ kc_resident_dq_kernel(AttnArgs a) {
         for (int v = 0; v < 16; ++v) dqacc[i][v] = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < NT; ++kt) {
-        if (kt < ntiles) {
+        if (kt < ntiles && D <= 64) {
+          // The streaming dQ kernel's fixed slot order over the resident
+          // tile: S^T, dP^T of key block 0 (phase A), of key block 1 with
+          // dS of block 0 (B), dQ^T += K^T dS^T of block 0 with dS of block
+          // 1 (C), of block 1 (D); each MFMA's operand read two slots ahead.
+          const char* ks = sK[kt];
+          const char* vs = sV[kt];
+          constexpr int NA = 2 * NS, NC = 2 * ND, NSLOT = 2 * NA + 2 * NC, LA = 2;
+          // keys of the tile inside the block (bit p = key kt * KT + p)
+          const int hi = len - kt * KT;
+          const uint64_t m = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+          const bool masked = m != ~0ull;  // uniform: the block's last, partial tile
+          const uint64_t mh = m >> (hb * 4);  // slot v: key (v/4)*8 + hb*4 + v%4
+          f32x16 sc[2], dp[2];
+          u32x4 dsb[2][2];
+          u32x4 opnd[LA + 1];
+          auto read_op = [&](int i) __attribute__((always_inline)) {
+            if (i < 2 * NA) {
+              const int blk = i / NA, j = i % NA, sk = j >> 1;
+              const char* src = (j & 1) ? vs : ks;
+              opnd[i % (LA + 1)] =
+                  *reinterpret_cast<const u32x4*>(src + blk * 32 * (D * 2) + kl_off[sk]);
+            } else {
+              const int j = (i - 2 * NA) % NC, blk = (i - 2 * NA) / NC;
+              const int db = j >> 1, c = j & 1;
+              const int rb = (blk * 32 + c * 16) * (D * 2);
+              const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_s16x4*)(ks + rb + vl_off[db][0])));
+              const u32x2 hi2 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_s16x4*)(ks + rb + vl_off[db][1])));
+              opnd[i % (LA + 1)] = u32x4{lo[0], lo[1], hi2[0], hi2[1]};
+            }
+          };
+          auto apply_mask = [&](int blk) __attribute__((always_inline)) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              if (!((mh >> (blk * 32 + (v / 4) * 8 + (v % 4))) & 1ull))
+                sc[blk][v] = -__builtin_inf();
+          };
+          // dS of score registers 2k, 2k+1 of key block blk, packed (kept
+          // unscaled: dQ is scaled once at the end).
+          auto ds_pair = [&](int blk, int k) __attribute__((always_inline)) {
+            const int v0 = 2 * k;
+            const float p0 =
+                __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0], a.scale_log2, bias));
+            const float p1 =
+                __builtin_amdgcn_exp2f(__builtin_fmaf(sc[blk][v0 + 1], a.scale_log2, bias));
+            dsb[blk][k >> 2][k & 3] =
+                pack2<DT>(p0 * (dp[blk][v0] - delta), p1 * (dp[blk][v0 + 1] - delta));
+          };
+#pragma unroll
+          for (int i = 0; i < LA; ++i) read_op(i);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = 0; i < NSLOT; ++i) {
+            if (i + LA < NSLOT) read_op(i + LA);
+            const u32x4 op = opnd[i % (LA + 1)];
+            if (i < 2 * NA) {
+              const int blk = i / NA, j = i % NA, sk = j >> 1;
+              if (j & 1) {
+                if (sk == 0) {
+#pragma unroll
+                  for (int v = 0; v < 16; ++v) dp[blk][v] = 0.0f;
+                }
+                dp[blk] = mfma32<DT>(op, dob[sk], dp[blk]);
+              } else {
+                if (sk == 0) {
+#pragma unroll
+                  for (int v = 0; v < 16; ++v) sc[blk][v] = 0.0f;
+                }
+                sc[blk] = mfma32<DT>(op, qb[sk], sc[blk]);
+              }
+            } else {
+              const int j = (i - 2 * NA) % NC, blk = (i - 2 * NA) / NC;
+              const int db = j >> 1, c = j & 1;
+              dqacc[db] = mfma32<DT>(op, dsb[blk][c], dqacc[db]);
+            }
+            if (i == NA && masked) apply_mask(0);
+            if (i == 2 * NA && masked) apply_mask(1);
+            if (i >= NA && i < 2 * NA) {
+              const int t = i - NA;
+#pragma unroll
+              for (int k = (t * 8) / NA; k < ((t + 1) * 8) / NA; ++k) ds_pair(0, k);
+            } else if (i >= 2 * NA && i < 2 * NA + NC) {
+              const int t = i - 2 * NA;
+#pragma unroll
+              for (int k = (t * 8) / NC; k < ((t + 1) * 8) / NC; ++k) ds_pair(1, k);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        } else if (kt < ntiles) {
           const char* ks = sK[kt];
           const char* vs = sV[kt];
           f32x16 sacc[2], dpacc[2];
