@@ -107,3 +107,32 @@ def test_attention_entries_refuse_host_tensors_before_any_launch():
             H.sel_attn_bwd(q, q, k, k, q, lse, rows, cu, cu_blk, cu_q, 0.125, key_centric=kc)
         with pytest.raises(RuntimeError, match="no CPU fallback"):
             H.sel_attn_fwd(q, k, k, rows, cu, cu_blk, cu_q, 0.125, key_centric=kc)
+
+
+def test_key_centric_partials_bounded_to_one_gib():
+    # The key-centric plan's partial results (Hq * N * topk * (2D + 4) bytes
+    # when all of them fit) stay within 1 GiB: beyond it the plan runs in
+    # passes and holds one pass's partials.  The rest of the key-centric part
+    # (block -> query map with slots, its sort buffers, per-pass item lists)
+    # grows with Hkv * N * topk, not with D or the query heads.
+    if not H.LIB_PATH.exists():
+        pytest.skip("liblsrm_hip.so not built")
+    lib = H.lib()
+    gib = 1 << 30
+
+    def extra(n, hq, hkv, d, topk, nb):
+        kc = lib.lsrm_sel_attn_workspace_size2(n, n, hq, hkv, d, topk, nb, 2)
+        plain = lib.lsrm_sel_attn_workspace_size2(n, n, hq, hkv, d, topk, nb, 0)
+        assert kc > plain > 0
+        return kc - plain
+
+    # small: every partial fits, so the plan holds all of them
+    n, hq, d, topk = 4096, 4, 64, 8
+    assert extra(n, hq, hq, d, topk, 40) >= hq * n * topk * (2 * d + 4)
+    # config 3 (6.6 GB unbounded) and LSRM's heads (Hq=32, Hkv=2, D=32: 4.6 GB)
+    for args in ((131072, 24, 24, 64, 16, 462), (131072, 32, 2, 32, 16, 462)):
+        n, hq, hkv, d, topk, nb = args
+        assert hq * n * topk * (2 * d + 4) > 4 * gib
+        e = extra(*args)
+        maps = hkv * n * topk * 4 * 6  # the listing map, its sort keys and buffers (bound)
+        assert gib <= e <= gib + maps + 64 * (1 << 20), (args, e / gib)
