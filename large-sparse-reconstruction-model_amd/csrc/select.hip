@@ -20,72 +20,96 @@ int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
 int64_t pool_partial_rows(int64_t n, int64_t nb);
 int64_t pool_first_count(int64_t n);
 
-constexpr int SCORE_TILE = 64;
 constexpr int SEL_MAXD = 128;
 constexpr int SEL_CAND_LDS = 8192;      // candidate scores cached in LDS
 constexpr int SEL_MAX_CAND = 65536;     // bitmap capacity (blocks per batch)
 constexpr int SEL_MAXK = 256;
 
-// scores[h, b, c] for b, c in [0, nb): 64x64 tile per workgroup, 4x4 per
-// thread, fp64 accumulation over (g, d) in order.  The pooled rows are staged
-// in LDS as doubles, SCORE_DC head-dim columns at a time (converted once per
-// element instead of at every use; the values and the order of the fused
-// multiply-adds are unchanged).
-constexpr int SCORE_DC = 32;
+// scores[h, b, c] for b, c in [0, nb): 128x128 tile per workgroup, 8x8 per
+// thread (rows ty + 16 i, columns tx + 16 j), fp64 accumulation over (g, d)
+// in order.  The pooled rows are staged in LDS as doubles, SCORE_DC head-dim
+// columns at a time and transposed ([column][row]), so a thread's eight row
+// operands are wave-broadcast reads and its eight column operands are
+// conflict-free reads of consecutive doubles: 16 LDS reads per 64 fused
+// multiply-adds (the kernel is bound by the fp64 FMA rate, not by LDS).
+// Converting each element once and the order of the fused multiply-adds
+// leave every score a fixed function of the pooled means.
+constexpr int SCORE_TILE = 128;
+constexpr int SCORE_DC = 16;
 __global__ __launch_bounds__(256) void score_kernel(
     const float* __restrict__ pq, const float* __restrict__ pk, int64_t nb,
     int hq, int hkv, int d, double* __restrict__ scores) {
-  __shared__ double sq[SCORE_TILE][SCORE_DC + 1];
-  __shared__ double sk[SCORE_TILE][SCORE_DC + 1];
+  __shared__ double sq[SCORE_DC][SCORE_TILE + 1];
+  __shared__ double sk[SCORE_DC][SCORE_TILE + 1];
   const int h = blockIdx.z;
   const int64_t b0 = (int64_t)blockIdx.y * SCORE_TILE;
   const int64_t c0 = (int64_t)blockIdx.x * SCORE_TILE;
   const int g_n = hq / hkv;
   const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-  double acc[4][4];
+  double acc[8][8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+    for (int j = 0; j < 8; ++j) acc[i][j] = 0.0;
 
   for (int g = 0; g < g_n; ++g) {
     const int hh = h * g_n + g;
     for (int dc = 0; dc < d; dc += SCORE_DC) {
       const int dn = d - dc < SCORE_DC ? d - dc : SCORE_DC;
-      for (int i = threadIdx.x; i < SCORE_TILE * SCORE_DC; i += 256) {
-        const int r = i / SCORE_DC, dd = i - r * SCORE_DC;
+#pragma unroll
+      for (int u = 0; u < SCORE_TILE * SCORE_DC / 256; ++u) {
+        const int i = (int)threadIdx.x + 256 * u;
+        const int r = i / SCORE_DC, dd = i % SCORE_DC;
         const bool in_d = dd < dn;
-        sq[r][dd] = (in_d && b0 + r < nb)
+        sq[dd][r] = (in_d && b0 + r < nb)
                         ? (double)pq[(b0 + r) * (int64_t)hq * d + (int64_t)hh * d + dc + dd]
                         : 0.0;
-        sk[r][dd] = (in_d && c0 + r < nb)
+        sk[dd][r] = (in_d && c0 + r < nb)
                         ? (double)pk[(c0 + r) * (int64_t)hkv * d + (int64_t)h * d + dc + dd]
                         : 0.0;
       }
       __syncthreads();
       for (int dd = 0; dd < dn; ++dd) {
-        double a[4], bv[4];
+        double a[8], bv[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = sq[ty * 4 + i][dd];
+        for (int i = 0; i < 8; ++i) a[i] = sq[dd][ty + 16 * i];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bv[j] = sk[tx * 4 + j][dd];
+        for (int j = 0; j < 8; ++j) bv[j] = sk[dd][tx + 16 * j];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 8; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fma(a[i], bv[j], acc[i][j]);
+          for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_fma(a[i], bv[j], acc[i][j]);
       }
       __syncthreads();
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t b = b0 + ty * 4 + i;
+  for (int i = 0; i < 8; ++i) {
+    const int64_t b = b0 + ty + 16 * i;
     if (b >= nb) continue;
+    double* out = scores + ((int64_t)h * nb + b) * nb;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t c = c0 + tx * 4 + j;
-      if (c < nb) scores[((int64_t)h * nb + b) * nb + c] = acc[i][j];
+    for (int j = 0; j < 8; ++j) {
+      const int64_t c = c0 + tx + 16 * j;
+      if (c < nb) out[c] = acc[i][j];
     }
+  }
+}
+
+// dst[t * topk + j] = ord[j] for the `total` / topk token rows at dst, the
+// stores spread over the calling threads (`first`, `step`).  When topk / 4
+// divides `step`, a thread's 16-byte stores all carry the same four ids.
+__device__ inline void fill_token_rows(int32_t* __restrict__ dst, int64_t total,
+                                       const int* __restrict__ ord, int topk, int first,
+                                       int step) {
+  const int q4 = topk >> 2;
+  if ((topk & 3) == 0 && step % q4 == 0 && ((uintptr_t)dst & 15) == 0) {
+    const int j = (first % q4) * 4;
+    const int4 val = make_int4(ord[j], ord[j + 1], ord[j + 2], ord[j + 3]);
+    int4* d4 = reinterpret_cast<int4*>(dst);
+    for (int64_t i = first; i < (total >> 2); i += step) d4[i] = val;
+  } else {
+    for (int64_t i = first; i < total; i += step) dst[i] = ord[i % topk];
   }
 }
 
@@ -106,6 +130,115 @@ __device__ inline void clear_block_rows(const int32_t* __restrict__ cu_blk, int6
 
 __device__ inline bool sel_better(double s1, int i1, double s2, int i2) {
   return s1 > s2 || (s1 == s2 && i1 < i2);
+}
+
+__device__ inline double readlane_f64(double x, int j) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, j);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), j);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// The best R candidates (score descending, id ascending) of those a wave
+// holds -- M per lane: candidate (lane, m) has id q0 + lane + 64 m and score
+// v[m], and bit m of `taken` marks it unavailable -- written to ls / li in
+// that order (ls may be null: ids only); returns how many there are
+// (min(R, available)).
+// Threshold pass: each lane's best available candidate is its lane best;
+// the lane bests of rank 0 .. R-1 are R distinct candidates no worse than
+// the rank R-1 lane best T, so every member of the best R is no worse than
+// T.  The candidates no worse than T (the survivors) are compacted through
+// cs / ci (64 entries) and ranked among themselves.  Fallback (fewer than R
+// lane bests, or more than 64 survivors): R rounds of lane-local scan plus
+// wave butterfly.  Both give the same list, since the best R under a strict
+// total order are unique.
+template <int M>
+__device__ int wave_best_r(const double (&v)[M], uint32_t taken, int q0, int R,
+                           double* __restrict__ ls, int* __restrict__ li,
+                           double* __restrict__ cs, int* __restrict__ ci) {
+  const int lane = threadIdx.x & 63;
+  if (R <= 0) return 0;
+  double bs = -__builtin_inf();
+  int bi = INT32_MAX;
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+    if (!((taken >> m) & 1u) && sel_better(v[m], q0 + lane + 64 * m, bs, bi)) {
+      bs = v[m];
+      bi = q0 + lane + 64 * m;
+    }
+  const int nv = __popcll(__ballot(bi != INT32_MAX));
+  int S = 65;
+  if (nv >= R) {
+    int rank = 0;
+#pragma unroll
+    for (int j = 0; j < 64; ++j)
+      rank += sel_better(readlane_f64(bs, j), __builtin_amdgcn_readlane(bi, j), bs, bi) ? 1 : 0;
+    const unsigned long long at = __ballot(bi != INT32_MAX && rank == R - 1);
+    const int tl = __builtin_amdgcn_readfirstlane(__ffsll((long long)at) - 1);
+    const double ts = readlane_f64(bs, tl);
+    const int ti = __builtin_amdgcn_readlane(bi, tl);
+    S = 0;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const int id = q0 + lane + 64 * m;
+      const bool p = !((taken >> m) & 1u) && !sel_better(ts, ti, v[m], id);
+      const unsigned long long bm = __ballot(p);
+      const int pos = S + (int)__builtin_amdgcn_mbcnt_hi(
+                              (uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
+      if (p && pos < 64) {
+        cs[pos] = v[m];
+        ci[pos] = id;
+      }
+      S += __popcll(bm);
+    }
+  }
+  if (S <= 64) {
+    // One wave's LDS accesses complete in order; the clobber keeps the
+    // compiler from moving the reads above the writes.
+    asm volatile("" ::: "memory");
+    const double xs = lane < S ? cs[lane] : -__builtin_inf();
+    const int xi = lane < S ? ci[lane] : INT32_MAX;
+    int rank = 0;
+    for (int j = 0; j < S; ++j)
+      rank += sel_better(readlane_f64(xs, j), __builtin_amdgcn_readlane(xi, j), xs, xi) ? 1 : 0;
+    const int nw = S < R ? S : R;
+    if (lane < S && rank < nw) {
+      if (ls) ls[rank] = xs;
+      li[rank] = xi;
+    }
+    return nw;
+  }
+  uint32_t tk = taken;
+  int nw = 0;
+  for (int n = 0; n < R; ++n) {
+    double rs = -__builtin_inf();
+    int ri = INT32_MAX;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      if (!((tk >> m) & 1u) && sel_better(v[m], q0 + lane + 64 * m, rs, ri)) {
+        rs = v[m];
+        ri = q0 + lane + 64 * m;
+      }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const double os = __shfl_xor(rs, o);
+      const int oi = __shfl_xor(ri, o);
+      if (sel_better(os, oi, rs, ri)) {
+        rs = os;
+        ri = oi;
+      }
+    }
+    ri = __builtin_amdgcn_readfirstlane(ri);
+    if (ri == INT32_MAX) break;  // no candidate left
+    const int lc = ri - q0;
+    if ((lc & 63) == lane) tk |= 1u << (lc >> 6);
+    if (lane == 0) {
+      if (ls) ls[nw] = rs;
+      li[nw] = ri;
+    }
+    ++nw;
+  }
+  return nw;
 }
 
 // One workgroup per (query block b, kv head h).
@@ -221,14 +354,14 @@ __global__ __launch_bounds__(256) void topk_kernel(
   t1 = t1 < t0 ? t0 : (t1 > n_tokens ? n_tokens : t1);
   int32_t* dst = topk_idx + ((int64_t)h * n_tokens + t0) * topk;
   const int64_t total = (t1 - t0) * topk;
-  for (int64_t i = tid; i < total; i += 256) dst[i] = s_out[i % topk];
+  fill_token_rows(dst, total, s_out, topk, tid, 256);
 }
 
 // One wave per (kv head, query block) row when the candidates fit the
 // registers (M per lane, blocks per batch <= 64 M): the row's scores stay in
-// registers, forced blocks are taken first, then k rounds of a lane-local
-// scan plus a wave butterfly pick the best (score descending, id ascending).
-// No LDS candidate cache and no workgroup barriers.
+// registers, forced blocks are taken first, then wave_best_r lists the best
+// of the rest (score descending, id ascending).  No LDS candidate cache and
+// no workgroup barriers.
 template <int M>
 __global__ __launch_bounds__(256) void topk_wave_kernel(
     const double* __restrict__ scores, int64_t nb,
@@ -281,26 +414,10 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(
   };
   if (force_self) take((int)(b - cs));
   for (int f = 0; f < n_forced; ++f) take(forced[f]);
-  for (; n < kmax;) {
-    double bs = -__builtin_inf();
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-      if (!((taken >> m) & 1u) && sel_better(v[m], lane + 64 * m, bs, bi)) {
-        bs = v[m];
-        bi = lane + 64 * m;
-      }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const double os = __shfl_xor(bs, o);
-      const int oi = __shfl_xor(bi, o);
-      if (sel_better(os, oi, bs, bi)) {
-        bs = os;
-        bi = oi;
-      }
-    }
-    take(__builtin_amdgcn_readfirstlane(bi));
-  }
+  __shared__ double s_cs[4][64];
+  __shared__ int s_ci[4][64];
+  n += wave_best_r<M>(v, taken, 0, kmax - n, nullptr, sel + n, s_cs[wv], s_ci[wv]);
+  asm volatile("" ::: "memory");
   // Ascending ids (distinct), -1 padding: id -> its rank among the chosen.
   __shared__ int s_out[4][SEL_MAXK];
   int* ord = s_out[wv];
@@ -317,16 +434,15 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(
   t1 = t1 < t0 ? t0 : (t1 > n_tokens ? n_tokens : t1);
   int32_t* dst = topk_idx + ((int64_t)h * n_tokens + t0) * topk;
   const int64_t total = (t1 - t0) * topk;
-  for (int64_t i = lane; i < total; i += 64) dst[i] = ord[i % topk];
+  fill_token_rows(dst, total, ord, topk, lane, 64);
 }
 
 // One workgroup per (kv head, query block) row for rows of up to 4 * 64 * M
 // candidates: the forced blocks are taken first; each wave keeps a quarter
-// of the row in registers (M per lane) and picks its best R = k - forced
-// candidates by R rounds of lane-local scan plus wave butterfly (score
-// descending, id ascending); wave 0 then takes the best R of the four lists.
-// Every member of the row's best R is among its quarter's best R, so the
-// result equals a selection over the whole row.
+// of the row in registers (M per lane) and lists its best R = k - forced
+// candidates (score descending, id ascending; wave_best_r); the four lists
+// are then merged by rank.  Every member of the row's best R is among its
+// quarter's best R, so the result equals a selection over the whole row.
 template <int M>
 __global__ __launch_bounds__(256) void topk_split_kernel(
     const double* __restrict__ scores, int64_t nb,
@@ -335,8 +451,11 @@ __global__ __launch_bounds__(256) void topk_split_kernel(
     const int32_t* __restrict__ forced, int n_forced, int force_self,
     int32_t* __restrict__ topk_idx, int32_t* __restrict__ compact) {
   __shared__ int s_forced[SEL_MAXK];
-  __shared__ double s_ls[4][SEL_MAXK];  // each wave's picks: score, id
-  __shared__ int s_li[4][SEL_MAXK];
+  __shared__ double s_ls[4][64];  // each wave's picks, best first: score, id
+  __shared__ int s_li[4][64];
+  __shared__ double s_cs[4][64];  // each wave's threshold survivors
+  __shared__ int s_ci[4][64];
+  __shared__ int s_nw[4];
   __shared__ int s_sel[SEL_MAXK];
   __shared__ int s_out[SEL_MAXK];
   __shared__ int s_nf;
@@ -389,82 +508,33 @@ __global__ __launch_bounds__(256) void topk_split_kernel(
     const int i = s_forced[t] - q0;
     if (i >= 0 && i < 64 * M && (i & 63) == lane) taken |= 1u << (i >> 6);
   }
-  const int avail = (nbb - q0 > 0 ? (nbb - q0 < 64 * M ? nbb - q0 : 64 * M) : 0);
-  const int r_wave = r_need < avail ? r_need : avail;  // forced ones excluded below
-  int nw = 0;
-  for (int n = 0; n < r_wave; ++n) {
-    double bs = -__builtin_inf();
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-      if (!((taken >> m) & 1u) && sel_better(v[m], q0 + lane + 64 * m, bs, bi)) {
-        bs = v[m];
-        bi = q0 + lane + 64 * m;
-      }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const double os = __shfl_xor(bs, o);
-      const int oi = __shfl_xor(bi, o);
-      if (sel_better(os, oi, bs, bi)) {
-        bs = os;
-        bi = oi;
-      }
-    }
-    bi = __builtin_amdgcn_readfirstlane(bi);
-    if (bi == 0x7fffffff) break;  // the quarter ran out (forced ones excluded)
-    const int li = bi - q0;
-    if ((li & 63) == lane) taken |= 1u << (li >> 6);
-    if (lane == 0) {
-      s_ls[wv][nw] = bs;
-      s_li[wv][nw] = bi;
-    }
-    ++nw;
-  }
-  if (lane == 0) s_li[wv][SEL_MAXK - 1] = nw;  // list length (nw < SEL_MAXK)
+  const int nw = wave_best_r<M>(v, taken, q0, r_need, s_ls[wv], s_li[wv], s_cs[wv], s_ci[wv]);
+  if (lane == 0) s_nw[wv] = nw;
+  if (tid < nf) s_sel[tid] = s_forced[tid];
   __syncthreads();
-  if (wv == 0) {
-    // Merge: the best r_need of the four lists (topk <= 64, so each list
-    // has at most 64 entries: lane l holds entry l of every list).
-    constexpr int T = 4;
-    double cv[T];
-    int ci[T];
+  // Merge: the rank of each list entry in the union of the four lists
+  // (each sorted best first) is its index plus, for every other list, the
+  // number of that list's entries better than it (a binary search); the
+  // entries of rank < r_need are the row's best r_need, since each member
+  // of those is among its own quarter's best r_need.
+  if (lane < nw) {
+    const double es = s_ls[wv][lane];
+    const int ei = s_li[wv][lane];
+    int rank = lane;
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-      if (lane < s_li[t][SEL_MAXK - 1]) {
-        cv[t] = s_ls[t][lane];
-        ci[t] = s_li[t][lane];
-      } else {
-        cv[t] = -__builtin_inf();
-        ci[t] = 0x7fffffff;
+    for (int t = 0; t < 4; ++t) {
+      if (t == wv) continue;
+      int lo = 0, hi = s_nw[t];
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sel_better(s_ls[t][mid], s_li[t][mid], es, ei))
+          lo = mid + 1;
+        else
+          hi = mid;
       }
+      rank += lo;
     }
-    for (int t = 0; t < nf; ++t)
-      if (lane == 0) s_sel[t] = s_forced[t];
-    for (int n = 0; n < r_need; ++n) {
-      double bs = -__builtin_inf();
-      int bi = 0x7fffffff;
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-        if (ci[t] != 0x7fffffff && sel_better(cv[t], ci[t], bs, bi)) {
-          bs = cv[t];
-          bi = ci[t];
-        }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const double os = __shfl_xor(bs, o);
-        const int oi = __shfl_xor(bi, o);
-        if (sel_better(os, oi, bs, bi)) {
-          bs = os;
-          bi = oi;
-        }
-      }
-      bi = __builtin_amdgcn_readfirstlane(bi);
-      if (bi == 0x7fffffff) break;
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-        if (ci[t] == bi) ci[t] = 0x7fffffff;  // ids are distinct
-      if (lane == 0) s_sel[nf + n] = bi;
-    }
+    if (rank < r_need) s_sel[nf + rank] = ei;
   }
   __syncthreads();
   // Ascending order by rank (ids are distinct), -1 padding.
@@ -483,7 +553,7 @@ __global__ __launch_bounds__(256) void topk_split_kernel(
   t1 = t1 < t0 ? t0 : (t1 > n_tokens ? n_tokens : t1);
   int32_t* dst = topk_idx + ((int64_t)h * n_tokens + t0) * topk;
   const int64_t total = (t1 - t0) * topk;
-  for (int64_t i = tid; i < total; i += 256) dst[i] = s_out[i % topk];
+  fill_token_rows(dst, total, s_out, topk, tid, 256);
 }
 
 // Rows of tokens outside every block ([0, cu_blk[0]) and [cu_blk[nb], n),

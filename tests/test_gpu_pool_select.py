@@ -256,6 +256,36 @@ def test_select_split_path_ties_and_nan():
         assert compact[:, b].tolist() == [expect, expect], (b, compact[:, b].tolist(), expect)
 
 
+@pytest.mark.parametrize("nb,topk", [(1500, 16), (1500, 64), (4881, 32), (4881, 64)])
+@pytest.mark.parametrize("pattern", ["random", "lane_periodic", "sorted"])
+def test_select_threshold_pass_and_fallback(nb, topk, pattern):
+    # One-token blocks, so the pooled queries are the queries themselves, and
+    # pooled keys given directly: 1500 blocks take the one-wave top-k, 4881
+    # the four-wave split.  "lane_periodic" scores depend on id % 64 only
+    # (eight tie classes), so each lane holds candidates of one score and the
+    # threshold pass has far more than 64 survivors (the exact fallback runs);
+    # "sorted" scores grow with the id; topk 64 leaves no lane-best threshold.
+    d = 64
+    g = torch.Generator().manual_seed(nb * 7 + topk)
+    q = torch.randn(nb, 1, d, generator=g).to(torch.bfloat16)
+    if pattern == "random":
+        pk = torch.randn(nb, 1, d, generator=g)
+    else:
+        q[:, :, 1:] = 0
+        q[:, :, 0] = 1
+        ids = torch.arange(nb, dtype=torch.float32)
+        pk = torch.zeros(nb, 1, d)
+        pk[:, 0, 0] = (ids % 64) // 8 if pattern == "lane_periodic" else ids / nb
+    cu = torch.arange(nb + 1, dtype=torch.int32)
+    cu_sb = torch.tensor([0, nb], dtype=torch.int32)
+    forced = [0, 5, 17]
+    topk_idx, compact = H.select_blocks(q.to(DEV), q.to(DEV), cu_sb.to(DEV), cu.to(DEV), topk,
+                                        forced, True, pooled_k=pk.reshape(nb, d).to(DEV))
+    ref = select_blocks_ref(_f32(q), pk.numpy(), cu_sb.numpy(), topk, forced, True)
+    np.testing.assert_array_equal(compact.cpu().numpy(), ref)
+    np.testing.assert_array_equal(topk_idx.cpu().numpy(), ref)
+
+
 def test_select_tokens_outside_blocks_get_empty_rows():
     # the blocks cover tokens [100, n - 50): the other tokens' rows are -1
     n, d, hq = 2000, 64, 2
