@@ -574,6 +574,23 @@ struct StreamCursor {
   int p, seg, tok, segend, ntb, nend;
 };
 
+// Longest key stream of a run tile that gets a position -> token map in LDS
+// (8 KB: two workgroups per CU still fit at head dim 64).  With blocks of a
+// few dozen keys nearly every copy group crosses a block boundary, and the
+// map replaces the walk over the segment list by one LDS read per lane.
+constexpr int KMAP_KEYS = 2048;
+
+// All 256 threads: map[p] = token of stream position p for the selection in
+// s (at most KMAP_KEYS positions); wave wv (wave-uniform) writes segments
+// wv, wv + 4, ...
+__device__ inline void build_token_map(const SelLds& s, int* map, int wv, int lane) {
+  for (int sg = wv; sg < s.n; sg += 4) {
+    const int p0 = s.cum[sg], p1 = s.cum[sg + 1], tb = s.tb[sg];
+    for (int p = p0 + lane; p < p1; p += 64) map[p] = p + tb;
+  }
+  __syncthreads();
+}
+
 // Plain LDS reads (seg < n, so both indices are in range thanks to the
 // sentinels); their results are first needed at the next crossing.
 __device__ inline void cursor_prefetch(const SelLds& s, StreamCursor& c) {
@@ -599,27 +616,30 @@ struct GroupCursor {
   int seg, tbase, send;
 };
 
-__device__ inline void group_init(const SelLds& s, GroupCursor& c) {
+// With a position -> token map every group takes the map (send = -1).
+__device__ inline void group_init(const SelLds& s, GroupCursor& c, bool mapped = false) {
   c.seg = 0;
   c.tbase = uniform(s.tb[0]);
-  c.send = uniform(s.cum[1]);  // INT_MAX sentinel when the stream is empty
+  c.send = mapped ? -1 : uniform(s.cum[1]);  // INT_MAX sentinel when the stream is empty
 }
 
 // Byte offset of this lane's 16-byte piece for the group at stream position
 // P.  lane_row = lane's row in the group, lane_off = lane_row * row_bytes +
 // chunk_byte (precomputed).  Positions past the stream load token t_safe.
-// Groups must be visited in increasing P.
+// Groups must be visited in increasing P.  `map` (LDS, or null): the token
+// of every stream position, read instead of walking the segments.
 template <int KPL>
 __device__ inline uint32_t group_offset(const SelLds& s, GroupCursor& c, int P,
                                         int nkeys, int t_safe, uint32_t row_bytes,
                                         int lane_row, uint32_t lane_off,
-                                        uint32_t chunk_byte) {
+                                        uint32_t chunk_byte, const int* map = nullptr) {
   if (P + KPL <= c.send) {  // wave-uniform: the whole group is in segment c.seg
     // Scalar row offset plus the lane's constant part: one vector add.
     const uint32_t base = (uint32_t)uniform((int)((uint32_t)(P + c.tbase) * row_bytes));
     return base + lane_off;
   }
   const int p = P + lane_row;
+  if (map) return (uint32_t)(p < nkeys ? map[p] : t_safe) * row_bytes + chunk_byte;
   int tok = t_safe;
   if (p < nkeys) {
     int sg = c.seg;

@@ -91,6 +91,10 @@ sel_attn_fwd_kernel(AttnArgs a) {
   __shared__ __align__(1024) char sV[4][G::BYTES];
   __shared__ SelLds sel;
   __shared__ typename std::conditional<UNION, UnionLds, int>::type ul;
+  // Run tiles whose key stream has at most KMAP_KEYS positions: the token
+  // of every position (build_token_map), read by the copy groups that cross
+  // block boundaries.
+  __shared__ int s_tokmap[MODE == FWD_RUN ? KMAP_KEYS : 1];
   __shared__ int s_slot;
 
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
@@ -166,6 +170,10 @@ sel_attn_fwd_kernel(AttnArgs a) {
     const int nkeys = uniform(sel.cum[sel.n]);
     const int ntiles = (nkeys + KT - 1) / KT;
     const int t_safe = uniform(sel.n > 0 ? sel.tok[0] : 0);  // in-bounds filler token
+    const bool use_map = MODE == FWD_RUN && nkeys <= KMAP_KEYS;
+    if constexpr (MODE == FWD_RUN) {
+      if (use_map) build_token_map(sel, s_tokmap, wv, lane);
+    }
 
     // This wave's row and its Q operand (B of S^T = K Q^T).
     const int r = wv * 32 + l32;
@@ -225,7 +233,7 @@ sel_attn_fwd_kernel(AttnArgs a) {
     // previous tile.
     GroupCursor cur[G::LPW];
 #pragma unroll
-    for (int j = 0; j < G::LPW; ++j) group_init(sel, cur[j]);
+    for (int j = 0; j < G::LPW; ++j) group_init(sel, cur[j], use_map);
     int ld_tile = 0;  // next tile whose K copies are issued
     uint32_t koff[G::LPW], voff[G::LPW];
     // Byte offsets of the rows of tile ld_tile for this lane's loads.
@@ -233,8 +241,8 @@ sel_attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < G::LPW; ++j) {
         const int P = ld_tile * KT + (wv * G::LPW + j) * G::KPL;
-        off[j] = group_offset<G::KPL>(sel, cur[j], P, nkeys, t_safe, row_bytes,
-                                      ld_row, ld_lane_off[j], ld_byte[j]);
+        off[j] = group_offset<G::KPL>(sel, cur[j], P, nkeys, t_safe, row_bytes, ld_row,
+                                      ld_lane_off[j], ld_byte[j], use_map ? s_tokmap : nullptr);
       }
       ++ld_tile;
     };
@@ -472,7 +480,7 @@ sel_attn_fwd_kernel(AttnArgs a) {
       l_run = 0.0f;
       m_run = 0.0f;
 #pragma unroll
-      for (int j = 0; j < G::LPW; ++j) group_init(sel, cur[j]);
+      for (int j = 0; j < G::LPW; ++j) group_init(sel, cur[j], use_map);
       ld_tile = 0;
       if (ntiles > 0) {
         advance(koff);
