@@ -103,6 +103,46 @@ def test_fwd_duplicates_empty_rows_and_batches():
     _run_case(q, k, v, topk, cu_sb, cu, cu_q, 0.125)
 
 
+@pytest.mark.parametrize("d", [32, 64, 128])
+def test_fwd_token_map_boundary(d):
+    # Run tiles whose key stream has at most 2048 positions read a position ->
+    # token map; longer streams walk the segment list.  Block 0's queries
+    # select 64 blocks of 32 keys (exactly 2048 positions), block 1's select
+    # 63 of them and one of 33 in reverse order (2049), block 2's nothing,
+    # block 3's three small blocks; the other rows list up to 64 blocks of
+    # 1..40 keys (nearly every 8-key copy group crosses a block boundary),
+    # with repeated ids and padding.
+    hq, hkv, topk = 4, 2, 64
+    rng = np.random.default_rng(d)
+    sizes = np.concatenate([np.full(64, 32), [33], rng.integers(1, 41, size=235)])
+    nb = len(sizes)
+    n = int(sizes.sum())
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32))
+    rows = np.full((hkv, nb, topk), -1, dtype=np.int32)
+    for h in range(hkv):
+        for b in range(4, nb):
+            m = int(rng.integers(1, topk + 1))
+            ids = rng.integers(65, nb, size=m)
+            if m > 3:
+                ids[1] = ids[0]
+            rows[h, b, :m] = ids
+    rows[:, 0, :] = np.arange(64)
+    rows[:, 1, :] = np.arange(64, 0, -1)
+    rows[:, 3, :3] = [70, 65, 200]
+    counts = np.diff(cu.numpy())
+    topk_idx = torch.from_numpy(np.repeat(rows, counts, axis=1))
+    keys = [int(sizes[r[r >= 0]].sum()) for r in rows[0, :4]]
+    assert keys == [2048, 2049, 0, int(sizes[[70, 65, 200]].sum())]
+    gen = torch.Generator().manual_seed(d + 1)
+    q = torch.randn(n, hq, d, generator=gen).to(torch.bfloat16)
+    k = torch.randn(n, hkv, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(n, hkv, d, generator=gen).to(torch.bfloat16)
+    cu_sb = torch.tensor([0, nb], dtype=torch.int32)
+    cu_q = torch.tensor([0, n], dtype=torch.int32)
+    # forward only: the map is the forward's (the backward walks the segments)
+    _run_case(q, k, v, topk_idx, cu_sb, cu, cu_q, 1.0 / math.sqrt(d))
+
+
 def test_bwd_cfg4_small():
     w = W.config(4, n=4096, heads=4)
     q, k, v, do = W.tensors(w, "cpu", with_grad_out=True)
