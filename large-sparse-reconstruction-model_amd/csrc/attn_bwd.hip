@@ -58,6 +58,9 @@ sel_attn_dq_kernel(AttnArgs a) {
   __shared__ __align__(1024) char sV[3][G::BYTES];
   __shared__ SelLds sel;
   __shared__ typename std::conditional<UNION, UnionLds, int>::type ul;
+  // Run tiles whose key stream has at most KMAP_KEYS positions: the token
+  // of every position (build_token_map), read at each segment crossing.
+  __shared__ int s_tokmap[MODE == DQ_RUN ? KMAP_KEYS : 1];
   __shared__ int s_slot;
 
   const int tid = threadIdx.x, lane = tid & 63, wv = uniform(tid >> 6);
@@ -147,6 +150,10 @@ sel_attn_dq_kernel(AttnArgs a) {
     const int nkeys = sel.cum[sel.n];
     const int ntiles = (nkeys + KT - 1) / KT;
     const int t_safe = sel.n > 0 ? sel.tok[0] : 0;
+    const bool use_map = MODE == DQ_RUN && uniform(nkeys) <= KMAP_KEYS;
+    if constexpr (MODE == DQ_RUN) {
+      if (use_map) build_token_map(sel, s_tokmap, wv, lane);
+    }
 
     const int r = wv * 32 + l32;
     const bool row_ok = r < rows;
@@ -212,7 +219,7 @@ sel_attn_dq_kernel(AttnArgs a) {
       cur[j].p = ld_key[j] - KT;
       cur[j].seg = 0;
       cur[j].tok = 0;
-      cur[j].segend = -1;
+      cur[j].segend = -1;  // mapped streams keep it: every step reads the map
       cur[j].ntb = 0;
       cur[j].nend = -1;
     }
@@ -225,14 +232,18 @@ sel_attn_dq_kernel(AttnArgs a) {
         if (c.p < nkeys) {
           c.tok += KT;
           if (c.p >= c.segend) {
-            if (c.p < c.nend) {
-              ++c.seg;
-              c.tok = c.p + c.ntb;
-              c.segend = c.nend;
+            if (use_map) {
+              c.tok = s_tokmap[c.p];
             } else {
-              cursor_seek(sel, c);
+              if (c.p < c.nend) {
+                ++c.seg;
+                c.tok = c.p + c.ntb;
+                c.segend = c.nend;
+              } else {
+                cursor_seek(sel, c);
+              }
+              cursor_prefetch(sel, c);
             }
-            cursor_prefetch(sel, c);
           }
           t = c.tok;
         }
