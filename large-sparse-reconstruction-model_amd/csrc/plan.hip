@@ -215,6 +215,41 @@ __global__ __launch_bounds__(256) void breaks_vec_kernel(
   if (live) brk[(int64_t)h * nq + i] = (i == 0 || start || diff) ? 1 : 0;
 }
 
+// Same for rows of P 16-byte pieces (k = 4 P), P a power of two <= 64: lane
+// (row i, piece p) holds piece p of row i, so a wave reads 64 / P whole rows
+// as one contiguous run per load; piece p of row i - 1 is the lane P below
+// (a load for a wave's first row), and the P lanes of a row OR their
+// differences.
+template <int P>
+__global__ __launch_bounds__(256) void breaks_rows_kernel(
+    const int32_t* __restrict__ topk, int64_t nq, const int32_t* __restrict__ cu_q,
+    int64_t batch, const int32_t* __restrict__ cu_sb, uint8_t* __restrict__ brk) {
+  static_assert(P >= 1 && P <= 64 && (P & (P - 1)) == 0, "rows must tile a wave");
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t i = t / P;
+  const int p = (int)(t % P);
+  const bool live = i < nq;
+  const int64_t ii = live ? i : nq - 1;
+  const u32x4* rows = reinterpret_cast<const u32x4*>(topk + (int64_t)h * nq * (4 * P));
+  const u32x4 cur = rows[ii * P + p];
+  u32x4 prev;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) prev[e] = (uint32_t)__shfl_up((int)cur[e], P);
+  if (lane < P) prev = rows[(ii > 0 ? ii - 1 : 0) * P + p];
+  int b = 0, bs = 0, nbb = 0;
+  bool start = true;
+  if (live) query_batch(cu_q, batch, cu_sb, i, &b, &bs, &nbb, &start);
+  int diff = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    diff |= norm_entry((int)cur[e], nbb) != norm_entry((int)prev[e], nbb) ? 1 : 0;
+#pragma unroll
+  for (int o = 1; o < P; o <<= 1) diff |= __shfl_xor(diff, o);
+  if (live && p == 0) brk[(int64_t)h * nq + i] = (i == 0 || start || diff) ? 1 : 0;
+}
+
 struct BrkF {
   const uint8_t* brk;
   int64_t nq;
@@ -393,7 +428,23 @@ int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
 
   if (nq > 0) {
     dim3 grid(ceil_div(nq, 256), (unsigned)hkv);
-    if (topk_n % 4 == 0 && ((uintptr_t)topk % 16) == 0)
+    const int64_t pieces = topk_n / 4;
+    const bool vec = topk_n % 4 == 0 && ((uintptr_t)topk % 16) == 0;
+    // Rows of 8 or more pieces: one row per lane would read 64 rows' worth
+    // of lines per load and lose them between the row's loads (config 5's
+    // 128-byte rows fetched 6.9x their bytes); shorter rows keep that form.
+    if (vec && pieces >= 8 && pieces <= 64 && (pieces & (pieces - 1)) == 0) {
+      const dim3 grow(ceil_div(nq * pieces, 256), (unsigned)hkv);
+#define LSRM_BRK(P)                                                                  \
+  case P:                                                                            \
+    hipLaunchKernelGGL(breaks_rows_kernel<P>, grow, dim3(256), 0, st, topk, nq, cu_q, \
+                       batch, cu_sb, brk);                                           \
+    break;
+      switch (pieces) {
+        LSRM_BRK(8) LSRM_BRK(16) LSRM_BRK(32) LSRM_BRK(64)
+      }
+#undef LSRM_BRK
+    } else if (vec)
       hipLaunchKernelGGL(breaks_vec_kernel, grid, dim3(256), 0, st, topk, nq,
                          (int)topk_n, cu_q, batch, cu_sb, brk);
     else

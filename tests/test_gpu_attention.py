@@ -143,6 +143,42 @@ def test_fwd_token_map_boundary(d):
     _run_case(q, k, v, topk_idx, cu_sb, cu, cu_q, 1.0 / math.sqrt(d))
 
 
+@pytest.mark.parametrize("topk", [32, 64])
+def test_fwd_long_rows_runs_and_batch_boundary(topk):
+    # Rows of 32 and more ids (the plan's row-comparison kernel reads them a
+    # wave of lanes per few rows): identical rows either side of the batch
+    # boundary still start a new run, rows that differ only in ids naming no
+    # block of their batch element form one run, and other rows change every
+    # few tokens.
+    n0, n1, hq, d = 600, 520, 2, 64
+    rng = np.random.default_rng(topk)
+    s0 = W.uniform_partition(n0, 8, 64, rng)
+    s1 = W.uniform_partition(n1, 8, 64, rng)
+    sizes = np.concatenate([s0, s1])
+    nb0, nb1 = len(s0), len(s1)
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32))
+    cu_sb = torch.tensor([0, nb0, nb0 + nb1], dtype=torch.int32)
+    cu_q = torch.tensor([0, n0, n0 + n1], dtype=torch.int32)
+    n = n0 + n1
+    m = min(nb0, nb1)
+    rows = np.full((1, n, topk), -1, dtype=np.int32)
+    t = 0
+    while t < n:
+        run = int(rng.integers(1, 9))
+        ids = rng.integers(0, m, size=topk)
+        ids[rng.random(topk) < 0.2] = -1
+        rows[0, t:t + run] = ids
+        t += run
+    rows[0, n0 - 40:n0 + 40] = rows[0, n0 - 40]  # one row across the boundary
+    rows[0, 100:140, topk - 1] = 10 ** 6          # out of range: same as -1
+    rows[0, 100:140:2, topk - 1] = -1
+    gen = torch.Generator().manual_seed(topk + 3)
+    q = torch.randn(n, hq, d, generator=gen).to(torch.bfloat16)
+    k = torch.randn(n, 1, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(n, 1, d, generator=gen).to(torch.bfloat16)
+    _run_case(q, k, v, torch.from_numpy(rows), cu_sb, cu, cu_q, 0.125)
+
+
 def test_bwd_cfg4_small():
     w = W.config(4, n=4096, heads=4)
     q, k, v, do = W.tensors(w, "cpu", with_grad_out=True)
