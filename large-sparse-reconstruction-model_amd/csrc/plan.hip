@@ -684,16 +684,24 @@ __global__ __launch_bounds__(256) void rev_pairs_kernel(
   }
 }
 
-// seg[s] = first sorted position whose key is >= s, for s = 0 .. hkv * nb.
+// seg[s] = first sorted position whose key is >= s, for s = 0 .. hkv * nb:
+// one thread per s, a binary search over the sorted keys (the work does not
+// depend on how the keys are spread; with every key the sentinel, a walk
+// between neighbouring keys would leave one thread writing all of seg).
 __global__ __launch_bounds__(256) void rev_bounds_kernel(const uint32_t* __restrict__ keys,
                                                          int64_t n, int64_t n_seg,
                                                          int32_t* __restrict__ seg) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i <= n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t kp = i > 0 ? (int64_t)keys[i - 1] : -1;
-    const int64_t kc = i < n ? (int64_t)keys[i] : n_seg;
-    for (int64_t s = kp + 1; s <= kc && s <= n_seg; ++s) seg[s] = (int32_t)i;
+  const int64_t sgi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (sgi > n_seg) return;
+  int64_t lo = 0, hi = n;  // answer in [lo, hi]
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)keys[mid] < sgi)
+      lo = mid + 1;
+    else
+      hi = mid;
   }
+  seg[sgi] = (int32_t)lo;
 }
 
 // Per-head CSR offsets and totals from the segment starts.
@@ -767,8 +775,8 @@ int build_query_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq, int64_
   if (rocprim::radix_sort_pairs(temp, tbv, keys, keys_out, vals, vals_out, (unsigned)n, 0,
                                 bits, st) != hipSuccess)
     return LSRM_ERR_LAUNCH;
-  hipLaunchKernelGGL(rev_bounds_kernel, dim3(grid), dim3(256), 0, st, keys_out,
-                     n, n_seg, seg);
+  hipLaunchKernelGGL(rev_bounds_kernel, dim3(ceil_div(n_seg + 1, 256)), dim3(256), 0, st,
+                     keys_out, n, n_seg, seg);
   LSRM_CHECK_LAUNCH();
   hipLaunchKernelGGL(rev_offsets_kernel, dim3(ceil_div(hkv * (nb + 1), 256)), dim3(256), 0, st,
                      seg, hkv, nb, map.cu_rev, map.totals);
