@@ -614,6 +614,7 @@ __device__ inline void cursor_seek(const SelLds& s, StreamCursor& c) {
 // crosses a boundary, or runs past the stream, takes the per-lane path.
 struct GroupCursor {
   int seg, tbase, send;
+  int ntb, nend;  // token base and end of segment seg + 1 (read one crossing ahead)
 };
 
 // With a position -> token map every group takes the map (send = -1).
@@ -621,6 +622,8 @@ __device__ inline void group_init(const SelLds& s, GroupCursor& c, bool mapped =
   c.seg = 0;
   c.tbase = uniform(s.tb[0]);
   c.send = mapped ? -1 : uniform(s.cum[1]);  // INT_MAX sentinel when the stream is empty
+  c.ntb = uniform(s.tb[1]);
+  c.nend = uniform(s.cum[2]);
 }
 
 // Byte offset of this lane's 16-byte piece for the group at stream position
@@ -640,6 +643,18 @@ __device__ inline uint32_t group_offset(const SelLds& s, GroupCursor& c, int P,
   }
   const int p = P + lane_row;
   if (map) return (uint32_t)(p < nkeys ? map[p] : t_safe) * row_bytes + chunk_byte;
+  if (P + KPL <= c.nend && c.nend <= nkeys) {
+    // wave-uniform: the group ends inside segment seg + 1 (which exists), so
+    // it crosses at most the one boundary c.send: tokens from the two token
+    // bases in scalar registers, then the cursor moves on one segment.
+    const int tok = p + (p < c.send ? c.tbase : c.ntb);
+    c.seg += 1;
+    c.tbase = c.ntb;
+    c.send = c.nend;
+    c.ntb = uniform(s.tb[c.seg + 1]);
+    c.nend = uniform(s.cum[c.seg + 2]);
+    return (uint32_t)tok * row_bytes + chunk_byte;
+  }
   int tok = t_safe;
   if (p < nkeys) {
     int sg = c.seg;
@@ -655,6 +670,8 @@ __device__ inline uint32_t group_offset(const SelLds& s, GroupCursor& c, int P,
     c.seg = uniform(sg);
     c.tbase = uniform(s.tb[c.seg]);
     c.send = uniform(s.cum[c.seg + 1]);
+    c.ntb = uniform(s.tb[c.seg + 1]);
+    c.nend = uniform(s.cum[c.seg + 2]);
   }
   return (uint32_t)tok * row_bytes + chunk_byte;
 }
