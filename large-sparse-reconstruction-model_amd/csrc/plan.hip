@@ -550,6 +550,89 @@ __global__ __launch_bounds__(256) void rev_scatter_kernel(
   }
 }
 
+// rev_count_kernel / rev_scatter_kernel with the workgroup's listings first
+// gathered in LDS (nb <= REV_LDS_BINS): a block listed by many rows (the
+// forced blocks, listed by every tile) takes one global atomic per
+// workgroup instead of one per listing.  The scatter reserves each block's
+// range for the workgroup with one atomic and places its listings in that
+// range through LDS counters; the segment sort that follows fixes the order.
+constexpr int REV_LDS_BINS = 8192;
+
+__global__ __launch_bounds__(256) void rev_count_lds_kernel(
+    const int32_t* __restrict__ topk, int64_t nq, int k,
+    const int32_t* __restrict__ cu_q, int64_t batch,
+    const int32_t* __restrict__ cu_sb, int64_t nb, RowSrc rows,
+    int32_t* __restrict__ counts) {
+  __shared__ int hist[REV_LDS_BINS];
+  const int h = blockIdx.y;
+  const int64_t r0 = (int64_t)blockIdx.x * blockDim.x;
+  if (r0 >= rows.n_rows(h)) return;  // whole workgroup
+  for (int i = threadIdx.x; i < nb; i += blockDim.x) hist[i] = 0;
+  __syncthreads();
+  const int64_t r = r0 + threadIdx.x;
+  if (r < rows.n_rows(h) && !rows.skip(h, r)) {
+    const int64_t q = rows.query(h, r);
+    int b, bs, nbb;
+    bool start;
+    query_batch(cu_q, batch, cu_sb, q, &b, &bs, &nbb, &start);
+    const int32_t* row = topk + ((int64_t)h * nq + q) * k;
+    for (int j = 0; j < k; ++j) {
+      const int v = row[j];
+      if (v >= 0 && v < nbb && (int64_t)bs + v < nb) atomicAdd(&hist[bs + v], 1);
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nb; i += blockDim.x)
+    if (hist[i]) atomicAdd(&counts[(int64_t)h * nb + i], hist[i]);
+}
+
+__global__ __launch_bounds__(256) void rev_scatter_lds_kernel(
+    const int32_t* __restrict__ topk, int64_t nq, int k,
+    const int32_t* __restrict__ cu_q, int64_t batch,
+    const int32_t* __restrict__ cu_sb, int64_t nb, RowSrc rows,
+    const int32_t* __restrict__ cu_rev, int32_t* __restrict__ fill,
+    int32_t* __restrict__ rev, int64_t cap) {
+  __shared__ int cnt[REV_LDS_BINS];   // listings of the workgroup, then its base
+  __shared__ int local[REV_LDS_BINS];  // placed so far
+  const int h = blockIdx.y;
+  const int64_t r0 = (int64_t)blockIdx.x * blockDim.x;
+  if (r0 >= rows.n_rows(h)) return;  // whole workgroup
+  for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+    cnt[i] = 0;
+    local[i] = 0;
+  }
+  __syncthreads();
+  const int64_t r = r0 + threadIdx.x;
+  const bool on = r < rows.n_rows(h) && !rows.skip(h, r);
+  int bs = 0, nbb = 0;
+  const int32_t* row = topk;
+  if (on) {
+    const int64_t q = rows.query(h, r);
+    int b;
+    bool start;
+    query_batch(cu_q, batch, cu_sb, q, &b, &bs, &nbb, &start);
+    row = topk + ((int64_t)h * nq + q) * k;
+    for (int j = 0; j < k; ++j) {
+      const int v = row[j];
+      if (v >= 0 && v < nbb && (int64_t)bs + v < nb) atomicAdd(&cnt[bs + v], 1);
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nb; i += blockDim.x)
+    if (cnt[i]) cnt[i] = atomicAdd(&fill[(int64_t)h * nb + i], cnt[i]);
+  __syncthreads();
+  if (on) {
+    for (int j = 0; j < k; ++j) {
+      const int v = row[j];
+      if (v >= 0 && v < nbb && (int64_t)bs + v < nb) {
+        const int64_t c = bs + v;
+        const int64_t pos = cu_rev[(int64_t)h * (nb + 1) + c] + cnt[c] + atomicAdd(&local[c], 1);
+        if (pos < cap) rev[(int64_t)h * cap + pos] = (int32_t)(rows.enc > 0 ? r * rows.enc + j : r);
+      }
+    }
+  }
+}
+
 struct CountF {
   const int32_t* counts;
   int64_t nb;
@@ -819,10 +902,15 @@ int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
     if (rc) return rc;
     return launch_zero_i32(map.totals, hkv, st);
   }
+  const bool lds_bins = nb <= REV_LDS_BINS;
   if (nq > 0) {
     dim3 grid(ceil_div(nq, 256), (unsigned)hkv);
-    hipLaunchKernelGGL(rev_count_kernel, grid, dim3(256), 0, st, topk, nq,
-                       (int)topk_n, cu_q, batch, cu_sb, nb, rows, counts);
+    if (lds_bins)
+      hipLaunchKernelGGL(rev_count_lds_kernel, grid, dim3(256), 0, st, topk, nq,
+                         (int)topk_n, cu_q, batch, cu_sb, nb, rows, counts);
+    else
+      hipLaunchKernelGGL(rev_count_kernel, grid, dim3(256), 0, st, topk, nq,
+                         (int)topk_n, cu_q, batch, cu_sb, nb, rows, counts);
     LSRM_CHECK_LAUNCH();
   }
   rc = run_scan(CountF{counts, nb}, CuRevW{map.cu_rev, nb}, nb, (int)hkv, sums,
@@ -830,9 +918,14 @@ int build_reverse_map(const int32_t* topk, int64_t hkv, int64_t nq,
   if (rc) return rc;
   if (nq > 0) {
     dim3 grid(ceil_div(nq, 256), (unsigned)hkv);
-    hipLaunchKernelGGL(rev_scatter_kernel, grid, dim3(256), 0, st, topk, nq,
-                       (int)topk_n, cu_q, batch, cu_sb, nb, rows, map.cu_rev,
-                       fill, map.rev, map.cap);
+    if (lds_bins)
+      hipLaunchKernelGGL(rev_scatter_lds_kernel, grid, dim3(256), 0, st, topk, nq,
+                         (int)topk_n, cu_q, batch, cu_sb, nb, rows, map.cu_rev,
+                         fill, map.rev, map.cap);
+    else
+      hipLaunchKernelGGL(rev_scatter_kernel, grid, dim3(256), 0, st, topk, nq,
+                         (int)topk_n, cu_q, batch, cu_sb, nb, rows, map.cu_rev,
+                         fill, map.rev, map.cap);
     LSRM_CHECK_LAUNCH();
     dim3 sgrid((unsigned)nb, (unsigned)hkv);
     hipLaunchKernelGGL(rev_sort_kernel, sgrid, dim3(256), 0, st, map.cu_rev,
