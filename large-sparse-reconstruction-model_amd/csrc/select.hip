@@ -52,36 +52,56 @@ __global__ __launch_bounds__(256) void score_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = 0.0;
 
-  for (int g = 0; g < g_n; ++g) {
+  // Chunks (g, dc) in order; each thread stages SCORE_PER elements of the Q
+  // rows and of the K rows per chunk.  The next chunk's global loads are
+  // issued into registers before the current chunk's multiply-adds, so
+  // their latency overlaps the arithmetic.
+  constexpr int SCORE_PER = SCORE_TILE * SCORE_DC / 256;
+  const int n_dc = (d + SCORE_DC - 1) / SCORE_DC;
+  const int n_chunk = g_n * n_dc;
+  float pq_r[SCORE_PER], pk_r[SCORE_PER];
+  auto fetch = [&](int ci) __attribute__((always_inline)) {
+    const int g = ci / n_dc, dc = (ci - g * n_dc) * SCORE_DC;
     const int hh = h * g_n + g;
-    for (int dc = 0; dc < d; dc += SCORE_DC) {
-      const int dn = d - dc < SCORE_DC ? d - dc : SCORE_DC;
+    const int dn = d - dc < SCORE_DC ? d - dc : SCORE_DC;
 #pragma unroll
-      for (int u = 0; u < SCORE_TILE * SCORE_DC / 256; ++u) {
-        const int i = (int)threadIdx.x + 256 * u;
-        const int r = i / SCORE_DC, dd = i % SCORE_DC;
-        const bool in_d = dd < dn;
-        sq[dd][r] = (in_d && b0 + r < nb)
-                        ? (double)pq[(b0 + r) * (int64_t)hq * d + (int64_t)hh * d + dc + dd]
-                        : 0.0;
-        sk[dd][r] = (in_d && c0 + r < nb)
-                        ? (double)pk[(c0 + r) * (int64_t)hkv * d + (int64_t)h * d + dc + dd]
-                        : 0.0;
-      }
-      __syncthreads();
-      for (int dd = 0; dd < dn; ++dd) {
-        double a[8], bv[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) a[i] = sq[dd][ty + 16 * i];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) bv[j] = sk[dd][tx + 16 * j];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_fma(a[i], bv[j], acc[i][j]);
-      }
-      __syncthreads();
+    for (int u = 0; u < SCORE_PER; ++u) {
+      const int i = (int)threadIdx.x + 256 * u;
+      const int r = i / SCORE_DC, dd = i % SCORE_DC;
+      const bool in_d = dd < dn;
+      pq_r[u] = (in_d && b0 + r < nb)
+                    ? pq[(b0 + r) * (int64_t)hq * d + (int64_t)hh * d + dc + dd]
+                    : 0.0f;
+      pk_r[u] = (in_d && c0 + r < nb)
+                    ? pk[(c0 + r) * (int64_t)hkv * d + (int64_t)h * d + dc + dd]
+                    : 0.0f;
     }
+  };
+  fetch(0);
+  for (int ci = 0; ci < n_chunk; ++ci) {
+    const int dc = (ci % n_dc) * SCORE_DC;
+    const int dn = d - dc < SCORE_DC ? d - dc : SCORE_DC;
+#pragma unroll
+    for (int u = 0; u < SCORE_PER; ++u) {
+      const int i = (int)threadIdx.x + 256 * u;
+      const int r = i / SCORE_DC, dd = i % SCORE_DC;
+      sq[dd][r] = (double)pq_r[u];
+      sk[dd][r] = (double)pk_r[u];
+    }
+    __syncthreads();
+    if (ci + 1 < n_chunk) fetch(ci + 1);
+    for (int dd = 0; dd < dn; ++dd) {
+      double a[8], bv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = sq[dd][ty + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bv[j] = sk[dd][tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_fma(a[i], bv[j], acc[i][j]);
+    }
+    __syncthreads();
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
