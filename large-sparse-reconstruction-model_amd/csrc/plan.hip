@@ -303,24 +303,81 @@ struct EmitTilesW {
 // --------------------------------------------------------- union tiles --
 // Consecutive short run tiles (fewer than tq / 4 queries) of one batch
 // element whose first queries fall in the same window of 3 tq / 4 queries
-// form a group of at most tq - 1 queries.  Groups of two or more run tiles
+// form a group of at most tq - 1 queries; two neighbours of which one has 8
+// or more queries join only when their rows share at least half of the
+// first one's valid ids.  Per-token rows change every few queries and share
+// most blocks with their neighbours; a block-row selection's short runs are
+// whole small blocks whose neighbours select other blocks (config 5: 0-6 of
+// 32 shared), where the union only adds masked keys to a tile that already
+// runs as a whole tile of its own.  Groups of two or more run tiles
 // become grouped tiles (TilePlan::gtiles): the forward runs them over the
 // union of their queries' selections with a per-query mask, or run by run
 // when that is cheaper.  Every other run tile is kept as it is.
-struct GroupF {
-  const int2* tiles;
-  const int32_t* count;
-  const int32_t* cu_q;
-  int64_t batch, nq;
-  int short_q, window_q;
-  __device__ int64_t limit(int h, int64_t) const { return count[h]; }
-  __device__ int operator()(int h, int64_t t) const {
-    if (t == 0) return 1;
-    const int2 a = tiles[(int64_t)h * nq + t - 1], b = tiles[(int64_t)h * nq + t];
-    if (a.y >= short_q || b.y >= short_q) return 1;
-    if (a.x / window_q != b.x / window_q) return 1;
-    return batch_of(cu_q, batch, a.x) != batch_of(cu_q, batch, b.x) ? 1 : 0;
+constexpr int GROUP_FEW_Q = 8;
+constexpr int GROUP_IDS = 16;  // ids of the first row held in registers
+
+// gbrk[h, t] = 1 where run tile t starts a new group.  One thread per tile:
+// the shared-ids count (at most a few hundred tiles per head need it) holds
+// 16 ids of one row in registers per pass over the other row, read 8 at a
+// time.
+__global__ __launch_bounds__(256) void group_breaks_kernel(
+    const int2* __restrict__ tiles, const int32_t* __restrict__ count,
+    const int32_t* __restrict__ cu_q, int64_t batch, const int32_t* __restrict__ topk,
+    int64_t nq, int k, int short_q, int window_q, uint8_t* __restrict__ gbrk) {
+  const int h = blockIdx.y;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= count[h]) return;
+  uint8_t* out = gbrk + (int64_t)h * nq + t;
+  if (t == 0) {
+    *out = 1;
+    return;
   }
+  const int2 a = tiles[(int64_t)h * nq + t - 1], b = tiles[(int64_t)h * nq + t];
+  if (a.y >= short_q || b.y >= short_q || a.x / window_q != b.x / window_q ||
+      batch_of(cu_q, batch, a.x) != batch_of(cu_q, batch, b.x)) {
+    *out = 1;
+    return;
+  }
+  if (a.y < GROUP_FEW_Q && b.y < GROUP_FEW_Q) {
+    *out = 0;
+    return;
+  }
+  // a run's rows are identical: its first query's row stands for it
+  const int32_t* ra = topk + ((int64_t)h * nq + a.x) * k;
+  const int32_t* rb = topk + ((int64_t)h * nq + b.x) * k;
+  int valid = 0, shared = 0;
+  for (int i0 = 0; i0 < k; i0 += GROUP_IDS) {
+    int x[GROUP_IDS];
+    bool hit[GROUP_IDS];
+#pragma unroll
+    for (int e = 0; e < GROUP_IDS; ++e) {
+      x[e] = i0 + e < k ? ra[i0 + e] : -1;
+      hit[e] = false;
+    }
+    for (int j0 = 0; j0 < k; j0 += 8) {
+      int y[8];  // -1 pads: a hit on an invalid id is not counted
+#pragma unroll
+      for (int u = 0; u < 8; ++u) y[u] = j0 + u < k ? rb[j0 + u] : -1;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int e = 0; e < GROUP_IDS; ++e) hit[e] |= x[e] == y[u];
+    }
+#pragma unroll
+    for (int e = 0; e < GROUP_IDS; ++e) {
+      valid += x[e] >= 0 ? 1 : 0;
+      shared += x[e] >= 0 && hit[e] ? 1 : 0;
+    }
+  }
+  *out = 2 * shared >= valid ? 0 : 1;
+}
+
+struct GroupF {
+  const uint8_t* gbrk;
+  const int32_t* count;
+  int64_t nq;
+  __device__ int64_t limit(int h, int64_t) const { return count[h]; }
+  __device__ int operator()(int h, int64_t t) const { return gbrk[(int64_t)h * nq + t]; }
 };
 struct GroupW {
   int32_t* gstart;  // [hkv, nq + 1]
@@ -461,7 +518,11 @@ int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
     if (group_short) {
       const int short_q = tq / 4 > 1 ? tq / 4 : 1;
       const int window_q = (3 * tq) / 4 > 1 ? (3 * tq) / 4 : 1;
-      rc = run_scan(GroupF{run_tiles, run_count, cu_q, batch, nq, short_q, window_q},
+      // brk is free again: it takes the group starts
+      hipLaunchKernelGGL(group_breaks_kernel, grid, dim3(256), 0, st, run_tiles, run_count,
+                         cu_q, batch, topk, nq, (int)topk_n, short_q, window_q, brk);
+      LSRM_CHECK_LAUNCH();
+      rc = run_scan(GroupF{brk, run_count, nq},
                     GroupW{gstart, nq}, nq, (int)hkv, sums, n_groups, st);
       if (rc) return rc;
       rc = run_scan(SplitF{gstart, n_groups, nq},

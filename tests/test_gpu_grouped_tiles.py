@@ -185,3 +185,56 @@ def test_gqa16_d32_per_token_rows_fwd_bwd():
     q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _voxel_case(n=4096, hq=32, hkv=2, topk=4, seed=11,
                                                          d=32)
     _check(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, do=_grad_out(q, 11))
+
+
+def _mid_runs_case(n=6144, hkv=2, topk=8, seed=12):
+    """Runs of 1..40 identical rows; each new row either swaps one id of the
+    previous row (neighbours share 7 of 8) or is drawn afresh (they share
+    about none), so short runs of 8 or more queries meet neighbours on both
+    sides of the shared-ids rule.  Some rows carry -1 padding."""
+    w = W.config(2, n=n, heads=hkv)
+    q, k, v = W.tensors(w, "cpu")
+    rng = np.random.default_rng(seed)
+    nb = w.n_blocks
+    rows = np.empty((hkv, n, topk), np.int32)
+    for h in range(hkv):
+        cur = rng.choice(nb, topk, replace=False)
+        i = 0
+        while i < n:
+            ln = int(rng.integers(1, 41))
+            if rng.random() < 0.5:
+                cur = cur.copy()
+                free = np.setdiff1d(np.arange(nb), cur)
+                cur[rng.integers(topk)] = rng.choice(free)
+            else:
+                cur = rng.choice(nb, topk, replace=False)
+            r = cur.copy()
+            if rng.random() < 0.2:
+                r[topk - 2:] = -1
+            rows[h, i:i + ln] = r
+            i += ln
+    return (q, k, v, torch.from_numpy(rows), w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens)
+
+
+@pytest.mark.parametrize("key_centric", [False, True])
+def test_mid_length_runs_join_by_shared_ids(key_centric):
+    # runs of 8..31 queries join a neighbouring short run only when their
+    # rows share at least half their ids; both outcomes through the forward
+    # and the backward of either plan
+    q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _mid_runs_case()
+    scale = 0.125
+    dev_args = [t.to(DEV) for t in (q, k, v, topk_idx, cu_sb, cu_blk, cu_q)]
+    do = _grad_out(q, 12)
+    o, lse = H.sel_attn_fwd(*dev_args, scale, key_centric=key_centric)
+    qf, kf, vf = (t.float().requires_grad_(True) for t in (q, k, v))
+    o_ref, lse_ref = sel_attn_ref(qf, kf, vf, topk_idx, cu_sb, cu_blk, cu_q, scale)
+    assert_attn_close(o, o_ref, "out")
+    fin = torch.isfinite(lse_ref)
+    assert torch.equal(torch.isfinite(lse.cpu()), fin)
+    assert float((lse.cpu()[fin] - lse_ref[fin]).abs().max()) <= 2e-2
+    dq, dk, dv, _ = H.sel_attn_bwd(do.to(DEV), *dev_args[:3], o, lse, *dev_args[3:], scale,
+                                   key_centric=key_centric)
+    o_ref.backward(do.float())
+    assert_attn_close(dq, qf.grad, "dq")
+    assert_attn_close(dk, kf.grad, "dk")
+    assert_attn_close(dv, vf.grad, "dv")
