@@ -314,62 +314,58 @@ struct EmitTilesW {
 // union of their queries' selections with a per-query mask, or run by run
 // when that is cheaper.  Every other run tile is kept as it is.
 constexpr int GROUP_FEW_Q = 8;
-constexpr int GROUP_IDS = 16;  // ids of the first row held in registers
 
-// gbrk[h, t] = 1 where run tile t starts a new group.  One thread per tile:
-// the shared-ids count (at most a few hundred tiles per head need it) holds
-// 16 ids of one row in registers per pass over the other row, read 8 at a
-// time.
+// gbrk[h, t] = 1 where run tile t starts a new group.  One thread per tile
+// decides the plain cases; the tiles that need the shared-ids count (at most
+// a few hundred per head) are taken one at a time by their whole wave: lane
+// j holds id j of both rows (one load round for rows of <= 64 ids) and the
+// other row's ids are broadcast with readlane.
 __global__ __launch_bounds__(256) void group_breaks_kernel(
     const int2* __restrict__ tiles, const int32_t* __restrict__ count,
     const int32_t* __restrict__ cu_q, int64_t batch, const int32_t* __restrict__ topk,
     int64_t nq, int k, int short_q, int window_q, uint8_t* __restrict__ gbrk) {
   const int h = blockIdx.y;
+  const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= count[h]) return;
-  uint8_t* out = gbrk + (int64_t)h * nq + t;
-  if (t == 0) {
-    *out = 1;
-    return;
-  }
-  const int2 a = tiles[(int64_t)h * nq + t - 1], b = tiles[(int64_t)h * nq + t];
-  if (a.y >= short_q || b.y >= short_q || a.x / window_q != b.x / window_q ||
-      batch_of(cu_q, batch, a.x) != batch_of(cu_q, batch, b.x)) {
-    *out = 1;
-    return;
-  }
-  if (a.y < GROUP_FEW_Q && b.y < GROUP_FEW_Q) {
-    *out = 0;
-    return;
-  }
-  // a run's rows are identical: its first query's row stands for it
-  const int32_t* ra = topk + ((int64_t)h * nq + a.x) * k;
-  const int32_t* rb = topk + ((int64_t)h * nq + b.x) * k;
-  int valid = 0, shared = 0;
-  for (int i0 = 0; i0 < k; i0 += GROUP_IDS) {
-    int x[GROUP_IDS];
-    bool hit[GROUP_IDS];
-#pragma unroll
-    for (int e = 0; e < GROUP_IDS; ++e) {
-      x[e] = i0 + e < k ? ra[i0 + e] : -1;
-      hit[e] = false;
-    }
-    for (int j0 = 0; j0 < k; j0 += 8) {
-      int y[8];  // -1 pads: a hit on an invalid id is not counted
-#pragma unroll
-      for (int u = 0; u < 8; ++u) y[u] = j0 + u < k ? rb[j0 + u] : -1;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int e = 0; e < GROUP_IDS; ++e) hit[e] |= x[e] == y[u];
-    }
-#pragma unroll
-    for (int e = 0; e < GROUP_IDS; ++e) {
-      valid += x[e] >= 0 ? 1 : 0;
-      shared += x[e] >= 0 && hit[e] ? 1 : 0;
+  const int64_t cnt = count[h];
+  int brk = 1;
+  bool check = false;
+  int qa = 0, qb = 0;
+  if (t > 0 && t < cnt) {
+    const int2 a = tiles[(int64_t)h * nq + t - 1], b = tiles[(int64_t)h * nq + t];
+    if (a.y < short_q && b.y < short_q && a.x / window_q == b.x / window_q &&
+        batch_of(cu_q, batch, a.x) == batch_of(cu_q, batch, b.x)) {
+      if (a.y < GROUP_FEW_Q && b.y < GROUP_FEW_Q) {
+        brk = 0;
+      } else {
+        // a run's rows are identical: its first query's row stands for it
+        check = true;
+        qa = a.x;
+        qb = b.x;
+      }
     }
   }
-  *out = 2 * shared >= valid ? 0 : 1;
+  uint64_t pend = __ballot(check);
+  while (pend) {
+    const int l = __builtin_ctzll(pend);
+    pend &= pend - 1;
+    const int64_t ra = ((int64_t)h * nq + __builtin_amdgcn_readlane(qa, l)) * k;
+    const int64_t rb = ((int64_t)h * nq + __builtin_amdgcn_readlane(qb, l)) * k;
+    int valid = 0, shared = 0;
+    for (int c0 = 0; c0 < k; c0 += 64) {
+      const int x = c0 + lane < k ? topk[ra + c0 + lane] : -1;
+      bool hit = false;
+      for (int d0 = 0; d0 < k; d0 += 64) {
+        const int y = d0 + lane < k ? topk[rb + d0 + lane] : -1;
+        const int m_end = k - d0 < 64 ? k - d0 : 64;
+        for (int m = 0; m < m_end; ++m) hit |= x == __builtin_amdgcn_readlane(y, m);
+      }
+      valid += __popcll(__ballot(x >= 0));
+      shared += __popcll(__ballot(x >= 0 && hit));
+    }
+    if (lane == l) brk = 2 * shared >= valid ? 0 : 1;
+  }
+  if (t < cnt) gbrk[(int64_t)h * nq + t] = (uint8_t)brk;
 }
 
 struct GroupF {

@@ -187,15 +187,22 @@ def test_gqa16_d32_per_token_rows_fwd_bwd():
     _check(q, k, v, topk_idx, cu_sb, cu_blk, cu_q, do=_grad_out(q, 11))
 
 
-def _mid_runs_case(n=6144, hkv=2, topk=8, seed=12):
-    """Runs of 1..40 identical rows; each new row either swaps one id of the
-    previous row (neighbours share 7 of 8) or is drawn afresh (they share
-    about none), so short runs of 8 or more queries meet neighbours on both
-    sides of the shared-ids rule.  Some rows carry -1 padding."""
-    w = W.config(2, n=n, heads=hkv)
-    q, k, v = W.tensors(w, "cpu")
+def _mid_runs_case(n=6144, hkv=2, topk=8, seed=12, d=64):
+    """Blocks of 8..40 tokens; runs of 1..40 identical rows; each new row
+    either swaps one id of the previous row (neighbours share all but one)
+    or is drawn afresh (they share about none), so short runs of 8 or more
+    queries meet neighbours on both sides of the shared-ids rule.  Some rows
+    carry -1 padding."""
     rng = np.random.default_rng(seed)
-    nb = w.n_blocks
+    sizes = rng.integers(8, 41, size=n // 8)
+    cu = np.concatenate([[0], np.cumsum(sizes)])
+    cu = cu[cu <= n]
+    cu[-1] = n
+    nb = len(cu) - 1
+    g = torch.Generator().manual_seed(seed)
+    q = (0.5 * torch.randn(n, hkv, d, generator=g)).to(torch.bfloat16)
+    k = (0.5 * torch.randn(n, hkv, d, generator=g)).to(torch.bfloat16)
+    v = (0.5 * torch.randn(n, hkv, d, generator=g)).to(torch.bfloat16)
     rows = np.empty((hkv, n, topk), np.int32)
     for h in range(hkv):
         cur = rng.choice(nb, topk, replace=False)
@@ -213,15 +220,16 @@ def _mid_runs_case(n=6144, hkv=2, topk=8, seed=12):
                 r[topk - 2:] = -1
             rows[h, i:i + ln] = r
             i += ln
-    return (q, k, v, torch.from_numpy(rows), w.cu_seqblocks, w.cu_block_tokens, w.cu_seqlens)
+    return (q, k, v, torch.from_numpy(rows), torch.tensor([0, nb], dtype=torch.int32),
+            torch.from_numpy(cu.astype(np.int32)), torch.tensor([0, n], dtype=torch.int32))
 
 
-@pytest.mark.parametrize("key_centric", [False, True])
-def test_mid_length_runs_join_by_shared_ids(key_centric):
+@pytest.mark.parametrize("key_centric,topk", [(False, 8), (True, 8), (False, 20), (False, 72)])
+def test_mid_length_runs_join_by_shared_ids(key_centric, topk):
     # runs of 8..31 queries join a neighbouring short run only when their
     # rows share at least half their ids; both outcomes through the forward
-    # and the backward of either plan
-    q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _mid_runs_case()
+    # and the backward of either plan, rows of one or two wave widths of ids
+    q, k, v, topk_idx, cu_sb, cu_blk, cu_q = _mid_runs_case(topk=topk)
     scale = 0.125
     dev_args = [t.to(DEV) for t in (q, k, v, topk_idx, cu_sb, cu_blk, cu_q)]
     do = _grad_out(q, 12)
