@@ -184,7 +184,7 @@ constexpr int POOL_G = 4;  // rows per load group
 // in the same launch: its items follow the first tensor's.  LPC = 32 (256
 // channels, with the lookup table; kernel pool_pieces_half): a wave covers
 // two chunks, one per half, the chunk index and block state per lane.
-template <int DT, bool IF, int NT, int LPC>
+template <int DT, bool IF, int NT, int LPC, bool IF2 = false>
 __device__ __forceinline__ void pool_slab_body(const uint16_t* __restrict__ x, int64_t n,
                                                int64_t ch, const int32_t* __restrict__ cu,
                                                int64_t nb, const int32_t* __restrict__ first,
@@ -237,6 +237,35 @@ __device__ __forceinline__ void pool_slab_body(const uint16_t* __restrict__ x, i
     for (int i = 0; i < 8; ++i)
       cnt += __popcll(__ballot((int64_t)cv[i] <= r0 && 8 * lane + i <= nb));
     b = __builtin_amdgcn_readfirstlane(cnt) - 1;
+  } else if constexpr (IF2) {
+    // Two-level count of the offsets <= r0 for this half-wave's chunk
+    // (nb + 1 <= 8192): its 32 lanes read every S-th offset (S = ceil((nb +
+    // 1) / 32) <= 256), then the S offsets from the last sampled hit on, up
+    // to 8 per lane in one round.  Offsets are nondecreasing, so the hits
+    // are a prefix and the count is base + the second round's hits.
+    static_assert(LPC == 32, "one chunk per half-wave");
+    const int lane = threadIdx.x & 63, hl = lane & 31;
+    const uint64_t half = lane < 32 ? 0xffffffffull : 0xffffffff00000000ull;
+    const int64_t S = (nb + 32) / 32;
+    const int64_t i1 = hl * S;
+    const int32_t v1 = cu[i1 <= nb ? i1 : nb];
+    load_group(buf[0], r0);
+    const int c1 = __popcll(__ballot(i1 <= nb && (int64_t)v1 <= r0) & half);
+    const int64_t base = c1 > 0 ? (int64_t)(c1 - 1) * S : 0;
+    int32_t v2[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int64_t i2 = base + hl + 32 * m;
+      v2[m] = cu[hl + 32 * m < S && i2 <= nb ? i2 : 0];
+    }
+    int cnt = 0;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int64_t i2 = base + hl + 32 * m;
+      cnt += __popcll(__ballot(c1 > 0 && hl + 32 * m < S && i2 <= nb && (int64_t)v2[m] <= r0) &
+                      half);
+    }
+    b = c1 > 0 ? base + cnt - 1 : -1;
   } else {
     load_group(buf[0], r0);
     b = first[j];
@@ -321,12 +350,15 @@ pool_pieces_slab(const uint16_t* __restrict__ x, int64_t n, int64_t ch,
 }
 
 // 256 channels: two chunks per wave (block state per lane, up to 128 VGPRs).
-template <int DT>
+// IF2: the block lookup in the kernel (nb + 1 <= POOL_IF2_MAX), else the
+// pool_chunk_first table.
+constexpr int64_t POOL_IF2_MAX = 8192;
+template <int DT, bool IF2>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void
 pool_pieces_half(const uint16_t* __restrict__ x, int64_t n, int64_t ch,
                  const int32_t* __restrict__ cu, int64_t nb,
                  const int32_t* __restrict__ first, float* __restrict__ partial) {
-  pool_slab_body<DT, false, 1, 32>(x, n, ch, cu, nb, first, partial, nullptr, nullptr);
+  pool_slab_body<DT, false, 1, 32, IF2>(x, n, ch, cu, nb, first, partial, nullptr, nullptr);
 }
 
 // 16-bit rows, channel count a multiple of S x 512 (S = 2 or 3): one wave
@@ -628,8 +660,12 @@ bool launch_half_chunks(const void* x, int64_t n, int64_t ch, const int32_t* cu,
   if constexpr (DT == LSRM_F32) {
     return false;
   } else {
-    hipLaunchKernelGGL((pool_pieces_half<DT>), grid, dim3(256), 0, st,
-                       reinterpret_cast<const uint16_t*>(x), n, ch, cu, nb, first, partial);
+    if (nb + 1 <= POOL_IF2_MAX)
+      hipLaunchKernelGGL((pool_pieces_half<DT, true>), grid, dim3(256), 0, st,
+                         reinterpret_cast<const uint16_t*>(x), n, ch, cu, nb, first, partial);
+    else
+      hipLaunchKernelGGL((pool_pieces_half<DT, false>), grid, dim3(256), 0, st,
+                         reinterpret_cast<const uint16_t*>(x), n, ch, cu, nb, first, partial);
     return true;
   }
 }
@@ -668,8 +704,12 @@ int launch_block_mean_pool(const void* x, int x_dtype, int64_t n, int64_t ch,
                                     inline_first, st);
     LSRM_CHECK_LAUNCH();
   } else if (n > 0) {
-    hipLaunchKernelGGL(pool_chunk_first, dim3((unsigned)((n_chunks + 255) / 256)),
-                       dim3(256), 0, st, cu, nb, n_chunks, first);
+    // the 256-channel 16-bit kernel finds the blocks itself up to POOL_IF2_MAX
+    const bool half_inline = vec && n_vec == 32 && x_dtype != LSRM_F32 &&
+                             n_chunks * n_vec < (int64_t{1} << 31) && nb + 1 <= POOL_IF2_MAX;
+    if (!half_inline)
+      hipLaunchKernelGGL(pool_chunk_first, dim3((unsigned)((n_chunks + 255) / 256)),
+                         dim3(256), 0, st, cu, nb, n_chunks, first);
     const int64_t items = n_chunks * n_vec;
     dim3 grid((unsigned)((items + 255) / 256));
 #define LSRM_POOL_P(DT)                                                      \

@@ -94,6 +94,30 @@ def test_pool_slab_path_small_and_empty_blocks(c, dtype, out_dtype, n_blocks):
         assert torch.equal(out[~nan.all(1)].view(ints), ref[~nan.all(1)].view(ints))
 
 
+@pytest.mark.parametrize("n_blocks", [512, 4881, 8191, 8192, 20000])
+def test_pool_256_channels_block_lookup(n_blocks):
+    # 256-channel 16-bit rows: up to 8191 blocks the kernel finds each
+    # chunk's first block itself (32 sampled offsets, then up to 256 offsets
+    # of the hit interval; 8191 blocks use the whole second round), beyond
+    # that it reads the lookup table.  Empty blocks (runs of equal offsets,
+    # one across a sampled offset), rows before the first and after the last
+    # block.
+    rng = np.random.default_rng(n_blocks)
+    sizes = rng.integers(0, 21, size=n_blocks)
+    s_rt = (n_blocks + 32) // 32
+    sizes[[0, 1, s_rt - 1, s_rt, min(2 * s_rt, n_blocks - 1)]] = 0
+    cu_np = np.concatenate([[45], 45 + np.cumsum(sizes)]).astype(np.int32)
+    n = int(cu_np[-1]) + 70
+    g = torch.Generator().manual_seed(n_blocks)
+    x = torch.randn(n, 256, generator=g).to(torch.bfloat16)
+    cu = torch.from_numpy(cu_np)
+    ref = torch.from_numpy(block_mean_pool_ref(_f32(x), cu_np)).to(torch.bfloat16)
+    out = H.block_mean_pool(x.to(DEV), cu.to(DEV), None).cpu()
+    nan = torch.isnan(ref)
+    assert torch.equal(torch.isnan(out), nan)
+    assert torch.equal(out[~nan.all(1)].view(torch.int16), ref[~nan.all(1)].view(torch.int16))
+
+
 @pytest.mark.parametrize("c,n_blocks,out_a,out_b", [
     (512, 300, torch.float32, None),      # slab path, in-kernel block lookup
     (1024, 800, None, torch.float32),     # two slabs per wave, lookup table
