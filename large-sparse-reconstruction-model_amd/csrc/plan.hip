@@ -218,36 +218,63 @@ __global__ __launch_bounds__(256) void breaks_vec_kernel(
 // Same for rows of P 16-byte pieces (k = 4 P), P a power of two <= 64: lane
 // (row i, piece p) holds piece p of row i, so a wave reads 64 / P whole rows
 // as one contiguous run per load; piece p of row i - 1 is the lane P below
-// (a load for a wave's first row), and the P lanes of a row OR their
-// differences.
+// (the last row of the previous group, or a load for the wave's first row),
+// and the P lanes of a row OR their differences.  A wave covers BRK_G such
+// groups with all their loads in flight, and looks its batch element up once
+// when its rows lie inside one (else row by row).
+constexpr int BRK_G = 8;
 template <int P>
 __global__ __launch_bounds__(256) void breaks_rows_kernel(
     const int32_t* __restrict__ topk, int64_t nq, const int32_t* __restrict__ cu_q,
     int64_t batch, const int32_t* __restrict__ cu_sb, uint8_t* __restrict__ brk) {
   static_assert(P >= 1 && P <= 64 && (P & (P - 1)) == 0, "rows must tile a wave");
+  constexpr int RPW = 64 / P;  // rows per group
   const int h = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t i = t / P;
-  const int p = (int)(t % P);
-  const bool live = i < nq;
-  const int64_t ii = live ? i : nq - 1;
+  const int64_t i0 =
+      ((int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * (RPW * BRK_G);
+  if (i0 >= nq) return;  // whole waves
+  const int p = lane % P, rl = lane / P;
   const u32x4* rows = reinterpret_cast<const u32x4*>(topk + (int64_t)h * nq * (4 * P));
-  const u32x4 cur = rows[ii * P + p];
-  u32x4 prev;
+  u32x4 cur[BRK_G];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) prev[e] = (uint32_t)__shfl_up((int)cur[e], P);
-  if (lane < P) prev = rows[(ii > 0 ? ii - 1 : 0) * P + p];
-  int b = 0, bs = 0, nbb = 0;
-  bool start = true;
-  if (live) query_batch(cu_q, batch, cu_sb, i, &b, &bs, &nbb, &start);
-  int diff = 0;
+  for (int g = 0; g < BRK_G; ++g) {
+    const int64_t i = i0 + g * RPW + rl;
+    cur[g] = rows[(i < nq ? i : nq - 1) * P + p];
+  }
+  u32x4 first_prev = cur[0];
+  if (lane < P && i0 > 0) first_prev = rows[(i0 - 1) * P + p];
+  const int64_t i_last = i0 + RPW * BRK_G - 1 < nq ? i0 + RPW * BRK_G - 1 : nq - 1;
+  int b0 = 0, bs0 = 0, nbb0 = 0;
+  bool st0 = true;
+  query_batch(cu_q, batch, cu_sb, i0, &b0, &bs0, &nbb0, &st0);
+  const int64_t qs0 = b0 >= 0 ? cu_q[b0] : 0;
+  const bool one = b0 >= 0 && i_last < (int64_t)cu_q[b0 + 1];
 #pragma unroll
-  for (int e = 0; e < 4; ++e)
-    diff |= norm_entry((int)cur[e], nbb) != norm_entry((int)prev[e], nbb) ? 1 : 0;
+  for (int g = 0; g < BRK_G; ++g) {
+    const int64_t i = i0 + g * RPW + rl;
+    u32x4 prev;
 #pragma unroll
-  for (int o = 1; o < P; o <<= 1) diff |= __shfl_xor(diff, o);
-  if (live && p == 0) brk[(int64_t)h * nq + i] = (i == 0 || start || diff) ? 1 : 0;
+    for (int e = 0; e < 4; ++e) {
+      const int up = __shfl_up((int)cur[g][e], P);
+      const int last = g > 0 ? __shfl((int)cur[g > 0 ? g - 1 : 0][e], (RPW - 1) * P + p)
+                             : (int)first_prev[e];
+      prev[e] = (uint32_t)(lane >= P ? up : last);
+    }
+    int nbb = nbb0;
+    bool start = i == qs0;
+    if (!one && i < nq) {
+      int b, bs;
+      query_batch(cu_q, batch, cu_sb, i, &b, &bs, &nbb, &start);
+    }
+    int diff = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      diff |= norm_entry((int)cur[g][e], nbb) != norm_entry((int)prev[e], nbb) ? 1 : 0;
+#pragma unroll
+    for (int o = 1; o < P; o <<= 1) diff |= __shfl_xor(diff, o);
+    if (i < nq && p == 0) brk[(int64_t)h * nq + i] = (i == 0 || start || diff) ? 1 : 0;
+  }
 }
 
 struct BrkF {
@@ -487,7 +514,8 @@ int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
     // of lines per load and lose them between the row's loads (config 5's
     // 128-byte rows fetched 6.9x their bytes); shorter rows keep that form.
     if (vec && pieces >= 8 && pieces <= 64 && (pieces & (pieces - 1)) == 0) {
-      const dim3 grow(ceil_div(nq * pieces, 256), (unsigned)hkv);
+      // one wave per BRK_G groups of 64 / pieces rows, four waves per block
+      const dim3 grow(ceil_div(ceil_div(nq, (64 / pieces) * BRK_G), 4), (unsigned)hkv);
 #define LSRM_BRK(P)                                                                  \
   case P:                                                                            \
     hipLaunchKernelGGL(breaks_rows_kernel<P>, grow, dim3(256), 0, st, topk, nq, cu_q, \
