@@ -42,8 +42,10 @@ def _bits(t):
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 def test_noalloc_matches_workspace_entry_twice(out_dtype):
     # call 1: the cfg3 key tensor (131072 x 1536 bf16, 462 blocks; the slab
-    # path); call 2: a smaller, ragged input (the scalar-channel path, blocks
-    # of 0-300 rows) over the scratch the first call left behind.
+    # path); call 2: 256 channels over 2000 blocks of 0-40 rows (the
+    # two-chunk kernel with its in-kernel block lookup); call 3: a smaller,
+    # ragged input (the scalar-channel path, blocks of 0-300 rows).  Each call
+    # runs over the scratch the previous one left behind.
     w = W.config(3)
     g = torch.Generator(device=DEV).manual_seed(5)
     x1 = (0.5 * torch.randn(w.n, w.hkv * w.d, generator=g, device=DEV)).to(torch.bfloat16)
@@ -52,7 +54,10 @@ def test_noalloc_matches_workspace_entry_twice(out_dtype):
     sizes = rng.integers(0, 301, size=40)
     cu2 = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)).to(DEV)
     x2 = torch.randn(int(sizes.sum()), 12, generator=g, device=DEV).to(torch.float16)
-    for x, cu in ((x1, cu1), (x2, cu2)):
+    sizes3 = rng.integers(0, 41, size=2000)
+    cu3 = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes3)]).astype(np.int32)).to(DEV)
+    x3 = torch.randn(int(sizes3.sum()), 256, generator=g, device=DEV).to(torch.bfloat16)
+    for x, cu in ((x1, cu1), (x3, cu3), (x2, cu2)):
         out, ref = _pool_both(x, cu, out_dtype)
         nan = torch.isnan(ref)
         assert torch.equal(torch.isnan(out), nan)
