@@ -510,10 +510,12 @@ int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
     dim3 grid(ceil_div(nq, 256), (unsigned)hkv);
     const int64_t pieces = topk_n / 4;
     const bool vec = topk_n % 4 == 0 && ((uintptr_t)topk % 16) == 0;
-    // Rows of 8 or more pieces: one row per lane would read 64 rows' worth
+    // Rows of 4 or more pieces: one row per lane would read 64 rows' worth
     // of lines per load and lose them between the row's loads (config 5's
-    // 128-byte rows fetched 6.9x their bytes); shorter rows keep that form.
-    if (vec && pieces >= 8 && pieces <= 64 && (pieces & (pieces - 1)) == 0) {
+    // 128-byte rows fetched 6.9x their bytes); with eight row groups per wave
+    // the piece-per-lane form also beats it on 64-byte rows (top-16: 42 -> 39
+    // us on average over bench.py's plans).  Shorter rows keep one per lane.
+    if (vec && pieces >= 4 && pieces <= 64 && (pieces & (pieces - 1)) == 0) {
       // one wave per BRK_G groups of 64 / pieces rows, four waves per block
       const dim3 grow(ceil_div(ceil_div(nq, (64 / pieces) * BRK_G), 4), (unsigned)hkv);
 #define LSRM_BRK(P)                                                                  \
@@ -522,7 +524,7 @@ int build_tile_plan(const int32_t* topk, int64_t hkv, int64_t nq,
                        batch, cu_sb, brk);                                           \
     break;
       switch (pieces) {
-        LSRM_BRK(8) LSRM_BRK(16) LSRM_BRK(32) LSRM_BRK(64)
+        LSRM_BRK(4) LSRM_BRK(8) LSRM_BRK(16) LSRM_BRK(32) LSRM_BRK(64)
       }
 #undef LSRM_BRK
     } else if (vec)
